@@ -1,0 +1,144 @@
+"""Seeded synthetic shared-KV cases on the host (numpy).
+
+Shapes follow the workloads of the reference's tests (tests/support/
+serving_shapes.py, reference.py:326-354 make_case): BF16 Q ~ N(0,1); KV rows
+~ N(0,1) with 16 outlier channels scaled x8, rounded to BF16, encoded with a
+frozen per-channel scale max(1.1 * absmax / 127, 1e-8); block32 pages in a
+shuffled pool; sink = linspace(-2, 2, H).
+
+Only the pages a query can read are materialised; other logical pages map to
+physical page 0, which the path never reads for them.
+"""
+import math
+
+import numpy as np
+
+DIM = 512
+BLOCK = 32
+
+
+def bf16_bits(x):
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def bf16_value(bits):
+    return (np.asarray(bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def kv_rows(rng, rows, outlier_channels):
+    x = rng.standard_normal((rows, DIM), dtype=np.float32)
+    x[:, outlier_channels] *= 8
+    return bf16_bits(x)
+
+
+def frozen_scale(values, margin=1.1):
+    amax = np.abs(values).max(0).astype(np.float32)
+    return np.maximum(np.float32(margin) * amax / np.float32(127), np.float32(1e-8)).astype(np.float32)
+
+
+def encode(values, scale):
+    inverse = (1.0 / scale.astype(np.float64)).astype(np.float32)
+    return np.clip(np.rint(values * inverse), -127, 127).astype(np.int8)
+
+
+class Kind:
+    """One paged INT8 cache kind (original or compressed)."""
+
+    def __init__(self, name, needed, rng, page_stride, table_width, pool_factor=1.25):
+        self.name = name
+        batch = len(needed)
+        touched = [sorted(set(int(i) // BLOCK for i in rows)) for rows in needed]
+        total = sum(len(t) for t in touched)
+        pages = max(1, int(math.ceil(total * pool_factor)))
+        physical = rng.permutation(pages)
+        self.table = np.zeros((batch, max(1, table_width)), dtype=np.int32)
+        k = 0
+        for b, logical in enumerate(touched):
+            for lp in logical:
+                self.table[b, lp] = physical[k]
+                k += 1
+        self.pages = pages
+        self.page_stride = page_stride
+        outliers = rng.choice(DIM, 16, replace=False)
+        self.values_bits = kv_rows(rng, pages * BLOCK, outliers)          # BF16 source rows
+        values = bf16_value(self.values_bits)
+        self.scale = frozen_scale(values)
+        codes = encode(values, self.scale)
+        self.pool = np.zeros(pages * page_stride, dtype=np.int8)
+        view = self.pool.reshape(pages, page_stride)[:, :BLOCK * DIM]
+        view[:] = codes.reshape(pages, BLOCK * DIM)
+
+
+def make_case(seed, ratio, queries, lengths, topk=1024, heads=8, window=128,
+              page_stride=BLOCK * DIM, index_mode="uniform", softmax_scale=1 / math.sqrt(DIM)):
+    """Returns (oracle-style dict, metadata).  index_mode for C4:
+    'uniform'  top-k drawn without replacement from the visible range, sorted;
+    'holes'    as uniform with every 7th entry -1 and every 11th out of range;
+    'dups'     indices i // 2 (duplicates);
+    'mixed'    random with replacement plus -1 padding."""
+    rng = np.random.default_rng(seed)
+    batch = len(queries)
+    cu = np.zeros(batch + 1, dtype=np.int32)
+    cu[1:] = np.cumsum(queries)
+    tokens = int(cu[-1])
+    seq = np.asarray(lengths, dtype=np.int32)
+    q = bf16_bits(rng.standard_normal((tokens, heads, DIM), dtype=np.float32))
+    sink = np.linspace(-2, 2, heads, dtype=np.float32)
+
+    positions = []
+    for b in range(batch):
+        for t in range(cu[b], cu[b + 1]):
+            positions.append((b, t, int(seq[b]) - int(cu[b + 1]) + t))
+
+    ori_needed = [[] for _ in range(batch)]
+    for b, t, pos in positions:
+        ori_needed[b].extend(range(max(0, pos + 1 - window), pos + 1))
+    ori = Kind("ori", ori_needed, rng, page_stride, (int(seq.max()) + BLOCK - 1) // BLOCK)
+
+    out = dict(q=q, ori=ori, cu_q=cu, seq_lens=seq, sink=sink, ratio=ratio, window=window,
+               softmax_scale=softmax_scale, cmp=None, cmp_indices=None, topk=0)
+    if ratio != 1:
+        indices = None
+        cmp_needed = [[] for _ in range(batch)]
+        if ratio == 4:
+            indices = np.full((tokens, 1, topk), -1, dtype=np.int32)
+            for b, t, pos in positions:
+                count = (pos + 1) // 4
+                if index_mode == "uniform":
+                    ids = np.sort(rng.permutation(count)[:topk]) if count else np.zeros(0, np.int64)
+                elif index_mode == "holes":
+                    ids = np.sort(rng.permutation(count)[:topk]) if count else np.zeros(0, np.int64)
+                    ids = ids.astype(np.int64)
+                    ids[::7] = -1
+                    ids[3::11] = count + 5
+                elif index_mode == "dups":
+                    ids = np.arange(min(topk, count)) // 2
+                elif index_mode == "mixed":
+                    n = min(topk, max(1, count))
+                    ids = rng.integers(0, max(1, count), n) if count else np.full(n, -1)
+                    ids[rng.random(n) < 0.2] = -1
+                else:
+                    raise ValueError(index_mode)
+                indices[t, 0, :len(ids)] = ids
+                cmp_needed[b].extend(int(i) for i in ids if 0 <= i < count)
+        else:
+            for b, t, pos in positions:
+                cmp_needed[b].extend(range((pos + 1) // ratio))
+        width = (int(seq.max()) // ratio + BLOCK - 1) // BLOCK
+        cmp = Kind("cmp", cmp_needed, rng, page_stride, width)
+        out.update(cmp=cmp, cmp_indices=indices, topk=topk if ratio == 4 else 0)
+    return out
+
+
+def oracle_case(case):
+    """Adapter to oracle.Case."""
+    import oracle.oracle as ora   # the checker; tests only
+    cmp = case["cmp"]
+    return ora.Case(q=case["q"], ori=case["ori"].pool, ori_stride=case["ori"].page_stride,
+                    ori_table=case["ori"].table, cu_q=case["cu_q"], seq_lens=case["seq_lens"],
+                    sink=case["sink"], ori_scale=case["ori"].scale,
+                    cmp=cmp.pool if cmp else None, cmp_stride=cmp.page_stride if cmp else 0,
+                    cmp_table=cmp.table if cmp else None, cmp_scale=cmp.scale if cmp else None,
+                    cmp_indices=case["cmp_indices"], ratio=case["ratio"], window=case["window"],
+                    softmax_scale=case["softmax_scale"])
