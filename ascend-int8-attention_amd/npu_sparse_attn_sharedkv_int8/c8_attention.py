@@ -1,0 +1,134 @@
+"""C8 route: scratch sizing, KV-partition choice and launcher selection.
+
+Interface counterpart: npu_sparse_attn_sharedkv_int8/c8_attention.py:18-138 of
+the reference checkout (CORES, HEADS, MAX_SPLITS, enabled(), supported(),
+prepare()).  The Ascend build plans tiles on the device from live metadata
+for 24 cores; this build fixes the plan on the host instead, from the graph
+capacity alone, so the plan (and hence the numerics) is a pure function of
+(tokens, ratio, top-k, max_seq_len) that tests and the CPU checker recompute:
+
+  tile   128 keys; a query's list is the window rows, then its compressed rows,
+         cut into 128-key tiles numbered continuously across the two kinds
+  splits KV partitions; tile k is folded into partition k % splits and the
+         partitions are merged by log-sum-exp in the same launch
+
+A query row is one work-group per partition, so splits is raised until the
+launch has about TARGET_GROUPS work-groups (two per MI355X compute unit).
+"""
+import copy
+import ctypes
+import os
+
+import torch
+
+from .runtime import native_launcher, library
+
+CORES = 256                # MI355X compute units
+HEADS = 8
+DIM = 512
+TILE = 128                 # keys per tile; matches SHAREDKV_C8_TILE in the C ABI
+MAX_SPLITS = 16
+WINDOW = 128
+BLOCK = 32
+MAX_TOPK = 1024
+TARGET_GROUPS = 2 * CORES
+PARTIAL_FLOATS = 520       # per (token, partition, head): 512 numerator, max, denominator, pad
+
+VARIANT_SPARSE, VARIANT_DENSE, VARIANT_SPARSE_SMALL = 20, 21, 22
+
+
+def enabled():
+    """SHAREDKV_C8_DECODE: '1' (default) routes to this kernel; '0' asks for the
+    legacy kernels, which this build does not have."""
+    value = os.environ.get("SHAREDKV_C8_DECODE", "1")
+    if value not in ("0", "1"):
+        raise ValueError("SHAREDKV_C8_DECODE must be 0 or 1")
+    return value == "1"
+
+
+def max_tiles(ratio, topk, max_seq_len=None):
+    """Upper bound on a query's tile count (window tile + compressed tiles)."""
+    window_tiles = (WINDOW + TILE - 1) // TILE
+    if ratio == 4:
+        return window_tiles + (min(topk, MAX_TOPK) + TILE - 1) // TILE
+    if ratio == 128:
+        if max_seq_len is None:
+            return MAX_SPLITS
+        return window_tiles + (max(0, int(max_seq_len)) // 128 + TILE - 1) // TILE
+    return window_tiles
+
+
+def choose_splits(tokens, ratio, topk, max_seq_len=None):
+    """KV partitions for a launch of `tokens` query rows (host-side plan)."""
+    if tokens <= 0:
+        return 1
+    wanted = (TARGET_GROUPS + tokens - 1) // tokens
+    return max(1, min(wanted, max_tiles(ratio, topk, max_seq_len), MAX_SPLITS))
+
+
+def supported(entry):
+    """C8 ABI: 8 heads, ratio 1/4/128, window 128, block32 pages, no explicit
+    original slots, top-k <= 1024 (reference c8_attention.py:56-71 requires
+    top-k == 1024 and ratio 4/128; the HIP kernel is general over both)."""
+    if not getattr(entry, "blocks", 0) or getattr(entry, "args", None) is None:
+        return False
+    p = entry.args
+    return (p.heads == HEADS and p.tokens > 0 and p.batch > 0 and p.ratio in (1, 4, 128)
+            and p.window == WINDOW and p.oriBlock == BLOCK and (p.ratio == 1 or p.cmpBlock == BLOCK)
+            and not p.oriIndices and (p.ratio != 4 or 0 < p.topk <= MAX_TOPK)
+            and 1 <= p.splits <= MAX_SPLITS and p.oriStride % 16 == 0 and p.cmpStride % 16 == 0)
+
+
+def workspace_bytes(tokens, splits):
+    return int(library().sharedkv_c8_workspace_bytes(tokens, splits))
+
+
+def partial_shape(tokens, splits):
+    return (tokens, splits, HEADS, PARTIAL_FLOATS) if splits > 1 else (0,)
+
+
+def prepare(entry, *, scratch_allocator=None, shared_storage=False):
+    """Bind scratch and the launcher; returns a prepared copy of `entry`.
+
+    workspace: one uint32 merge ticket per query row.  It is zeroed here, and
+    every launch leaves it zero again, so a workspace must not be shared by
+    launches that can run concurrently (separate streams get separate
+    scratch through scratch_allocator's (name, stream) key).
+    partial: FP32 [tokens, splits, 8, 520] partition states (splits > 1).
+    """
+    if getattr(entry, "c8_dynamic", False) or not supported(entry):
+        return entry
+    p = entry.args
+    device = entry.case.q.device
+    allocate = scratch_allocator or (lambda name, shape, dtype, dev: torch.empty(shape, dtype=dtype, device=dev))
+    need_ws = workspace_bytes(p.tokens, p.splits)
+    shape = partial_shape(p.tokens, p.splits)
+    need_partial = 1
+    for extent in shape:
+        need_partial *= extent
+    workspace, partial = entry.workspace, entry.partial
+    if shared_storage:
+        if workspace is None or workspace.numel() < need_ws or (
+                p.splits > 1 and (partial is None or partial.numel() < need_partial)):
+            raise ValueError("C8 shared controls require the full workspace and partial extents")
+    else:
+        if workspace is None or workspace.numel() < need_ws:
+            workspace = allocate("workspace", (need_ws,), torch.uint8, device)
+        if p.splits > 1 and (partial is None or partial.numel() < need_partial):
+            partial = allocate("partial", shape, torch.float32, device)
+    workspace[:need_ws].zero_()
+
+    out = copy.copy(entry)
+    out.args = type(p).from_buffer_copy(p)
+    out.args.workspace = workspace.data_ptr()
+    out.args.partial = partial.data_ptr() if (partial is not None and p.splits > 1) else 0
+    out.workspace, out.partial = workspace, partial
+    out.blocks = p.tokens * p.splits
+    out.argument_address = ctypes.addressof(out.args)
+    small = p.ratio == 4 and p.tokens < 24
+    out.variant = VARIANT_SPARSE_SMALL if small else (VARIANT_SPARSE if p.ratio == 4 else VARIANT_DENSE)
+    out.native = native_launcher()
+    if out.native.attention_args_size != ctypes.sizeof(type(p)):
+        raise RuntimeError("C8 host/device argument ABI mismatch")
+    out.c8_dynamic = True
+    return out

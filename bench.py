@@ -1,0 +1,177 @@
+"""Benchmark: INT8 shared-KV decode queries/s and HBM GB/s on one MI355X.
+
+Workload (BASELINE.json metric "INT8 sharedKV decode queries/s + HBM GB/s (% of
+peak), B=32 C4 top-k1024"): B=32 sequences x T=2 query tokens (main + draft
+slot), H=8, D=512, BF16 Q; contexts ~U[2048, 65536]; every sequence on the C4
+launch: SWA128 window + top-k1024 compressed rows drawn from the visible range;
+INT8 block32 pages at the serving page stride (622592 B) in a pool sized 1.25x
+the need with shuffled block tables.  Synthetic data generated on the GPU.
+
+A step is one attention launch (one layer of one decode step).  Steps rotate
+over `--layers` layers whose pages interleave in the 622592-B page stride the
+way a serving pool holds every layer's 16 KiB page, so consecutive steps read
+different HBM (the union of bytes read per rotation exceeds the 256 MB MALL).
+The K timed steps are one captured HIP graph replay (serving runs decode in
+graphs); W warmup steps run eagerly before it and the graph is replayed once
+untimed.  Kernel time per launch = HIP-event time of the replay / K, on the
+replay stream.  The CPU baseline is the C restatement (oracle/, "port")
+timed on a bounded sample on this host, rank 0 only.
+
+Prints ONE JSON line on stdout; progress goes to stderr.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT, ROOT / "ascend-int8-attention_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+METRIC = "INT8 sharedKV decode queries/s + HBM GB/s (% of peak), B=32 C4 top-k1024"
+PEAK_HBM_GBS = 8000.0
+SERVING_STRIDE = 622592
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def workload(name, rng):
+    """(seed, ratio, queries, lengths, page stride, description) of a launch."""
+    if name == "headline":
+        lengths = rng.integers(2048, 65537, 32)
+        return (7, 4, [2] * 32, lengths, SERVING_STRIDE,
+                "headline: C4 top-k1024 decode, B=32 x T=2 (main + draft), ctx~U[2048,65536]")
+    if name == "c128":
+        lengths = rng.integers(2048, 65537, 32)
+        return (8, 128, [2] * 32, lengths, SERVING_STRIDE, "C128 decode, B=32 x T=2, ctx~U[2048,65536]")
+    if name == "c4_b64_long":
+        lengths = rng.integers(65536, 131073, 64)
+        return (4, 4, [1] * 64, lengths, SERVING_STRIDE, "config 4 C4 layer: B=64 x T=1, ctx~U[65536,131072]")
+    if name == "c128_b64_long":
+        lengths = rng.integers(65536, 131073, 64)
+        return (14, 128, [1] * 64, lengths, SERVING_STRIDE, "config 4 C128 layer: B=64 x T=1, ctx~U[65536,131072]")
+    raise SystemExit(f"unknown workload {name}")
+
+
+def cpu_baseline(dc, layers, splits, seconds):
+    """Time the C restatement on whole launches of the same workload until
+    about `seconds` of wall time have passed (bounded sample)."""
+    import oracle.oracle as ora
+    from tests import workloads
+    threads = max(1, min(16, os.cpu_count() or 1))
+    hosts = [workloads.oracle_case(dc.host(layer)) for layer in range(min(layers, 2))]
+    queries = 0
+    launches = 0
+    start = time.perf_counter()
+    while time.perf_counter() - start < seconds:
+        ora.tiled_attention(hosts[launches % len(hosts)], tile=128, splits=splits, return_lse=False,
+                            threads=threads)
+        queries += int(dc.meta["cu_q"][-1])
+        launches += 1
+    elapsed = time.perf_counter() - start
+    return dict(value=queries / elapsed, unit="queries/s", cores=threads, kind="port",
+                sample=f"{launches} whole launches of the bench workload ({queries} queries, "
+                       f"{min(layers, 2)} layers' data) through oracle/libsharedkv_oracle.so, "
+                       f"{threads} OpenMP threads, {elapsed:.1f} s")
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=160)
+    ap.add_argument("--warmup", type=int, default=32)
+    ap.add_argument("--layers", type=int, default=16, help="layers rotated over (<= 38 in the page stride)")
+    ap.add_argument("--workload", default="headline")
+    ap.add_argument("--splits", type=int, default=None, help="override the host plan's KV partitions")
+    ap.add_argument("--page-stride", type=int, default=None, help="override the workload's page stride (bytes)")
+    ap.add_argument("--merge-kernel", action="store_true", help="fold KV partitions in a second kernel")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
+              "the per-sequence sharding plan is described in DESIGN.md", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+    from npu_sparse_attn_sharedkv_int8 import PreparedAttention
+    from tests.device_cases import DeviceCase
+
+    torch.cuda.set_device(0)
+    if args.merge_kernel:
+        from npu_sparse_attn_sharedkv_int8.runtime import library
+        library().sharedkv_c8_set_merge_mode(1)
+    rng = np.random.default_rng(2026)
+    seed, ratio, queries, lengths, stride, description = workload(args.workload, rng)
+    stride = args.page_stride or stride
+    layers = max(1, min(args.layers, stride // 16384))
+    log(f"[bench] generating {description}; {layers} layers at page stride {stride}")
+    t0 = time.perf_counter()
+    dc = DeviceCase(seed, ratio, queries, lengths, page_stride=stride, layers=layers)
+    torch.cuda.synchronize()
+    log(f"[bench] generated in {time.perf_counter() - t0:.1f} s: ori pages {dc.ori.pages}, "
+        f"cmp pages {dc.cmp.pages if dc.cmp else 0}")
+    ops = [PreparedAttention(dc.cases[l], dc.ori_scales[l], dc.cmp_scales[l], splits=args.splits)
+           for l in range(layers)]
+    splits = ops[0].splits
+    live_queries = int(sum(queries))
+    bytes_per_launch = [dc.algorithmic_bytes(l) for l in range(layers)]
+
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        log(f"[bench] warmup {args.warmup} eager launches (splits={splits})")
+        for i in range(args.warmup):
+            ops[i % layers].run()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for i in range(args.steps):
+                ops[i % layers].run()
+        graph.replay()                      # untimed first replay (graph upload)
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        wall0 = time.perf_counter()
+        start.record(stream)
+        graph.replay()
+        end.record(stream)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - wall0
+    event_ms = start.elapsed_time(end)
+    ms_per_step = event_ms / args.steps
+    log(f"[bench] {args.steps} steps: {event_ms:.3f} ms by events, {wall * 1e3:.3f} ms wall")
+    mean_bytes = sum(bytes_per_launch[i % layers] for i in range(args.steps)) / args.steps
+    achieved = mean_bytes / (ms_per_step * 1e-3) / 1e9
+
+    traffic = None
+    traffic_file = ROOT / "profiles" / f"traffic_{args.workload}.json"
+    if traffic_file.exists():
+        traffic = json.loads(traffic_file.read_text()).get("bytes_per_launch")
+
+    record = {
+        "metric": METRIC, "value": live_queries / (ms_per_step * 1e-3), "unit": "queries/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_per_step, "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "i8", "data": "synthetic (GPU-generated, seeded)",
+        "config": {"workload": description, "batch": len(queries), "query_tokens": live_queries, "heads": 8,
+                   "dim": 512, "ratio": ratio, "topk": 1024 if ratio == 4 else 0, "window": 128,
+                   "page_stride": stride, "layers_rotated": layers, "tile": 128, "splits": splits,
+                   "lse": False, "timing": "one HIP graph replay of K launches, HIP events on its stream"},
+        "latency_us_per_layer": ms_per_step * 1e3,
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": achieved / PEAK_HBM_GBS, "traffic": traffic,
+                     "algorithmic_bytes_per_launch": mean_bytes},
+    }
+    if not args.no_cpu:
+        log(f"[bench] CPU baseline ({args.cpu_seconds:.0f} s sample)")
+        record["cpu_baseline"] = cpu_baseline(dc, layers, splits, args.cpu_seconds)
+    print(json.dumps(record), flush=True)
+
+
+if __name__ == "__main__":
+    main()

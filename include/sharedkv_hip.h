@@ -1,0 +1,107 @@
+/*
+ * C ABI of the MI355X (gfx950) shared-KV INT8 ("C8") attention and INT8 KV
+ * cache writer: libsharedkv_hip.so.
+ *
+ * Plain pointers and sizes only.  Pointer fields hold device addresses; the
+ * stream argument is a hipStream_t passed as void*.  Every entry point
+ * returns a hipError_t value (0 = success; hipErrorInvalidValue = 1 for a
+ * rejected argument block) and launches asynchronously on that stream.
+ *
+ * Reference interfaces replaced (paths relative to the reference checkout):
+ *   SharedKVArgs                      csrc/kernels/c8/args.h:7-14 (200 bytes, same order)
+ *   CacheWriteArgs                    csrc/kernels/cache_write.h:4-8 (same order)
+ *   launch_sharedkv_c8_sparse         csrc/kernels/c8/c4.cpp:70-71
+ *   launch_sharedkv_c8_dense          csrc/kernels/c8/c128.cpp:107-108
+ *   launch_sharedkv_c8_sparse_small   csrc/kernels/c8/c4_small.cpp:21-22
+ *   launch_cache_write                csrc/kernels/cache_write.cpp:79-88
+ * The reference launchers return void; these return the launch status.
+ */
+#pragma once
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Attention arguments (csrc/kernels/c8/args.h:7-14).  Strides are bytes
+ * between pages; tables address pages.  Fields this implementation reads:
+ *   q (BF16 [tokens][8][512]), ori/cmp (INT8 pages [*, 32, 1, 512]),
+ *   oriScale/cmpScale (FP32 [512]), oriTable/cmpTable (INT32 [batch][width]),
+ *   indices (INT32 [tokens][1][topk], C4), cuQ (INT32 [batch+1]),
+ *   seqLens (INT32 [batch]), sinks (FP32 [8]), out (BF16 [tokens][8][512]),
+ *   lse (FP32 [tokens][8] or 0), workspace (ticket words, see
+ *   sharedkv_c8_workspace_bytes, zero before first use), partial (FP32
+ *   split partials, see sharedkv_c8_partial_bytes), splits (KV partitions).
+ * oriIndices must be 0 (explicit original slots are not on this path). */
+typedef struct SharedKVArgs {
+    uint64_t q, ori, cmp, oriScale, cmpScale, oriTable, cmpTable, indices;
+    uint64_t cuQ, seqLens, sinks, out, workspace, lse;
+    uint64_t oriStride, cmpStride, partial, oriIndices;
+    uint32_t tokens, heads, batch, oriBlock, cmpBlock, oriTableWidth, cmpTableWidth;
+    uint32_t ratio, window, topk, splits, oriTopk, oriPages;
+    float softmaxScale;
+} SharedKVArgs;
+
+/* Cache-writer arguments (csrc/kernels/cache_write.h:4-8).  Strides are in
+ * elements: pageStride in INT8 elements, updateStride in BF16 elements,
+ * slotStride / slotColumnStride in slot elements. */
+typedef struct CacheWriteArgs {
+    uint64_t cache, updates, slots, inverseScale;
+    uint64_t pageStride, updateStride, slotStride, slotColumnStride;
+    uint32_t tokens, pages, pageSize, int64Slots, pairedSlots;
+} CacheWriteArgs;
+
+/* Keys per tile of the attention kernels.  Together with SharedKVArgs.splits
+ * it fixes the numerics: tile k of a query (kinds in order: original window,
+ * then compressed rows) is folded into partition k % splits. */
+#define SHAREDKV_C8_TILE 128
+
+/* Optional integer dumps for parity tests (all device pointers, may be 0).
+ * Layout per token t, positions P = 128 + cmpCapacity:
+ *   qcodes [t][2 kinds][16][512] INT8: rows 0-7 Q head codes, 8-15 residuals
+ *   alpha  [t][2][8] FP32
+ *   scores [t][P][16] INT32: QK S_hi heads 0-7, S_lo 8-15 per list position
+ *          (original window at 0.., compressed list at 128..)
+ *   probs  [t][P][16] INT8: p8 heads 0-7, p_low 8-15
+ *   values [t][tileCapacity][16][512] INT32: PV V_hi rows 0-7, V_lo 8-15 */
+typedef struct SharedKVDebug {
+    uint64_t qcodes, alpha, scores, probs, values;
+    uint32_t cmpCapacity, tileCapacity;
+} SharedKVDebug;
+
+/* C4 attention: SWA128 window plus top-k compressed rows (topk <= 1024).
+ * Replaces launch_sharedkv_c8_sparse (c4.cpp:70-71).  `blocks` is accepted
+ * for ABI compatibility; 0 launches nothing.  The grid is derived from
+ * args->tokens and args->splits. */
+int launch_sharedkv_c8_sparse(uint32_t blocks, void *stream, const SharedKVArgs *args);
+
+/* Small-capacity C4 entry (c4_small.cpp:21-22); same kernel family here. */
+int launch_sharedkv_c8_sparse_small(uint32_t blocks, void *stream, const SharedKVArgs *args);
+
+/* C128 attention: SWA128 window plus every compressed row (c128.cpp:107-108). */
+int launch_sharedkv_c8_dense(uint32_t blocks, void *stream, const SharedKVArgs *args);
+
+/* Same launch as the three above (ratio taken from args->ratio), with the
+ * integer dumps written to `debug`.  Test entry; slower. */
+int sharedkv_c8_attention_debug(void *stream, const SharedKVArgs *args, const SharedKVDebug *debug);
+
+/* Fused INT8 quantise + slot scatter (cache_write.cpp:79-88).  `blocks` is
+ * accepted for ABI compatibility; 0 launches nothing. */
+int launch_cache_write(uint32_t blocks, void *stream, const CacheWriteArgs *args);
+
+/* Scratch sizes in bytes for a launch with `tokens` query rows. */
+uint64_t sharedkv_c8_workspace_bytes(uint32_t tokens, uint32_t splits);
+uint64_t sharedkv_c8_partial_bytes(uint32_t tokens, uint32_t splits);
+
+/* 0 = fold split partials in the last work-group of each query (one launch),
+ * 1 = fold them in a second kernel.  Process-wide; default 0. */
+int sharedkv_c8_set_merge_mode(int mode);
+
+/* sizeof(SharedKVArgs), sizeof(CacheWriteArgs), library ABI version. */
+uint32_t sharedkv_attention_args_size(void);
+uint32_t sharedkv_cache_args_size(void);
+uint32_t sharedkv_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif

@@ -1,0 +1,292 @@
+"""GPU parity of the HIP attention kernels against the CPU checker.
+
+Bar: INT8 Q codes, int32 QK partials, P codes and int32 PV partials bit-exact
+(debug entry); BF16 outputs bit-exact with the checker run on the same plan
+(128-key tiles, the launch's KV partitions) and within max-abs 2e-2 /
+mean-abs 2e-3 of the reference's own reference.py vectors; LSE within 2e-6
+absolute of the checker (log is the device's own).
+"""
+import sys
+
+import numpy as np
+import pytest
+
+from tests import workloads
+from tests.device_cases import (query_subcase, run_hip, run_hip_debug, run_oracle, to_device, bits_of,
+                                default_cmp_capacity)
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def kinds_with_rows(case):
+    """[tokens, 2] mask: the window always has rows; the compressed kind has
+    rows when its (compacted or raw) list is non-empty."""
+    cu, lens = case["cu_q"], case["seq_lens"]
+    live = int(cu[-1])
+    used = np.zeros((live, 2), bool)
+    used[:, 0] = True
+    for b in range(len(lens)):
+        for t in range(cu[b], cu[b + 1]):
+            pos = int(lens[b]) - int(cu[b + 1]) + t
+            count = (pos + 1) // case["ratio"] if case["ratio"] != 1 else 0
+            if case["ratio"] == 4:
+                ix = case["cmp_indices"][t, 0]
+                used[t, 1] = bool(((ix >= 0) & (ix < count)).any()) if count < len(ix) else True
+            elif case["ratio"] == 128:
+                used[t, 1] = count > 0
+    return used
+
+
+def compare(case, out, lse, splits, rows=None, tag=""):
+    ref, ref_lse, _ = run_oracle(case if rows is None else query_subcase(case, rows), splits)
+    got = out if rows is None else out[rows]
+    got_lse = lse if rows is None else lse[rows]
+    live = ref.shape[0] if rows is not None else int(case["cu_q"][-1])
+    diff = got[:live] != ref[:live]
+    assert not diff.any(), f"{tag}: {int(diff.sum())} BF16 mismatches of {diff.size}"
+    np.testing.assert_allclose(got_lse[:live], ref_lse[:live], rtol=0, atol=2e-6, err_msg=tag)
+
+
+DEBUG_CASES = [
+    ("c128_ctx4096", 0, 128, [1], [4096], "uniform"),
+    ("c4_ctx16384", 1, 4, [1], [16384], "uniform"),
+    ("c4_holes", 2, 4, [2], [4200], "holes"),
+    ("c4_mixed_compact", 3, 4, [1, 2], [1500, 900], "mixed"),
+    ("c4_dups", 4, 4, [1], [4400], "dups"),
+    ("c128_mixed", 5, 128, [2, 1, 3], [100, 300, 1300], "uniform"),
+    ("r1_window", 6, 1, [2, 1], [90, 700], "uniform"),
+]
+
+
+@pytest.mark.parametrize("splits", [1, 3])
+@pytest.mark.parametrize("name,seed,ratio,queries,lengths,mode", DEBUG_CASES, ids=[c[0] for c in DEBUG_CASES])
+def test_integer_partials_bit_exact(name, seed, ratio, queries, lengths, mode, splits):
+    case = workloads.make_case(seed, ratio, queries, lengths, index_mode=mode)
+    say(f"[debug parity] {name} splits={splits}")
+    out, lse, dumps, op, (cap, tiles) = run_hip_debug(case, splits=splits)
+    ref, ref_lse, rd = run_oracle(case, splits, debug=True, cmp_capacity=cap, tile_capacity=tiles)
+    live = int(case["cu_q"][-1])
+    # The kernel encodes Q for a kind only when the kind has rows to read;
+    # compare Q codes of the kinds that do.
+    used = kinds_with_rows(case)
+    for key in ("qcodes", "alpha"):
+        np.testing.assert_array_equal(dumps[key][:live][used], rd[key][:live][used], err_msg=f"{name} {key}")
+    for key in ("scores", "probs", "values"):
+        np.testing.assert_array_equal(dumps[key][:live], rd[key][:live], err_msg=f"{name} {key}")
+    assert (out[:live] == ref[:live]).all(), name
+    np.testing.assert_allclose(lse[:live], ref_lse[:live], rtol=0, atol=2e-6)
+
+
+@pytest.mark.parametrize("name,seed,ratio,queries,lengths,mode", DEBUG_CASES, ids=[c[0] for c in DEBUG_CASES])
+def test_default_plan_matches_checker(name, seed, ratio, queries, lengths, mode):
+    """The production launch with its own KV-partition choice."""
+    case = workloads.make_case(seed, ratio, queries, lengths, index_mode=mode)
+    say(f"[parity] {name}")
+    out, lse, op = run_hip(case)
+    compare(case, out, lse, op.splits, tag=name)
+
+
+def _golden(name):
+    from pathlib import Path
+    return np.load(Path(__file__).resolve().parent / "golden" / "vectors" / f"{name}.npz")
+
+
+@pytest.mark.parametrize("name", ["c128_ctx4096", "c4_raw_holes", "c4_compact_mixed", "c128_mixed", "c4_dups"])
+def test_against_reference_vectors(name):
+    """HIP output vs reference.py's own tiled_quantized_reference output with a
+    128-key plan: BASELINE tolerance (max-abs 2e-2, mean-abs 2e-3) and, where
+    the plan matches ours, near bit-exactness."""
+    import torch
+    from npu_sparse_attn_sharedkv_int8 import PreparedAttention, SharedKVCase
+    z = _golden(name)
+    dev = "cuda"
+    pool = lambda key, stride: torch.from_numpy(z[key]).to(dev).as_strided(  # noqa: E731
+        (len(z[key]) // stride, 32, 1, 512), (stride, 512, 512, 1))
+    ratio = int(z["ratio"])
+    case = SharedKVCase(
+        q=torch.from_numpy(z["q"].view(np.int16)).to(dev).view(torch.bfloat16),
+        ori=pool("ori_pool", int(z["ori_stride"])), ori_block_table=torch.from_numpy(z["ori_table"]).to(dev),
+        cu_q=torch.from_numpy(z["cu_q"]).to(dev), seq_lens=torch.from_numpy(z["seq_lens"]).to(dev),
+        sink=torch.from_numpy(z["sink"]).to(dev), cmp=pool("cmp_pool", int(z["cmp_stride"])),
+        cmp_block_table=torch.from_numpy(z["cmp_table"]).to(dev),
+        cmp_indices=torch.from_numpy(z["cmp_indices"]).to(dev) if "cmp_indices" in z.files else None,
+        ratio=ratio, window=int(z["window"]), softmax_scale=float(z["softmax_scale"]))
+    plans = [tuple(int(v) for v in p) for p in z["plans"]]
+    for i, (tile, splits, jd, js, _) in enumerate(plans):
+        if tile != 128 or jd or js:
+            continue
+        say(f"[reference vectors] {name} plan {i} splits={splits}")
+        op = PreparedAttention(case, torch.from_numpy(z["ori_scale"]).to(dev),
+                               torch.from_numpy(z["cmp_scale"]).to(dev), splits=splits, return_lse=True)
+        op.run()
+        torch.cuda.synchronize()
+        got = bits_of(op.out)
+        live = int(z["cu_q"][-1])
+        a = got[:live].astype(np.uint32) << 16
+        b = z[f"out_{i}"][:live].astype(np.uint32) << 16
+        fa, fb = a.view(np.float32), b.view(np.float32)
+        assert np.abs(fa - fb).max() <= 2e-2 and np.abs(fa - fb).mean() <= 2e-3
+        assert (got[:live] == z[f"out_{i}"][:live]).mean() >= 0.999
+        np.testing.assert_allclose(op.lse.cpu().numpy()[:live], z[f"lse_{i}"][:live], rtol=0, atol=1e-5)
+
+
+# ------------------------------------------------------ BASELINE configs
+
+SERVING_STRIDE = 622592     # vLLM compact page stride (38 layers x 16 KiB)
+
+
+def config_specs(index):
+    """The BASELINE.json configs at full shape (caches generated on the GPU);
+    each entry is one launch: (seed, ratio, queries, lengths, page stride)."""
+    rng = np.random.default_rng(100 + (index if isinstance(index, int) else 99))
+    if index == 0:
+        return [(0, 128, [1], [4096], 16384)]
+    if index == 1:
+        return [(1, 4, [1], [16384], 16384)]
+    if index == 2:
+        lengths = rng.integers(2048, 65537, 32)
+        return [(2, 4, [2] * 16, lengths[:16], SERVING_STRIDE), (12, 128, [2] * 16, lengths[16:], SERVING_STRIDE)]
+    if index == 3:
+        return [(3, 4, [2048], [32768], 16384)]
+    if index == 4:
+        lengths = rng.integers(65536, 131073, 64)
+        return [(4, 4, [1] * 64, lengths, 20480), (14, 128, [1] * 64, lengths, 20480)]
+    if index == "headline":
+        lengths = rng.integers(2048, 65537, 32)
+        return [(7, 4, [2] * 32, lengths, SERVING_STRIDE)]
+    raise ValueError(index)
+
+
+@pytest.mark.parametrize("index", [0, 1, 2, 3, 4, "headline"])
+def test_baseline_configs(index):
+    """Full-size launches; every row is checked when the launch has <= 128
+    rows, else 96 rows spread over the launch (each recomputed alone by the
+    checker with an identical selection)."""
+    import torch
+    from npu_sparse_attn_sharedkv_int8 import PreparedAttention
+    from tests.device_cases import DeviceCase
+    for part, (seed, ratio, queries, lengths, stride) in enumerate(config_specs(index)):
+        tokens = int(sum(queries))
+        say(f"[config {index}.{part}] tokens={tokens} ratio={ratio} stride={stride}")
+        dc = DeviceCase(seed, ratio, queries, lengths, page_stride=stride)
+        op = PreparedAttention(dc.dev, dc.ori_scale, dc.cmp_scale, return_lse=True)
+        op.run()
+        torch.cuda.synchronize()
+        rows = None if tokens <= 128 else np.linspace(0, tokens - 1, 96).astype(int)
+        compare(dc.host(), bits_of(op.out), op.lse.cpu().numpy(), op.splits, rows=rows,
+                tag=f"config {index}.{part}")
+        del op, dc
+        torch.cuda.empty_cache()
+
+
+def test_padded_graph_rows_are_zero_and_guards_hold():
+    """Capacity rows past the live tokens (seq_len 0 / cu_q sentinel) are
+    zero-filled; bytes around the output and LSE are untouched."""
+    import torch
+    from npu_sparse_attn_sharedkv_int8 import PreparedAttention
+    case = workloads.make_case(21, 4, [2, 1, 0, 0], [3000, 700, 0, 0], index_mode="mixed")
+    live = int(case["cu_q"][-1])
+    # Capacity of 6 query rows: append 3 NaN-poisoned padding rows.
+    q = np.concatenate([case["q"], np.full((3, 8, 512), 0x7FC0, np.uint16)])
+    padded = dict(case, q=q, cmp_indices=np.concatenate([case["cmp_indices"],
+                                                        np.full((3, 1, 1024), -1, np.int32)]))
+    padded["cu_q"] = np.array([0, 2, 3, 6, 6], np.int32)      # graph pads a synthetic request
+    padded["seq_lens"] = np.array([3000, 700, 0, 0], np.int32)
+    dev, oscale, cscale, keep = to_device(padded)
+    guard_out = torch.full((6 + 2, 8, 512), 123, dtype=torch.bfloat16, device="cuda")
+    guard_lse = torch.full((6 + 2, 8), 123, dtype=torch.float32, device="cuda")
+    say("[padding] capacity 6, live 3")
+    op = PreparedAttention(dev, oscale, cscale, output=guard_out[1:-1], lse_output=guard_lse[1:-1])
+    op.run()
+    torch.cuda.synchronize()
+    assert (guard_out[[0, -1]].float().cpu() == 123).all() and (guard_lse[[0, -1]].cpu() == 123).all()
+    assert (op.out[live:].float().cpu() == 0).all() and (op.lse[live:].cpu() == 0).all()
+    compare(case, bits_of(op.out)[:live], op.lse.cpu().numpy()[:live], op.splits, tag="padding")
+
+
+def test_graph_replay_with_changing_live_metadata():
+    """One captured launch replayed while the device-side live metadata
+    changes; every replay equals an eager launch on the same inputs."""
+    import torch
+    from npu_sparse_attn_sharedkv_int8 import PreparedAttention
+    case = workloads.make_case(22, 4, [2, 2, 2], [5000, 2600, 9000], index_mode="uniform")
+    dev, oscale, cscale, keep = to_device(case)
+    op = PreparedAttention(dev, oscale, cscale, return_lse=True)
+    eager = PreparedAttention(dev, oscale, cscale, return_lse=True, splits=op.splits)
+    stream = torch.cuda.Stream()
+    say("[graph] capture")
+    with torch.cuda.stream(stream):
+        op.run()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            op.run()
+    variants = [(np.array([0, 2, 4, 6]), np.array([5000, 2600, 9000])),
+                (np.array([0, 2, 4, -1]), np.array([5000, 2600, 0])),
+                (np.array([0, 1, 2, 2]), np.array([4000, 2600, 0])),
+                (np.array([0, 2, 4, 6]), np.array([5000, 2600, 9000]))]
+    for i, (cu, lens) in enumerate(variants):
+        dev.cu_q.copy_(torch.from_numpy(cu.astype(np.int32)))
+        dev.seq_lens.copy_(torch.from_numpy(lens.astype(np.int32)))
+        op.out.fill_(7)
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        eager.run()
+        torch.cuda.synchronize()
+        say(f"[graph] replay {i}")
+        assert torch.equal(op.out, eager.out), i
+        assert torch.equal(op.lse, eager.lse), i
+
+
+def test_rebind_same_geometry():
+    import torch
+    from npu_sparse_attn_sharedkv_int8 import PreparedAttention
+    a = workloads.make_case(23, 128, [1, 2], [3000, 8000])
+    b = workloads.make_case(24, 128, [1, 2], [3100, 7000])
+    # Same geometry: scales stay bound across a rebind (as in the reference),
+    # so b is read with a's scales, and b's block tables take a's widths.
+    for kind in ("ori", "cmp"):
+        b[kind].scale = a[kind].scale
+        table = np.zeros_like(a[kind].table)
+        table[:, :b[kind].table.shape[1]] = b[kind].table
+        b[kind].table = table
+    dev_a, oa, ca, ka = to_device(a)
+    dev_b, ob, cb, kb = to_device(b)
+    op = PreparedAttention(dev_a, oa, ca, return_lse=True, splits=4)
+    op.run()
+    torch.cuda.synchronize()
+    first, first_lse = bits_of(op.out), op.lse.cpu().numpy()
+    out_b = torch.empty_like(dev_b.q)
+    lse_b = torch.empty((3, 8), dtype=torch.float32, device="cuda")
+    op._rebind_same_geometry(dev_b, output=out_b, lse_output=lse_b)
+    say("[rebind]")
+    op.run()
+    torch.cuda.synchronize()
+    compare(a, first, first_lse, 4, tag="rebind-a")
+    compare(b, bits_of(out_b), lse_b.cpu().numpy(), 4, tag="rebind-b")
+
+
+def test_splits_variants_match_checker():
+    case = workloads.make_case(25, 4, [2, 1], [20000, 700], index_mode="holes")
+    for splits in (1, 2, 5, 9, 16):
+        say(f"[splits] {splits}")
+        out, lse, op = run_hip(case, splits=splits)
+        compare(case, out, lse, splits, tag=f"splits {splits}")
+
+
+def test_empty_launch_is_a_no_op():
+    import torch
+    from npu_sparse_attn_sharedkv_int8 import PreparedAttention
+    case = workloads.make_case(26, 4, [1], [600])
+    dev, oscale, cscale, keep = to_device(case)
+    dev.q = dev.q[:0]
+    dev.cmp_indices = dev.cmp_indices[:0]
+    op = PreparedAttention(dev, oscale, cscale)
+    assert op.blocks == 0
+    assert op.run().shape == (0, 8, 512)
+    torch.cuda.synchronize()

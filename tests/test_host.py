@@ -1,0 +1,177 @@
+"""Host-side logic and the C ABI, without a GPU.
+
+- libsharedkv_hip.so loads and exports every function include/sharedkv_hip.h
+  declares; the argument blocks have the reference's sizes and field offsets
+  (SharedKVArgs 200 bytes, csrc/kernels/c8/args.h:7-14 of the reference).
+- The Python boundary rejects contract violations with ValueError before any
+  device work (attention.py:31-83, cache.py:25-41 of the reference).
+- The host plan (tile 128, KV partitions) is the documented pure function.
+"""
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from npu_sparse_attn_sharedkv_int8 import (CacheQuantization, PreparedAttention, PreparedCacheWrite,
+                                           SharedKVCase)
+from npu_sparse_attn_sharedkv_int8 import c8_attention, runtime
+from npu_sparse_attn_sharedkv_int8._paths import native_path
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "sharedkv_hip.h"
+
+
+def declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:int|uint32_t|uint64_t|void)\s+\**\s*(\w+)\s*\(", text, flags=re.M)))
+
+
+def test_library_exports_every_declared_function():
+    lib = ctypes.CDLL(str(native_path()))
+    names = declared_functions()
+    assert "launch_sharedkv_c8_sparse" in names and "launch_cache_write" in names
+    for name in names:
+        assert hasattr(lib, name), name
+    assert set(runtime.EXPORTS) <= set(names)
+
+
+def test_argument_blocks_match_reference_layout():
+    lib = runtime.library()
+    assert lib.sharedkv_attention_args_size() == 200 == ctypes.sizeof(runtime.SharedKVArgs)
+    assert lib.sharedkv_cache_args_size() == ctypes.sizeof(runtime.CacheWriteArgs) == 88
+    a = runtime.SharedKVArgs
+    assert a.q.offset == 0 and a.oriIndices.offset == 136 and a.tokens.offset == 144
+    assert a.oriPages.offset == 192 and a.softmaxScale.offset == 196
+    c = runtime.CacheWriteArgs
+    assert c.slotColumnStride.offset == 56 and c.tokens.offset == 64 and c.pairedSlots.offset == 80
+
+
+def test_scratch_sizes():
+    lib = runtime.library()
+    assert lib.sharedkv_c8_partial_bytes(64, 1) == 0
+    assert lib.sharedkv_c8_partial_bytes(64, 8) == 64 * 8 * 8 * 520 * 4
+    assert lib.sharedkv_c8_workspace_bytes(64, 8) >= 64 * 4
+    assert lib.sharedkv_c8_workspace_bytes(1, 1) % 256 == 0
+
+
+def test_launchers_reject_bad_blocks_without_a_device():
+    """Argument checks run before any HIP call, so they are testable here."""
+    lib = runtime.library()
+    args = runtime.SharedKVArgs()
+    assert lib.launch_sharedkv_c8_sparse(0, None, ctypes.byref(args)) == 0   # 0 blocks: no launch
+    assert lib.launch_sharedkv_c8_sparse(1, None, ctypes.byref(args)) == 1   # ratio 0 rejected
+    args.ratio = 128
+    assert lib.launch_sharedkv_c8_dense(1, None, ctypes.byref(args)) == 1    # null pointers rejected
+    cw = runtime.CacheWriteArgs()
+    assert lib.launch_cache_write(1, None, ctypes.byref(cw)) == 1
+    assert lib.sharedkv_c8_set_merge_mode(2) == 1
+    assert lib.sharedkv_c8_set_merge_mode(0) == 0
+
+
+def test_host_plan():
+    assert c8_attention.max_tiles(4, 1024) == 9
+    assert c8_attention.max_tiles(128, 0, 4096) == 2
+    assert c8_attention.max_tiles(1, 0) == 1
+    assert c8_attention.choose_splits(64, 4, 1024) == 8
+    assert c8_attention.choose_splits(1, 4, 1024) == 9
+    assert c8_attention.choose_splits(4096, 4, 1024) == 1
+    assert c8_attention.choose_splits(1, 128, 0, 4096) == 2
+    assert c8_attention.choose_splits(2, 128, 0) == c8_attention.MAX_SPLITS
+
+
+def test_c8_switch():
+    import os
+    old = os.environ.get("SHAREDKV_C8_DECODE")
+    try:
+        os.environ["SHAREDKV_C8_DECODE"] = "2"
+        with pytest.raises(ValueError):
+            c8_attention.enabled()
+        os.environ["SHAREDKV_C8_DECODE"] = "1"
+        assert c8_attention.enabled()
+    finally:
+        if old is None:
+            os.environ.pop("SHAREDKV_C8_DECODE", None)
+        else:
+            os.environ["SHAREDKV_C8_DECODE"] = old
+
+
+def cpu_case(**over):
+    t, h = 2, 8
+    q = torch.zeros((t, h, 512), dtype=torch.bfloat16)
+    cache = torch.zeros((4, 32, 1, 512), dtype=torch.int8)
+    fields = dict(q=q, ori=cache, ori_block_table=torch.zeros((1, 4), dtype=torch.int32),
+                  cu_q=torch.tensor([0, 2], dtype=torch.int32), seq_lens=torch.tensor([40], dtype=torch.int32),
+                  sink=torch.zeros(h), cmp=cache, cmp_block_table=torch.zeros((1, 4), dtype=torch.int32),
+                  cmp_indices=torch.zeros((t, 1, 1024), dtype=torch.int32), ratio=4)
+    fields.update(over)
+    return SharedKVCase(**fields)
+
+
+def test_attention_validation_errors():
+    scale = torch.ones(512)
+    with pytest.raises(ValueError, match="GPU"):
+        PreparedAttention(cpu_case(), scale, scale)          # host tensors
+    with pytest.raises(ValueError, match="implementation"):
+        PreparedAttention(cpu_case(), scale, scale, implementation="npu")
+
+
+def test_cache_write_validation_errors():
+    cache = torch.zeros((4, 32, 1, 512), dtype=torch.int8)
+    with pytest.raises(ValueError, match="GPU"):
+        PreparedCacheWrite(cache, torch.zeros((2, 512), dtype=torch.bfloat16), torch.zeros(2, dtype=torch.int32),
+                           torch.ones(512))
+
+
+@pytest.mark.parametrize("bad", [0.0, -1.0, float("nan"), float("inf")])
+def test_reject_invalid_frozen_scales(bad):
+    """tests/unit/test_reference.py:15-20 of the reference."""
+    scale = torch.ones(512)
+    scale[17] = bad
+    with pytest.raises(ValueError):
+        CacheQuantization(scale)
+
+
+def test_quantization_kat_and_append_invariance():
+    """tests/unit/test_reference.py:22-40 of the reference."""
+    quant = CacheQuantization(torch.ones(512))
+    row = torch.zeros(1, 512)
+    row[0, :8] = torch.tensor([-200.0, -127.0, -1.5, -0.5, 0.5, 1.5, 127.0, 200.0])
+    assert quant.quantize(row)[0, :8].tolist() == [-127, -127, -2, 0, 0, 2, 127, 127]
+    assert quant.quantize(row).dtype == torch.int8
+    cal = CacheQuantization.calibrate([torch.ones(3, 512)])
+    scale, inverse = cal.scale.clone(), cal.inverse_scale.clone()
+    prefix = torch.linspace(-1, 1, 512).reshape(1, 512)
+    before = cal.quantize(prefix)
+    cal.quantize(torch.full((2, 512), 1000.0))
+    assert torch.equal(cal.scale, scale) and torch.equal(cal.inverse_scale, inverse)
+    assert torch.equal(cal.quantize(prefix), before)
+
+
+def test_msmodelslim_requires_zero_offsets():
+    """tests/unit/test_reference.py:42-48 of the reference."""
+    tensors = {"layer.kv_cache_scale": torch.ones(512), "layer.kv_cache_offset": torch.zeros(512)}
+    assert torch.equal(CacheQuantization.from_msmodelslim(tensors, "layer").scale, torch.ones(512))
+    tensors["layer.kv_cache_offset"][0] = 1
+    with pytest.raises(ValueError, match="nonzero offsets"):
+        CacheQuantization.from_msmodelslim(tensors, "layer")
+
+
+def test_contract_encoding_matches_checker():
+    """The host encoding helper equals the checker's restatement on random rows."""
+    import oracle.oracle as ora
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((64, 512)).astype(np.float32) * 4
+    scale = np.abs(rng.standard_normal(512)).astype(np.float32) * 0.03 + 1e-3
+    quant = CacheQuantization(torch.from_numpy(scale))
+    np.testing.assert_array_equal(quant.inverse_scale.numpy(), ora.inverse_scale(scale))
+    np.testing.assert_array_equal(quant.quantize(torch.from_numpy(x)).numpy(),
+                                  ora.quantize(x, ora.inverse_scale(scale)))
+
+
+def test_case_to_moves_every_tensor():
+    case = cpu_case()
+    moved = case.to("cpu")
+    assert moved is not case and moved.ratio == 4 and torch.equal(moved.q, case.q)

@@ -1,0 +1,298 @@
+"""Pins the CPU checker (oracle/) before any GPU result is compared with it.
+
+Sources of truth, in order:
+  1. vectors written by the reference's own reference.py (tests/golden/):
+     tiled_quantized_reference, joint_quantized_row, sharedkv_reference (FP64)
+     and CacheQuantization, on seeded cases and several tiling plans;
+  2. the reference's known-answer tests (tests/unit/test_reference.py of the
+     reference checkout): rounding/clipping, shared sink denominator,
+     padding indices, integer oracle vs FP64 attention;
+  3. what the mathematics fixes: exact integer dot products recomputed by
+     brute force from the dumped codes and the gathered rows, the residual
+     reconstruction bounds of the Q and P splits, the pairwise-sum tree,
+     and exp against float64.
+"""
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import oracle.oracle as ora
+from tests import workloads
+from tests.device_cases import query_subcase
+
+GOLDEN = Path(__file__).resolve().parent / "golden" / "vectors"
+CASES = sorted(p.stem for p in GOLDEN.glob("c*.npz"))
+
+
+def golden_case(z):
+    has = lambda k: k in z.files  # noqa: E731
+    return ora.Case(q=z["q"], ori=z["ori_pool"], ori_stride=int(z["ori_stride"]), ori_table=z["ori_table"],
+                    cu_q=z["cu_q"], seq_lens=z["seq_lens"], sink=z["sink"], ori_scale=z["ori_scale"],
+                    cmp=z["cmp_pool"] if has("cmp_pool") else None,
+                    cmp_stride=int(z["cmp_stride"]) if has("cmp_stride") else 0,
+                    cmp_table=z["cmp_table"] if has("cmp_table") else None,
+                    cmp_scale=z["cmp_scale"] if has("cmp_scale") else None,
+                    cmp_indices=z["cmp_indices"] if has("cmp_indices") else None,
+                    ratio=int(z["ratio"]), window=int(z["window"]), softmax_scale=float(z["softmax_scale"]))
+
+
+def bf16_ulps(a_bits, b_bits):
+    a = a_bits.astype(np.int32)
+    b = b_bits.astype(np.int32)
+    # Same sign region: the bit patterns are ordered like the values.
+    return np.abs(a - b)
+
+
+# ------------------------------------------------------------ golden vectors
+
+@pytest.mark.parametrize("name", CASES)
+def test_tiled_attention_matches_reference_vectors(name):
+    """reference.py:210-323 outputs: bit-exact except rare 1-ulp BF16 flips
+    from exp/summation ulps (torch.exp is not correctly rounded)."""
+    z = np.load(GOLDEN / f"{name}.npz")
+    case = golden_case(z)
+    for i, (tile, splits, jd, js, limit) in enumerate(z["plans"]):
+        out, lse, _ = ora.tiled_attention(case, int(tile), int(splits), joint_dense=bool(jd),
+                                          joint_sparse=bool(js), joint_tile_limit=int(limit))
+        ref, ref_lse = z[f"out_{i}"], z[f"lse_{i}"]
+        live = int(z["cu_q"][-1])
+        ulps = bf16_ulps(out[:live], ref[:live])
+        assert ulps.max() <= 1, (name, i)
+        assert (ulps == 0).mean() >= 0.999, (name, i)
+        np.testing.assert_allclose(lse[:live], ref_lse[:live], rtol=0, atol=2e-6)
+
+
+def test_joint_row_matches_reference_vectors():
+    z = np.load(GOLDEN / "joint_rows.npz")
+    for tag, bias in (("plain", None), ("bias", z["bias"])):
+        out, lse = ora.joint_row(z["q"], [z["rows0"], z["rows1"]], [z["scale0"], z["scale1"]], z["sink"],
+                                 1 / math.sqrt(512), bias=bias)
+        assert bf16_ulps(out, z[f"out_{tag}"]).max() <= 1
+        assert (out == z[f"out_{tag}"]).mean() >= 0.999
+        np.testing.assert_allclose(lse, z[f"lse_{tag}"], rtol=0, atol=2e-6)
+
+
+@pytest.mark.parametrize("name", CASES)
+def test_encoding_matches_reference_vectors(name):
+    """CacheQuantization.inverse_scale and quantize (reference.py:47-53)."""
+    z = np.load(GOLDEN / f"{name}.npz")
+    np.testing.assert_array_equal(ora.inverse_scale(z["ori_scale"]), z["ori_inverse"])
+    if "cmp_scale" in z.files:
+        np.testing.assert_array_equal(ora.inverse_scale(z["cmp_scale"]), z["cmp_inverse"])
+    values = ora.bf16_to_f32(z["quant_source_bits"])
+    np.testing.assert_array_equal(ora.quantize(values, z["ori_inverse"]), z["quant_codes"])
+
+
+@pytest.mark.parametrize("name", CASES)
+def test_fp64_attention_matches_reference_vectors(name):
+    """sharedkv_reference (reference.py:129-139) over decoded INT8 rows."""
+    z = np.load(GOLDEN / f"{name}.npz")
+    out, lse = ora.fp64_attention(golden_case(z))
+    live = int(z["cu_q"][-1])
+    np.testing.assert_allclose(out[:live], z["fp64_out"][:live], rtol=1e-6, atol=1e-6)
+    np.testing.assert_allclose(lse[:live], z["fp64_lse"][:live], rtol=1e-6, atol=1e-6)
+
+
+# ------------------------------------------------- reference known answers
+
+def test_rounding_and_clipping_kat():
+    """tests/unit/test_reference.py:22-28: half-even rounding, clamp at 127."""
+    row = np.zeros((1, 512), np.float32)
+    row[0, :8] = [-200.0, -127.0, -1.5, -0.5, 0.5, 1.5, 127.0, 200.0]
+    codes = ora.quantize(row, ora.inverse_scale(np.ones(512, np.float32)))
+    assert codes[0, :8].tolist() == [-127, -127, -2, 0, 0, 2, 127, 127]
+
+
+def test_sink_shares_the_denominator_kat():
+    """tests/unit/test_reference.py:50-58: q = 0, rows of 10 and 20, sink 0
+    -> three equal weights, output exactly 10 (sink has no value), lse log 3."""
+    q = np.zeros((2, 512), np.uint16)
+    rows = [np.full((1, 512), 10, np.int8), np.full((1, 512), 20, np.int8)]
+    ones = np.ones(512, np.float32)
+    out, lse = ora.joint_row(q, rows, [ones, ones], np.zeros(2, np.float32), 1.0)
+    assert np.all(ora.bf16_to_f32(out) == 10.0)
+    np.testing.assert_allclose(lse, math.log(3), rtol=1e-6, atol=1e-6)
+
+
+def test_padding_indices_do_not_contribute_kat():
+    """tests/unit/test_reference.py:74-82: -1 and huge indices select nothing."""
+    case = workloads.make_case(9, 4, [1], [257], index_mode="uniform")
+    base = workloads.oracle_case(case)
+    out_a, lse_a = ora.fp64_attention(base)
+    padded = dict(case)
+    ix = case["cmp_indices"].copy()
+    ix[ix < 0] = 2 ** 30
+    padded["cmp_indices"] = ix
+    out_b, lse_b = ora.fp64_attention(workloads.oracle_case(padded))
+    np.testing.assert_array_equal(out_a, out_b)
+    np.testing.assert_array_equal(lse_a, lse_b)
+    # The integer path agrees bit for bit too.
+    a, la, _ = ora.tiled_attention(base)
+    b, lb, _ = ora.tiled_attention(workloads.oracle_case(padded))
+    np.testing.assert_array_equal(a, b)
+    np.testing.assert_array_equal(la, lb)
+
+
+@pytest.mark.parametrize("ratio", [1, 4, 128])
+def test_integer_oracle_close_to_fp64_attention(ratio):
+    """tests/unit/test_reference.py:60-72: rel-L2 < 0.01, LSE within 2e-4."""
+    case = workloads.make_case(23, ratio, [2, 1], [129, 257])
+    c = workloads.oracle_case(case)
+    out, lse, _ = ora.tiled_attention(c)
+    ref, ref_lse = ora.fp64_attention(c)
+    got = ora.bf16_to_f32(out).astype(np.float64)
+    assert np.linalg.norm(got - ref) / np.linalg.norm(ref) < 0.01
+    np.testing.assert_allclose(lse, ref_lse, rtol=2e-4, atol=2e-4)
+
+
+# ---------------------------------------------------- mathematical pins
+
+def test_expf_against_float64():
+    x = np.concatenate([np.linspace(-87, 0, 200001, dtype=np.float32),
+                        np.float32([-1e-30, -0.5, -1.0, -86.9])])
+    got = ora.expf(x).astype(np.float64)
+    want = np.exp(x.astype(np.float64))
+    ulp = np.spacing(want.astype(np.float32)).astype(np.float64)
+    assert np.max(np.abs(got - want) / ulp) <= 1.5
+    assert ora.expf(np.float32([0.0]))[0] == 1.0
+    assert ora.expf(np.float32([-88.0, -1e30]))[0] == 0.0
+
+
+def test_tree_sum_is_pairwise():
+    import ctypes
+    rng = np.random.default_rng(1)
+    for count in (1, 5, 64, 100, 128):
+        x = rng.random(count, dtype=np.float32)
+        padded = 1 << (count - 1).bit_length()
+        v = np.zeros(padded, np.float32)
+        v[:count] = x
+        while len(v) > 1:
+            v = (v[0::2] + v[1::2]).astype(np.float32)
+        got = ora.lib().sko_tree_sum(ctypes.c_void_p(x.ctypes.data), count, padded)
+        assert np.float32(got) == v[0]
+
+
+def _pin_case(seed, ratio, mode="uniform"):
+    lengths = {4: [600, 5000], 128: [300, 9000], 1: [90, 700]}[ratio]
+    return workloads.make_case(seed, ratio, [2, 1], lengths, index_mode=mode)
+
+
+def _selection(case):
+    """Brute-force reference.py:93-126 selection (+ compaction 250-252):
+    per token, the list of (kind, logical row or None) in tile order."""
+    cu, lens = case["cu_q"], case["seq_lens"]
+    lists = []
+    for b in range(len(lens)):
+        for t in range(cu[b], cu[b + 1]):
+            pos = int(lens[b]) - int(cu[b + 1]) + t
+            ori = list(range(max(0, pos - 127), pos + 1))
+            cmp = []
+            if case["ratio"] != 1:
+                count = (pos + 1) // case["ratio"]
+                if case["ratio"] == 4:
+                    raw = [int(i) for i in case["cmp_indices"][t, 0]]
+                    if count < len(raw) <= 1024:
+                        cmp = [i for i in raw if 0 <= i < count]
+                    else:
+                        cmp = [i if 0 <= i < count else None for i in raw]
+                else:
+                    cmp = list(range(count))
+            lists.append((b, ori, cmp))
+    return lists
+
+
+@pytest.mark.parametrize("ratio,mode", [(4, "uniform"), (4, "holes"), (4, "dups"), (4, "mixed"), (128, None),
+                                        (1, None)])
+def test_integer_partials_by_brute_force(ratio, mode):
+    """QK and PV int32 partials equal exact integer dot products of the dumped
+    codes with the rows the selection rule picks; the Q and P splits
+    reconstruct their inputs within the rounding bounds."""
+    case = _pin_case(31, ratio, mode or "uniform")
+    c = workloads.oracle_case(case)
+    out, lse, dbg = ora.tiled_attention(c, tile=128, splits=2, debug=True)
+    for t, (b, ori, cmp) in enumerate(_selection(case)):
+        for kind, rows, kd in ((0, ori, case["ori"]), (1, cmp, case["cmp"])):
+            if kd is None:
+                continue
+            qc = dbg["qcodes"][t, kind].astype(np.int64)
+            alpha = dbg["alpha"][t, kind]
+            # Q split: |q8| peaks at 127 per head and q8 + qlo/127 matches q*scale/alpha.
+            folded = ora.bf16_to_f32(case["q"][t]).astype(np.float64) * kd.scale.astype(np.float64)
+            assert np.all(np.abs(qc[:8]).max(1) == 127)
+            recon = qc[:8] + qc[8:] / 127.0
+            assert np.max(np.abs(recon - folded / alpha[:, None])) <= 0.5 / 127 + 1e-4
+            for j, idx in enumerate(rows):
+                base = 0 if kind == 0 else 128
+                s = dbg["scores"][t, base + j]
+                if idx is None:
+                    continue
+                row = ora.gather_rows(kd.pool, kd.page_stride, kd.table, b, [idx])[0].astype(np.int64)
+                np.testing.assert_array_equal(s[:8], qc[:8] @ row)
+                np.testing.assert_array_equal(s[8:], qc[8:] @ row)
+        # PV: per tile, the dumped P codes times the tile's rows.
+        tiles = []
+        for kind, rows, kd in ((0, ori, case["ori"]), (1, cmp, case["cmp"])):
+            for start in range(0, len(rows), 128):
+                tiles.append((kind, rows[start:start + 128], start, kd))
+        for number, (kind, rows, start, kd) in enumerate(tiles):
+            if number >= dbg["values"].shape[1]:
+                break
+            base = (0 if kind == 0 else 128) + start
+            p = dbg["probs"][t, base:base + len(rows)].astype(np.int64)   # [n, 16]
+            assert p[:, :8].min() >= 0 and p[:, :8].max() <= 127
+            kv = np.zeros((len(rows), 512), np.int64)
+            for j, idx in enumerate(rows):
+                if idx is not None:
+                    kv[j] = ora.gather_rows(kd.pool, kd.page_stride, kd.table, b, [idx])[0]
+            np.testing.assert_array_equal(dbg["values"][t, number], p.T @ kv)
+
+
+def test_subcase_rows_reproduce_full_case_rows():
+    """query_subcase (used to check large GPU launches on a row sample) keeps
+    each row's selection, so the checker gives identical bits."""
+    case = workloads.make_case(5, 4, [2, 3], [3000, 1200], index_mode="mixed")
+    full, full_lse, _ = ora.tiled_attention(workloads.oracle_case(case), splits=3)
+    rows = [0, 2, 4]
+    sub = query_subcase(case, rows)
+    part, part_lse, _ = ora.tiled_attention(workloads.oracle_case(sub), splits=3)
+    np.testing.assert_array_equal(part, full[rows])
+    np.testing.assert_array_equal(part_lse, full_lse[rows])
+
+
+# ------------------------------------------------------------- cache writer
+
+@pytest.mark.parametrize("int64,paired", [(False, False), (True, False), (False, True), (True, True)])
+def test_cache_writer_oracle(int64, paired):
+    """cache.py:16-69 + cache_write.cpp:38-73: codes of each valid row land at
+    page*stride + offset*512; negative/out-of-range destinations are skipped;
+    every other byte keeps its value."""
+    rng = np.random.default_rng(7)
+    pages, size, stride, rows = 6, 32, 32 * 512 + 4096, 40
+    pool = np.full(pages * stride, 73, np.int8)
+    upd = workloads.bf16_bits(rng.standard_normal((rows, 512), dtype=np.float32) * 3)
+    scale = workloads.frozen_scale(workloads.bf16_value(upd))
+    inv = ora.inverse_scale(scale)
+    flat = rng.permutation(pages * size)[:rows].astype(np.int64)
+    flat[3], flat[9] = -1, pages * size + 7
+    if paired:
+        slots = np.stack([flat // size, flat % size], 1)
+        slots[9] = [pages, 0]
+        slots[11] = [2, size]      # offset past the page
+        slots[12] = [-5, 3]
+    else:
+        slots = flat
+    slots = slots.astype(np.int64 if int64 else np.int32)
+    written = ora.cache_write(pool, stride, pages, size, upd, slots, inv, paired=paired)
+    expect = np.full_like(pool, 73)
+    codes = workloads.encode(workloads.bf16_value(upd), scale)
+    count = 0
+    for r in range(rows):
+        page, off = (int(slots[r, 0]), int(slots[r, 1])) if paired else (int(flat[r]) // size, int(flat[r]) % size)
+        if (slots[r, 0] if paired else flat[r]) < 0 or page >= pages or not 0 <= off < size:
+            continue
+        expect[page * stride + off * 512: page * stride + off * 512 + 512] = codes[r]
+        count += 1
+    assert written == count
+    np.testing.assert_array_equal(pool, expect)
