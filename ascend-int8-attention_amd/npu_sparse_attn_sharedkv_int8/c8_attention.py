@@ -13,7 +13,10 @@ capacity alone, so the plan (and hence the numerics) is a pure function of
          partitions are merged by log-sum-exp in the same launch
 
 A query row is one work-group per partition, so splits is raised until the
-launch has about TARGET_GROUPS work-groups (two per MI355X compute unit).
+launch has about TARGET_GROUPS work-groups (one per MI355X compute unit;
+measured on the B=32 x T=2 C4 decode: 4 partitions of ~2-3 tiles beat 8
+partitions of ~1 tile, whose fixed per-work-group latency and merge traffic
+dominate).
 """
 import copy
 import ctypes
@@ -31,7 +34,7 @@ MAX_SPLITS = 16
 WINDOW = 128
 BLOCK = 32
 MAX_TOPK = 1024
-TARGET_GROUPS = 2 * CORES
+TARGET_GROUPS = CORES
 PARTIAL_FLOATS = 520       # per (token, partition, head): 512 numerator, max, denominator, pad
 
 VARIANT_SPARSE, VARIANT_DENSE, VARIANT_SPARSE_SMALL = 20, 21, 22
@@ -90,10 +93,11 @@ def partial_shape(tokens, splits):
 def prepare(entry, *, scratch_allocator=None, shared_storage=False):
     """Bind scratch and the launcher; returns a prepared copy of `entry`.
 
-    workspace: one uint32 merge ticket per query row.  It is zeroed here, and
-    every launch leaves it zero again, so a workspace must not be shared by
-    launches that can run concurrently (separate streams get separate
-    scratch through scratch_allocator's (name, stream) key).
+    workspace: one uint32 merge ticket per query row (the last partition of a
+    row to finish folds the row).  It is zeroed here, and every launch leaves
+    it zero again, so a workspace must not be shared by launches that can run
+    concurrently (separate streams get separate scratch through
+    scratch_allocator's (name, stream) key).
     partial: FP32 [tokens, splits, 8, 520] partition states (splits > 1).
     """
     if getattr(entry, "c8_dynamic", False) or not supported(entry):

@@ -50,7 +50,15 @@ EXPORTS = ("launch_sharedkv_c8_sparse", "launch_sharedkv_c8_dense", "launch_shar
 
 @lru_cache(maxsize=1)
 def library():
-    """Load the C-ABI library and declare every exported signature."""
+    """Load the C-ABI library and declare every exported signature.
+
+    torch is imported first so that its HIP runtime (libamdhip64.so.7, loaded
+    by libtorch_hip) is the one this library binds to: the library's
+    dependency is resolved by that SONAME, and a process that loaded the
+    system copy first would end up with two HIP runtimes and stream handles
+    that do not belong to the runtime launching the kernels.
+    """
+    import torch  # noqa: F401  (binds the library to torch's HIP runtime)
     lib = ctypes.CDLL(str(native_path()))
     for name in ("launch_sharedkv_c8_sparse", "launch_sharedkv_c8_dense", "launch_sharedkv_c8_sparse_small"):
         fn = getattr(lib, name)

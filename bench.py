@@ -89,7 +89,7 @@ def main():
     ap.add_argument("--workload", default="headline")
     ap.add_argument("--splits", type=int, default=None, help="override the host plan's KV partitions")
     ap.add_argument("--page-stride", type=int, default=None, help="override the workload's page stride (bytes)")
-    ap.add_argument("--merge-kernel", action="store_true", help="fold KV partitions in a second kernel")
+    ap.add_argument("--merge", type=int, default=0, help="0: fused partition merge, 1: separate merge launch")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
@@ -104,9 +104,9 @@ def main():
     from tests.device_cases import DeviceCase
 
     torch.cuda.set_device(0)
-    if args.merge_kernel:
-        from npu_sparse_attn_sharedkv_int8.runtime import library
-        library().sharedkv_c8_set_merge_mode(1)
+    from npu_sparse_attn_sharedkv_int8.runtime import library
+    if library().sharedkv_c8_set_merge_mode(args.merge):
+        raise SystemExit(f"unknown merge mode {args.merge}")
     rng = np.random.default_rng(2026)
     seed, ratio, queries, lengths, stride, description = workload(args.workload, rng)
     stride = args.page_stride or stride
@@ -161,7 +161,8 @@ def main():
         "config": {"workload": description, "batch": len(queries), "query_tokens": live_queries, "heads": 8,
                    "dim": 512, "ratio": ratio, "topk": 1024 if ratio == 4 else 0, "window": 128,
                    "page_stride": stride, "layers_rotated": layers, "tile": 128, "splits": splits,
-                   "lse": False, "timing": "one HIP graph replay of K launches, HIP events on its stream"},
+                   "lse": False, "merge": "fused" if args.merge == 0 else "separate launch",
+                   "timing": "one HIP graph replay of K launches, HIP events on its stream"},
         "latency_us_per_layer": ms_per_step * 1e3,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": achieved / PEAK_HBM_GBS, "traffic": traffic,

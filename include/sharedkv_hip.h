@@ -27,11 +27,12 @@ extern "C" {
  * between pages; tables address pages.  Fields this implementation reads:
  *   q (BF16 [tokens][8][512]), ori/cmp (INT8 pages [*, 32, 1, 512]),
  *   oriScale/cmpScale (FP32 [512]), oriTable/cmpTable (INT32 [batch][width]),
- *   indices (INT32 [tokens][1][topk], C4), cuQ (INT32 [batch+1]),
+ *   indices (INT32 [tokens][1][topk], ratio 4), cuQ (INT32 [batch+1]),
  *   seqLens (INT32 [batch]), sinks (FP32 [8]), out (BF16 [tokens][8][512]),
- *   lse (FP32 [tokens][8] or 0), workspace (ticket words, see
- *   sharedkv_c8_workspace_bytes, zero before first use), partial (FP32
- *   split partials, see sharedkv_c8_partial_bytes), splits (KV partitions).
+ *   lse (FP32 [tokens][8] or 0), partial (FP32 [tokens][splits][8][520]
+ *   partition states when splits > 1, see sharedkv_c8_partial_bytes),
+ *   splits (KV partitions), oriPages (pool size of the window cache; rows on
+ *   pages past it are masked).  workspace is accepted and not read.
  * oriIndices must be 0 (explicit original slots are not on this path). */
 typedef struct SharedKVArgs {
     uint64_t q, ori, cmp, oriScale, cmpScale, oriTable, cmpTable, indices;
@@ -71,14 +72,15 @@ typedef struct SharedKVDebug {
 
 /* C4 attention: SWA128 window plus top-k compressed rows (topk <= 1024).
  * Replaces launch_sharedkv_c8_sparse (c4.cpp:70-71).  `blocks` is accepted
- * for ABI compatibility; 0 launches nothing.  The grid is derived from
- * args->tokens and args->splits. */
+ * for ABI compatibility; 0 launches nothing.  The grid is tokens * splits
+ * work-groups (plus a tokens * 8 merge grid when splits > 1). */
 int launch_sharedkv_c8_sparse(uint32_t blocks, void *stream, const SharedKVArgs *args);
 
 /* Small-capacity C4 entry (c4_small.cpp:21-22); same kernel family here. */
 int launch_sharedkv_c8_sparse_small(uint32_t blocks, void *stream, const SharedKVArgs *args);
 
-/* C128 attention: SWA128 window plus every compressed row (c128.cpp:107-108). */
+/* C128 attention: SWA128 window plus every compressed row (c128.cpp:107-108).
+ * Also serves ratio 1 (window only; the reference's legacy R1 plan). */
 int launch_sharedkv_c8_dense(uint32_t blocks, void *stream, const SharedKVArgs *args);
 
 /* Same launch as the three above (ratio taken from args->ratio), with the
@@ -93,8 +95,9 @@ int launch_cache_write(uint32_t blocks, void *stream, const CacheWriteArgs *args
 uint64_t sharedkv_c8_workspace_bytes(uint32_t tokens, uint32_t splits);
 uint64_t sharedkv_c8_partial_bytes(uint32_t tokens, uint32_t splits);
 
-/* 0 = fold split partials in the last work-group of each query (one launch),
- * 1 = fold them in a second kernel.  Process-wide; default 0. */
+/* Partition merge placement.  Mode 1 (the only mode of this build): with
+ * splits > 1 the attention launch is followed by a merge kernel on the same
+ * stream.  Returns 0 for mode 1, hipErrorInvalidValue otherwise. */
 int sharedkv_c8_set_merge_mode(int mode);
 
 /* sizeof(SharedKVArgs), sizeof(CacheWriteArgs), library ABI version. */

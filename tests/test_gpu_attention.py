@@ -290,3 +290,65 @@ def test_empty_launch_is_a_no_op():
     assert op.blocks == 0
     assert op.run().shape == (0, 8, 512)
     torch.cuda.synchronize()
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+def test_merge_modes_match_checker(mode):
+    """Partition states folded by the last partition of each row (mode 0,
+    device-coherent state exchange across XCDs) or by a second launch
+    (mode 1): both bit-exact with the checker."""
+    from npu_sparse_attn_sharedkv_int8.runtime import library
+    lib = library()
+    try:
+        assert lib.sharedkv_c8_set_merge_mode(mode) == 0
+        case = workloads.make_case(27, 4, [2] * 12, list(range(3000, 3000 + 12 * 700, 700)), index_mode="mixed")
+        for splits in (2, 3, 7, 16):
+            say(f"[merge mode {mode}] splits={splits}")
+            out, lse, op = run_hip(case, splits=splits)
+            compare(case, out, lse, splits, tag=f"mode {mode} splits {splits}")
+    finally:
+        lib.sharedkv_c8_set_merge_mode(0)
+
+
+def test_repeated_fused_merges_on_changing_inputs():
+    """One prepared operator rebound to new inputs 24 times in a row, without
+    host synchronisation between launches; every launch is checked, so a stale
+    partition state or a ticket left behind by an earlier launch would show."""
+    import torch
+    from npu_sparse_attn_sharedkv_int8 import PreparedAttention
+    cases = [workloads.make_case(40 + i, 128 if i % 2 else 4, [2, 1, 2], [2500 + 97 * i, 7000 - 55 * i, 4100])
+             for i in range(4)]
+    # Same geometry within a ratio: shared scales, block tables of one width.
+    for first in (0, 1):
+        group = cases[first::2]
+        for kind in ("ori", "cmp"):
+            width = max(c[kind].table.shape[1] for c in group)
+            for c in group:
+                c[kind].scale = group[0][kind].scale
+                table = np.zeros((c[kind].table.shape[0], width), np.int32)
+                table[:, :c[kind].table.shape[1]] = c[kind].table
+                c[kind].table = table
+    devs = [to_device(c) for c in cases]
+    outs = []
+    ops = {}
+    for i in range(24):
+        c = i % 4
+        dev, oscale, cscale, _ = devs[c]
+        ratio = cases[c]["ratio"]
+        if ratio not in ops:
+            ops[ratio] = PreparedAttention(dev, oscale, cscale, splits=5, return_lse=True)
+        op = ops[ratio]
+        out = torch.empty_like(dev.q)
+        lse = torch.empty((dev.q.shape[0], 8), dtype=torch.float32, device="cuda")
+        op._rebind_same_geometry(dev, output=out, lse_output=lse)
+        op.run()
+        outs.append((c, out, lse))
+    torch.cuda.synchronize()
+    say("[repeated fused merges] 24 launches")
+    refs = {}
+    for c, out, lse in outs:
+        if c not in refs:
+            refs[c] = run_oracle(cases[c], 5)[:2]
+        ref, ref_lse = refs[c]
+        assert (bits_of(out) == ref).all(), c
+        np.testing.assert_allclose(lse.cpu().numpy(), ref_lse, rtol=0, atol=2e-6)

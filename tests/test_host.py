@@ -68,6 +68,7 @@ def test_launchers_reject_bad_blocks_without_a_device():
     cw = runtime.CacheWriteArgs()
     assert lib.launch_cache_write(1, None, ctypes.byref(cw)) == 1
     assert lib.sharedkv_c8_set_merge_mode(2) == 1
+    assert lib.sharedkv_c8_set_merge_mode(1) == 0
     assert lib.sharedkv_c8_set_merge_mode(0) == 0
 
 
@@ -75,7 +76,8 @@ def test_host_plan():
     assert c8_attention.max_tiles(4, 1024) == 9
     assert c8_attention.max_tiles(128, 0, 4096) == 2
     assert c8_attention.max_tiles(1, 0) == 1
-    assert c8_attention.choose_splits(64, 4, 1024) == 8
+    assert c8_attention.choose_splits(64, 4, 1024) == 4
+    assert c8_attention.choose_splits(32, 4, 1024) == 8
     assert c8_attention.choose_splits(1, 4, 1024) == 9
     assert c8_attention.choose_splits(4096, 4, 1024) == 1
     assert c8_attention.choose_splits(1, 128, 0, 4096) == 2
