@@ -13,7 +13,7 @@
  *   launch_sharedkv_c8_sparse         csrc/kernels/c8/c4.cpp:70-71
  *   launch_sharedkv_c8_dense          csrc/kernels/c8/c128.cpp:107-108
  *   launch_sharedkv_c8_sparse_small   csrc/kernels/c8/c4_small.cpp:21-22
- *   launch_cache_write                csrc/kernels/cache_write.cpp:79-88
+ *   launch_cache_write                csrc/kernels/cache_write.cpp:71-80
  * The reference launchers return void; these return the launch status.
  */
 #pragma once
@@ -32,7 +32,9 @@ extern "C" {
  *   lse (FP32 [tokens][8] or 0), partial (FP32 [tokens][splits][8][520]
  *   partition states when splits > 1, see sharedkv_c8_partial_bytes),
  *   splits (KV partitions), oriPages (pool size of the window cache; rows on
- *   pages past it are masked).  workspace is accepted and not read.
+ *   pages past it are masked), workspace (one uint32 merge ticket per query
+ *   row, sharedkv_c8_workspace_bytes; zero before the first launch, and each
+ *   launch leaves it zero, so launches that may overlap need their own).
  * oriIndices must be 0 (explicit original slots are not on this path). */
 typedef struct SharedKVArgs {
     uint64_t q, ori, cmp, oriScale, cmpScale, oriTable, cmpTable, indices;
@@ -73,7 +75,7 @@ typedef struct SharedKVDebug {
 /* C4 attention: SWA128 window plus top-k compressed rows (topk <= 1024).
  * Replaces launch_sharedkv_c8_sparse (c4.cpp:70-71).  `blocks` is accepted
  * for ABI compatibility; 0 launches nothing.  The grid is tokens * splits
- * work-groups (plus a tokens * 8 merge grid when splits > 1). */
+ * work-groups (plus a tokens-wide merge grid in merge mode 1). */
 int launch_sharedkv_c8_sparse(uint32_t blocks, void *stream, const SharedKVArgs *args);
 
 /* Small-capacity C4 entry (c4_small.cpp:21-22); same kernel family here. */
@@ -87,7 +89,7 @@ int launch_sharedkv_c8_dense(uint32_t blocks, void *stream, const SharedKVArgs *
  * integer dumps written to `debug`.  Test entry; slower. */
 int sharedkv_c8_attention_debug(void *stream, const SharedKVArgs *args, const SharedKVDebug *debug);
 
-/* Fused INT8 quantise + slot scatter (cache_write.cpp:79-88).  `blocks` is
+/* Fused INT8 quantise + slot scatter (cache_write.cpp:71-80).  `blocks` is
  * accepted for ABI compatibility; 0 launches nothing. */
 int launch_cache_write(uint32_t blocks, void *stream, const CacheWriteArgs *args);
 
@@ -95,9 +97,11 @@ int launch_cache_write(uint32_t blocks, void *stream, const CacheWriteArgs *args
 uint64_t sharedkv_c8_workspace_bytes(uint32_t tokens, uint32_t splits);
 uint64_t sharedkv_c8_partial_bytes(uint32_t tokens, uint32_t splits);
 
-/* Partition merge placement.  Mode 1 (the only mode of this build): with
- * splits > 1 the attention launch is followed by a merge kernel on the same
- * stream.  Returns 0 for mode 1, hipErrorInvalidValue otherwise. */
+/* Partition merge placement for launches with splits > 1 (process-wide).
+ * Mode 0 (default): fused; the last partition of a query row to finish
+ * (ticket in `workspace`) folds the row inside the attention launch.
+ * Mode 1: a separate merge kernel follows on the same stream.  Both give
+ * identical results.  Returns 0, or hipErrorInvalidValue for other modes. */
 int sharedkv_c8_set_merge_mode(int mode);
 
 /* sizeof(SharedKVArgs), sizeof(CacheWriteArgs), library ABI version. */
