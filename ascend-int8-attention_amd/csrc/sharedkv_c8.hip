@@ -9,22 +9,23 @@
 //   split merge     csrc/kernels/c8/attention_impl.h:397-441, reference.py:317-323
 //   cache writer    csrc/kernels/cache_write.cpp:9-88
 //
-// Design (one GPU, HBM bound).  One work-group of 4 waves per (query row, KV
-// partition); partition `part` owns tiles part, part + S, ... of the row's key
-// list (window rows, then compressed rows, cut into 128-key tiles).
+// Design (one GPU, HBM bound).  One work-group of 8 waves (two per SIMD) per
+// (query row, KV partition), one work-group per CU; partition `part` owns
+// tiles part, part + S, ... of the row's key list (window rows, then
+// compressed rows, cut into 128-key tiles).
 //   prologue   every independent load of the row (metadata, indices, Q, both
 //              scale vectors) is issued at once: one memory round trip
-//   addresses  the partition's rows are turned into page codes
-//              (page * 32 + row in page, -1 = masked) in LDS: one round trip
-//              of block-table reads per chunk of tiles
-//   tiles      each of the 4 waves loads its 32 keys straight into the
-//              B-operand registers of v_mfma_i32_16x16x64_i8 (QK needs no
-//              LDS), writes them once to LDS as the V tile, and issues the
-//              next tile's loads into the same registers while softmax and
-//              PV run; PV reads V transposed with ds_read_b64_tr_b8.  Two
-//              work-groups per CU (256 VGPRs, 80 KB LDS)
-//   softmax    FP32 in registers; rows are 8 heads x {code, residual} = the
-//              16 MFMA rows; max and pairwise sums cross waves through LDS
+//   addresses  the partition's rows become page codes (page * 32 + row in
+//              page, -1 = masked) in LDS: one round trip of block-table
+//              reads per chunk of tiles, during which Q is encoded for both
+//              cache kinds
+//   tiles      rows go from HBM straight into a two-tile LDS ring by LDS DMA
+//              (whole 512-byte rows per instruction); the next tile is in
+//              flight while the current one is computed.  QK: each wave takes
+//              16 keys, v_mfma_i32_16x16x64_i8 with the 16 MFMA rows = 8 heads
+//              x {code, residual}; PV: each wave takes 64 output columns and
+//              reads V transposed with ds_read_b64_tr_b8
+//   softmax    FP32 in registers; max and pairwise sums cross waves in LDS
 //   partials   with S > 1 partitions, FP32 [num, max, den] go to `partial`;
 //              the last partition of a row to finish (a ticket per row in
 //              `workspace`) folds them, or c8_merge does in a second launch
@@ -43,22 +44,22 @@ namespace {
 constexpr int D = 512;
 constexpr int HEADS = 8;
 constexpr int N = SHAREDKV_C8_TILE;    // keys per tile
-constexpr int THREADS = 256;           // 4 waves
+constexpr int THREADS = 512;           // 8 waves: two per SIMD
 constexpr int WAVES = THREADS / 64;
-constexpr int VROW = D + 16;           // LDS row stride of the V tile
-constexpr int VTILE = N * VROW + (N / 16) * 128;   // each 16-row block adds 128 B
 constexpr int PROW = N + 16;           // LDS row stride of the P codes
-constexpr int CODE_TILES = 10;         // tiles whose row codes are resident at once
+constexpr int CODE_TILES = 12;         // tiles whose row codes are resident at once
 constexpr int MAX_LIST = 1024;         // C4 top-k capacity of the index list
 constexpr int PART_FLOATS = 520;       // per (row, split, head): 512 numerator, max, denominator
 constexpr int WINDOW = 128;
 constexpr int BLOCK_ROWS = 32;
 constexpr uint32_t MAX_SPLITS = 16;
-static_assert(N == 128 && WINDOW == N, "one window tile of 128 keys; 4 waves x 32 keys");
+static_assert(N == 128 && WINDOW == N && WAVES == 8, "one window tile of 128 keys; 8 waves x 16 keys");
+static_assert(MAX_LIST == 2 * THREADS, "two C4 index entries per thread");
 
 typedef int v4i __attribute__((ext_vector_type(4)));
 typedef int v2i __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) v2i lds_v2i;
 typedef __attribute__((address_space(3))) int8_t lds_i8;
@@ -82,14 +83,16 @@ __device__ __forceinline__ uint32_t f32_to_bf16(float x)
     return u >> 16;
 }
 
-// exp(x): Cody & Waite reduction x = n ln2 + r with a 16-bit head of ln2 and
-// its tail, then the degree-8 Taylor series of e^r in Horner form with fma,
-// scaled by 2^n.  The CPU checker evaluates the identical sequence, so the
-// softmax weights (and the INT8 P codes derived from them) agree bit for bit.
-__device__ __forceinline__ float sk_expf(float x)
+// exp(x) for x <= 0 (or NaN), the only arguments the softmax and the merge
+// produce (differences x - max(...)): Cody & Waite reduction x = n ln2 + r
+// with a 16-bit head of ln2 and its tail, then the degree-8 Taylor series of
+// e^r in Horner form with fma, scaled by 2^n; below -87 the result is 0.  The
+// CPU checker evaluates the identical sequence (its x > 88 overflow branch
+// never fires for such arguments), so the softmax weights and the INT8 P
+// codes derived from them agree bit for bit.
+__device__ __forceinline__ float sk_expf_nonpos(float x)
 {
     if (!(x >= -87.0f)) return x != x ? x : 0.0f;
-    if (x > 88.0f) return __builtin_inff();
     float n = __builtin_rintf(x * 1.44269504088896341f);
     float r = __builtin_fmaf(-n, 0.693145751953125f, x);
     r = __builtin_fmaf(-n, 1.42860682030941723212e-6f, r);
@@ -133,32 +136,84 @@ __device__ __forceinline__ float row16_tree_sum(float x)
     x = x + dpp<DPP_HALF_MIRROR>(x);
     return x + dpp<DPP_MIRROR>(x);
 }
+// Maximum over the 64 lanes of a wave (the same value in every lane).
+__device__ __forceinline__ float wave_max(float x)
+{
+    x = row16_max(x);
+    const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 0));
+    const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 16));
+    const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 32));
+    const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 48));
+    return fmaxf(fmaxf(a, b), fmaxf(c, d));
+}
 
 // A value that is the same in every lane (read from LDS after a barrier),
 // moved to a scalar register so it does not occupy a VGPR.
 __device__ __forceinline__ int uni(int x) { return __builtin_amdgcn_readfirstlane(x); }
 
-// LDS byte offset of key row `key` in the V tile.  Rows are 528 B apart and
-// each 16-row block starts 128 B further on, so 16-byte row writes of 16
-// consecutive keys hit distinct banks (4 banks apart) and the transposed
-// 8-row reads of two neighbouring 16-row blocks land on opposite bank halves.
-__device__ __forceinline__ int vrow(int key) { return key * VROW + (key >> 4) * 128; }
+// Tiles live in LDS as 128 key rows of 512 B, filled straight from HBM by
+// LDS DMA (global_load_lds_dwordx4: one instruction moves 64 lanes x 16 B
+// into 1 KiB of consecutive LDS).  Instruction r (0..7) of wave w moves the
+// rows of keys 16w + r and 16w + 8 + r into row slots 16w + 2r and 16w + 2r
+// + 1, so each lane follows one key through the wave's 8 instructions.
+// Inside a slot the 16-byte chunks are XOR-swizzled with swz(slot), which
+// keeps the DMA writes whole-row and makes both readers conflict-free: the
+// QK operand reads (16 lanes = the 16 keys of a wave, one chunk each) and the
+// transposed PV reads (16 lanes = 8 keys x two 8-byte halves of one chunk;
+// neighbouring 16-lane groups use opposite halves of the banks).
+__device__ __forceinline__ int slot_of(int key) { return (key & ~15) + 2 * (key & 7) + ((key >> 3) & 1); }
+__device__ __forceinline__ int swz(int slot) { return ((slot >> 1) & 7) | (((slot ^ (slot >> 4)) & 1) << 3); }
+__device__ __forceinline__ int tile_offset(int slot, int chunk) { return slot * D + ((chunk ^ swz(slot)) << 4); }
 
 // MFMA row m of the 16-row operands: rows 4g..4g+3 hold heads 2g and 2g+1,
 // each as {code, residual}.  Output lane group g then owns both rows of both
 // of its heads.
 __device__ __forceinline__ int row_of(int head, int residual) { return 4 * (head >> 1) + 2 * (head & 1) + residual; }
 
-struct Shared {
-    int8_t v[VTILE];                // V tile; Q code staging [16][512] at kind switches
-    int8_t p[16 * PROW];            // P codes [MFMA row][key]
-    int32_t code[CODE_TILES * N];   // row codes of the resident tiles: page * 32 + row, -1 masked
-    float scale[2][D];              // channel scales of the window / compressed cache
-    float red[2][WAVES][HEADS];     // per-wave max / sum exchange
-    float asc[HEADS];               // alpha * softmax_scale of the current kind
+// Waits that do not imply a memory fence: LDS DMA of the next tile stays in
+// flight across them.  vm_wait<N> returns once at most N of this wave's
+// vector-memory operations are outstanding (they complete in issue order);
+// lds_barrier makes this wave's LDS writes visible to the work-group.
+template <int N_OUT>
+__device__ __forceinline__ void vm_wait()
+{
+    static_assert(N_OUT == 0 || N_OUT == 8, "encoded waits");
+    if (N_OUT == 0) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    else asm volatile("s_waitcnt vmcnt(8)" ::: "memory");
+}
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// LDS DMA of 16 bytes per lane: lane l's 16 bytes at `src` land at LDS byte
+// address lds + 16 l.  Written as inline assembly so that the compiler does
+// not track it: its own tracking cannot tell the two ring buffers apart and
+// would wait for the next tile's DMA before every LDS read.  The callers
+// order these copies with vm_wait and lds_barrier instead.  M0 carries the
+// LDS address (the compiler keeps nothing live in M0 in this file).
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(uint64_t src, uint32_t lds)
+{
+    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" :: "v"(src), "s"(lds) : "memory", "m0");
+}
+#pragma clang diagnostic pop
+
+constexpr int QSTAGE = D + 16;   // row stride of the Q code staging area
+constexpr int DMA_PER_TILE = N * D / 1024 / WAVES;   // LDS DMA instructions per wave and tile
+static_assert(DMA_PER_TILE == 8, "vm_wait<8> covers one tile in flight");
+
+// Small arrays first, so their LDS offsets fit instruction offset fields.
+struct alignas(16) Shared {
+    float red[2][HEADS][WAVES];     // per-wave max / sum exchange
+    float asc[2][HEADS];            // alpha * softmax_scale per kind
     int32_t scan[WAVES];
     int32_t misc[8];
+    float scale[2][D];              // channel scales of the window / compressed cache
+    int8_t p[16 * PROW];            // P codes [MFMA row][key]
+    int32_t code[CODE_TILES * N];   // row codes of the resident tiles: page * 32 + row, -1 masked
+    uint64_t addr[CODE_TILES * N];  // HBM address of each resident row (masked rows: an in-bounds dummy)
+    int8_t tile[2][N * D];          // two K/V tiles (the DMA ring); Q code staging before the first tile
 };
+static_assert(2 * 16 * QSTAGE <= N * D, "Q staging fits in one tile buffer");
 
 struct Row {
     int32_t batch, position, first_ori, ori_count, count, list_len, t0, total;
@@ -194,7 +249,7 @@ __device__ __forceinline__ f32x4 state_load4(__amdgpu_buffer_rsrc_t r, int offse
 // Folds the S partition states of one query row (reference.py:317-323):
 // top = max of the partition maxima; f_s = exp(max_s - top);
 // out = bf16(sum_s num_s f_s / sum_s den_s f_s), lse = top + log(den).
-// Thread = (head tid / 32, columns 16 (tid % 32) .. + 15) of a 256-thread
+// Thread = (head tid / 64, columns 8 (tid % 64) .. + 7) of a 512-thread
 // group.  Partitions are folded in order.  MAXS bounds S at compile time so
 // every load is issued before any is used (offsets of partitions past S are
 // clamped to partition 0 and their values ignored).  Returns false, writing
@@ -203,15 +258,18 @@ template <int MAXS, int POLICY>
 __device__ __forceinline__ bool fold_states(const __amdgpu_buffer_rsrc_t states, int S, int tid,
                                             uint16_t *out_row, float *lse_row)
 {
-    const int h = tid >> 5, col = (tid & 31) * 16;
+    const int h = tid >> 6, col = (tid & 63) * 8;
     const int head_base = h * PART_FLOATS * 4;
     const int part_step = HEADS * PART_FLOATS * 4;
     float ms[MAXS], ds[MAXS];
+    f32x4 v0[MAXS], v1[MAXS];
 #pragma unroll
     for (int sp = 0; sp < MAXS; ++sp) {
         const int at = head_base + (sp < S ? sp : 0) * part_step;
         ms[sp] = state_load<POLICY>(states, at + 512 * 4);
         ds[sp] = state_load<POLICY>(states, at + 513 * 4);
+        v0[sp] = state_load4<POLICY>(states, at + col * 4);
+        v1[sp] = state_load4<POLICY>(states, at + (col + 4) * 4);
     }
     if (ds[0] < 0.0f) return false;
     float top = ms[0];
@@ -220,29 +278,27 @@ __device__ __forceinline__ bool fold_states(const __amdgpu_buffer_rsrc_t states,
     float f[MAXS], dsum = 0.0f;
 #pragma unroll
     for (int sp = 0; sp < MAXS; ++sp) {
-        f[sp] = sk_expf(ms[sp] - top);
+        f[sp] = sk_expf_nonpos(ms[sp] - top);
         dsum = sp < S ? dsum + ds[sp] * f[sp] : dsum;
     }
+    float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-    for (int c4 = 0; c4 < 4; ++c4) {
-        f32x4 v[MAXS];
+    for (int sp = 0; sp < MAXS; ++sp)
+        if (sp < S) {
+            acc[0] = acc[0] + v0[sp].x * f[sp];
+            acc[1] = acc[1] + v0[sp].y * f[sp];
+            acc[2] = acc[2] + v0[sp].z * f[sp];
+            acc[3] = acc[3] + v0[sp].w * f[sp];
+            acc[4] = acc[4] + v1[sp].x * f[sp];
+            acc[5] = acc[5] + v1[sp].y * f[sp];
+            acc[6] = acc[6] + v1[sp].z * f[sp];
+            acc[7] = acc[7] + v1[sp].w * f[sp];
+        }
+    uint32_t w[4];
 #pragma unroll
-        for (int sp = 0; sp < MAXS; ++sp)
-            v[sp] = state_load4<POLICY>(states, head_base + (sp < S ? sp : 0) * part_step + (col + 4 * c4) * 4);
-        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int sp = 0; sp < MAXS; ++sp)
-            if (sp < S) {
-                acc.x = acc.x + v[sp].x * f[sp];
-                acc.y = acc.y + v[sp].y * f[sp];
-                acc.z = acc.z + v[sp].z * f[sp];
-                acc.w = acc.w + v[sp].w * f[sp];
-            }
-        const uint32_t lo = f32_to_bf16(acc.x / dsum) | (f32_to_bf16(acc.y / dsum) << 16);
-        const uint32_t hi = f32_to_bf16(acc.z / dsum) | (f32_to_bf16(acc.w / dsum) << 16);
-        *reinterpret_cast<u32x2 *>(out_row + h * D + col + 4 * c4) = u32x2{lo, hi};
-    }
-    if (lse_row && (tid & 31) == 0) lse_row[h] = top + logf(dsum);
+    for (int e = 0; e < 4; ++e) w[e] = f32_to_bf16(acc[2 * e] / dsum) | (f32_to_bf16(acc[2 * e + 1] / dsum) << 16);
+    *reinterpret_cast<v4i *>(out_row + h * D + col) = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+    if (lse_row && (tid & 63) == 0) lse_row[h] = top + logf(dsum);
     return true;
 }
 
@@ -256,7 +312,7 @@ __device__ __forceinline__ void fold_row(const __amdgpu_buffer_rsrc_t states, in
 }
 
 template <int RATIO, bool DEBUG>
-__global__ void __launch_bounds__(THREADS, 2)   // 2 waves per SIMD: two work-groups per CU
+__global__ void __launch_bounds__(THREADS, 1)   // one work-group per CU: the 128 KiB tile ring fills the LDS
 c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uint32_t items, uint32_t fused)
 {
     __shared__ Shared s;
@@ -282,25 +338,23 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
         my_cu1 = cu[tid + 1];
         my_len = lens[tid];
     }
-    // Q row t: 8 heads x 512 BF16; thread = head tid / 32, channels (tid % 32) * 16.
-    const int qh = tid >> 5, qd0 = (tid & 31) * 16;
-    const uint16_t *qrow = reinterpret_cast<const uint16_t *>(p.q) + ((int64_t)t * HEADS + qh) * D + qd0;
-    const v4i q0 = *reinterpret_cast<const v4i *>(qrow);
-    const v4i q1 = *reinterpret_cast<const v4i *>(qrow + 8);
-    // Scales of both kinds into LDS (kind = tid / 128, 4 channels per thread).
+    // Q row t: 8 heads x 512 BF16; thread = head (= wave), channels lane * 8.
+    const int qd0 = lane * 8;
+    const v4i qv = *gptr<v4i>(p.q + (((uint64_t)t * HEADS + wave) * D + qd0) * 2);
+    // Scales of both kinds into LDS (kind = tid / 256, 2 channels per thread).
     {
-        const int kind = tid >> 7, c = (tid & 127) * 4;
+        const int kind = tid >> 8, c = (tid & 255) * 2;
         const uint64_t base = (kind && RATIO != 1) ? p.cmpScale : p.oriScale;
-        *reinterpret_cast<f32x4 *>(&s.scale[kind][c]) = *gptr<f32x4>(base + (uint64_t)c * 4);
+        *reinterpret_cast<f32x2 *>(&s.scale[kind][c]) = *gptr<f32x2>(base + (uint64_t)c * 4);
     }
-    // C4 index entries 4 tid .. 4 tid + 3 of row t.
-    int ix[4] = {-1, -1, -1, -1};
+    // C4 index entries 2 tid, 2 tid + 1 of row t.
+    int ix[2] = {-1, -1};
     if (RATIO == 4) {
         const int topk = (int)p.topk;
         const int32_t *row_ix = reinterpret_cast<const int32_t *>(p.indices) + (int64_t)t * topk;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            if (tid * 4 + i < topk) ix[i] = row_ix[tid * 4 + i];
+        for (int i = 0; i < 2; ++i)
+            if (tid * 2 + i < topk) ix[i] = row_ix[tid * 2 + i];
     }
     const float *sinks = reinterpret_cast<const float *>(p.sinks);
     const float sink0 = sinks[2 * g], sink1 = sinks[2 * g + 1];
@@ -337,8 +391,7 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
         // a separate merge launch, partition 0 also marks the row
         // (denominator -1) so that launch leaves it alone.
         if (part == 0) {
-            reinterpret_cast<v4i *>(out_row)[tid * 2] = v4i{0, 0, 0, 0};
-            reinterpret_cast<v4i *>(out_row)[tid * 2 + 1] = v4i{0, 0, 0, 0};
+            reinterpret_cast<v4i *>(out_row)[tid] = v4i{0, 0, 0, 0};
             if (lse_row && tid < HEADS) lse_row[tid] = 0.0f;
             if (S > 1 && !fused && tid < HEADS)
                 reinterpret_cast<float *>(p.partial)[((int64_t)t * S * HEADS + tid) * PART_FLOATS + 513] = -1.0f;
@@ -354,13 +407,13 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
     m.ori_count = m.position + 1 - m.first_ori;
     if (m.ori_count < 0) m.ori_count = 0;
     m.count = RATIO == 1 ? 0 : (m.position + 1) / RATIO;
-    int ipos[4] = {-1, -1, -1, -1};   // list position of each owned C4 entry (-1: none)
+    int ipos[2] = {-1, -1};   // list position of each owned C4 entry (-1: none)
     if (RATIO == 4) {
         const int topk = (int)p.topk;
         const bool compact = m.count < topk && topk <= MAX_LIST;   // reference.py:250
-        int ok[4], mine = 0;
+        int ok[2], mine = 0;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < 2; ++i) {
             ok[i] = ix[i] >= 0 && ix[i] < m.count;
             mine += ok[i];
         }
@@ -380,13 +433,13 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
                 total += s.scan[w];
             }
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
+            for (int i = 0; i < 2; ++i)
                 if (ok[i]) ipos[i] = at++;
             m.list_len = uni(total);
         } else {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int j = tid * 4 + i;
+            for (int i = 0; i < 2; ++i) {
+                const int j = tid * 2 + i;
                 if (j < topk) ipos[i] = j;
                 if (!ok[i]) ix[i] = -1;        // hole: a masked column in place
             }
@@ -402,286 +455,311 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
     const int my_tiles = m.total > part ? (m.total - part + S - 1) / S : 0;   // tiles part, part + S, ...
 
     // ---- per-lane softmax state for heads 2g and 2g+1 ----
-    float mx[2] = {sink0, sink1}, den[2], num[2][8];
+    float mx[2] = {sink0, sink1}, den[2], num[2][4];
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
         den[hh] = part == 0 ? 1.0f : 0.0f;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) num[hh][j] = 0.0f;
+        for (int j = 0; j < 4; ++j) num[hh][j] = 0.0f;
     }
 
     const int positions = 128 + (int)dbg.cmpCapacity;
-    const int c0 = 128 * wave;      // this wave's 128 PV output columns: c0 + 16 j + n
+    const int c0 = 64 * wave;       // this wave's 64 PV output columns: c0 + 16 j + n
+    const int32_t *otab = reinterpret_cast<const int32_t *>(p.oriTable) + (int64_t)m.batch * p.oriTableWidth;
+    const int32_t *ctab = reinterpret_cast<const int32_t *>(p.cmpTable) + (int64_t)m.batch * p.cmpTableWidth;
 
-    // Row codes of partition tiles [first, first + CODE_TILES) into s.code.
-    auto build_codes = [&](int first) {
-        const int ntiles = my_tiles - first < CODE_TILES ? my_tiles - first : CODE_TILES;
-        for (int i = tid; i < ntiles * N; i += THREADS) s.code[i] = -1;
-        __syncthreads();
-        const int32_t *otab = reinterpret_cast<const int32_t *>(p.oriTable) + (int64_t)m.batch * p.oriTableWidth;
-        const int32_t *ctab = reinterpret_cast<const int32_t *>(p.cmpTable) + (int64_t)m.batch * p.cmpTableWidth;
-        // Rows whose logical page lies outside the block table, or whose
-        // physical page is negative or (window cache) past the pool, stay
-        // masked instead of being dereferenced.
-        for (int i = tid; i < ntiles * N; i += THREADS) {
-            const int k = part + S * (first + i / N), r = i % N;
-            int idx = -1;
-            const int32_t *tab = otab;
-            int width = (int)p.oriTableWidth;
-            if (k < m.t0) {
-                if (r < m.ori_count) idx = m.first_ori + r;
-            } else if (RATIO == 128) {
-                const int pos = (k - m.t0) * N + r;
-                if (pos < m.list_len) idx = pos;
-                tab = ctab;
-                width = (int)p.cmpTableWidth;
+    // Q folding and residual split for both kinds (reference.py:274-279),
+    // done once while the block-table reads of the first chunk are in
+    // flight.  Thread = head `wave`, channels qd0 .. qd0 + 7.  Codes are
+    // staged in tile buffer 1 (before any tile lands there) and picked up
+    // in the MFMA A layout.
+    v4i qa0[8], qa1[8];   // Q codes per 64-byte D block, window / compressed kind
+    auto encode_q = [&](bool want0, bool want1) {
+        const uint32_t qw[4] = {(uint32_t)qv.x, (uint32_t)qv.y, (uint32_t)qv.z, (uint32_t)qv.w};
+#pragma unroll
+        for (int kind = 0; kind < 2; ++kind) {
+            if (!(kind ? want1 : want0)) continue;
+            const float *scale = s.scale[kind] + qd0;
+            float f[8];
+            float amax = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                f[e] = bf16_to_f32((qw[e >> 1] >> (16 * (e & 1))) & 0xffffu) * scale[e];
+                amax = fmaxf(amax, fabsf(f[e]));
             }
-            if (idx >= 0 && idx / BLOCK_ROWS < width) {
-                const int32_t page = tab[idx / BLOCK_ROWS];
-                const bool ok = page >= 0 && (k >= m.t0 || (uint32_t)page < p.oriPages);
-                if (ok) s.code[i] = page * BLOCK_ROWS + idx % BLOCK_ROWS;
+            amax = wave_max(amax);              // the head's 512 channels
+            float alpha = amax * (float)(1.0 / 127.0);
+            alpha = alpha < 1e-12f ? 1e-12f : alpha;
+            const float inv = 1.0f / alpha;
+            uint32_t hiw[2] = {0, 0}, low[2] = {0, 0};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float x = clamp127(f[e] * inv);
+                const float hi = __builtin_rintf(x);
+                const float lo = __builtin_rintf((x - hi) * 127.0f);
+                hiw[e >> 2] |= ((uint32_t)(int32_t)hi & 0xffu) << (8 * (e & 3));
+                low[e >> 2] |= ((uint32_t)(int32_t)lo & 0xffu) << (8 * (e & 3));
+            }
+            int8_t *stage = s.tile[1] + kind * 16 * QSTAGE;
+            *reinterpret_cast<u32x2 *>(stage + row_of(wave, 0) * QSTAGE + qd0) = u32x2{hiw[0], hiw[1]};
+            *reinterpret_cast<u32x2 *>(stage + row_of(wave, 1) * QSTAGE + qd0) = u32x2{low[0], low[1]};
+            if (lane == 0) s.asc[kind][wave] = alpha * p.softmaxScale;
+            if (DEBUG) {
+                if (dbg.qcodes) {
+                    int8_t *qc = reinterpret_cast<int8_t *>(dbg.qcodes) + (((int64_t)t * 2 + kind) * 16) * D;
+                    *reinterpret_cast<u32x2 *>(qc + wave * D + qd0) = u32x2{hiw[0], hiw[1]};
+                    *reinterpret_cast<u32x2 *>(qc + (8 + wave) * D + qd0) = u32x2{low[0], low[1]};
+                }
+                if (dbg.alpha && lane == 0)
+                    reinterpret_cast<float *>(dbg.alpha)[((int64_t)t * 2 + kind) * 8 + wave] = alpha;
             }
         }
+        lds_barrier();
+        const int8_t *st0 = s.tile[1], *st1 = s.tile[1] + 16 * QSTAGE;
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj) {
+            qa0[jj] = want0 ? *reinterpret_cast<const v4i *>(st0 + n * QSTAGE + 64 * jj + 16 * g) : v4i{0, 0, 0, 0};
+            qa1[jj] = want1 ? *reinterpret_cast<const v4i *>(st1 + n * QSTAGE + 64 * jj + 16 * g) : v4i{0, 0, 0, 0};
+        }
+    };
+
+    // LDS DMA of resident tile `i` into ring buffer `buf`: 8 instructions per
+    // wave, always all 64 lanes (masked keys read a harmless in-bounds
+    // address instead), so each tile is exactly DMA_PER_TILE vector-memory
+    // operations per wave for vm_wait.
+    auto issue_tile = [&](int i, int buf) {
+        const int h = lane >> 5, c = lane & 31;
+        const uint64_t *rows = s.addr + i * N + 16 * wave + 8 * h;   // keys 16 wave + 8 h + r
+        const uint32_t dst = (uint32_t)(uintptr_t)(lds_i8 *)(s.tile[buf]) + 16 * wave * D;
+        const int hx = (h ^ wave) & 1;
+#pragma unroll
+        for (int r = 0; r < DMA_PER_TILE; ++r) {
+            const int chunk = c ^ r ^ (hx << 3);   // swz(16 wave + 2 r + h)
+            dma16(rows[r] + (uint32_t)(chunk << 4), (uint32_t)uni((int)(dst + 2 * r * D)));
+        }
+    };
+
+    for (int first = 0; first < my_tiles; first += CODE_TILES) {
+        const int ntiles = my_tiles - first < CODE_TILES ? my_tiles - first : CODE_TILES;
+        // ---- row codes of partition tiles [first, first + ntiles) ----
+        for (int i = tid; i < ntiles * N; i += THREADS) {
+            s.code[i] = -1;
+            s.addr[i] = p.q;              // masked rows: DMA reads 512 B of Q, never used
+        }
+        // Window / C128 rows: at most CODE_TILES * N / THREADS entries per
+        // thread, all block-table reads issued before any is used.  Rows
+        // whose logical page lies outside the block table, or whose physical
+        // page is negative or (window cache) past the pool, stay masked.
+        constexpr int PER = CODE_TILES * N / THREADS;
+        int tpage[PER], tidx[PER];
+#pragma unroll
+        for (int e = 0; e < PER; ++e) {
+            const int i = tid + e * THREADS;
+            tidx[e] = -1;
+            tpage[e] = -1;
+            if (i >= ntiles * N) continue;
+            const int k = part + S * (first + i / N), r = i % N;
+            if (k < m.t0) {
+                if (r < m.ori_count) {
+                    const int idx = m.first_ori + r;
+                    if (idx / BLOCK_ROWS < (int)p.oriTableWidth) {
+                        tidx[e] = idx;
+                        tpage[e] = otab[idx / BLOCK_ROWS];
+                    }
+                }
+            } else if (RATIO == 128) {
+                const int idx = (k - m.t0) * N + r;
+                if (idx < m.list_len && idx / BLOCK_ROWS < (int)p.cmpTableWidth) {
+                    tidx[e] = idx;
+                    tpage[e] = ctab[idx / BLOCK_ROWS];
+                }
+            }
+        }
+        int cpage[2] = {-1, -1}, cslot[2] = {-1, -1};
         if (RATIO == 4) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
+            for (int e = 0; e < 2; ++e) {
                 if (ipos[e] < 0 || ix[e] < 0) continue;
                 const int k = m.t0 + ipos[e] / N;
                 if (k < part || (k - part) % S) continue;
                 const int i = (k - part) / S - first;
-                if (i < 0 || i >= ntiles) continue;
-                const int idx = ix[e];
-                if (idx / BLOCK_ROWS < (int)p.cmpTableWidth) {
-                    const int32_t page = ctab[idx / BLOCK_ROWS];
-                    if (page >= 0) s.code[i * N + ipos[e] % N] = page * BLOCK_ROWS + idx % BLOCK_ROWS;
+                if (i < 0 || i >= ntiles || ix[e] / BLOCK_ROWS >= (int)p.cmpTableWidth) continue;
+                cslot[e] = i * N + ipos[e] % N;
+                cpage[e] = ctab[ix[e] / BLOCK_ROWS];
+            }
+        }
+        if (first == 0) {
+            bool want0 = false, want1 = false;
+            for (int i = 0; i < my_tiles; ++i) {
+                const bool kind1 = part + S * i >= m.t0;
+                want0 |= !kind1;
+                want1 |= kind1;
+            }
+            encode_q(want0, want1);       // its barrier also orders the -1 fill before the writes below
+        } else {
+            lds_barrier();
+        }
+#pragma unroll
+        for (int e = 0; e < PER; ++e) {
+            if (tidx[e] < 0) continue;
+            const int i = tid + e * THREADS;
+            const bool window = part + S * (first + i / N) < m.t0;
+            const bool ok = tpage[e] >= 0 && (!window || (uint32_t)tpage[e] < p.oriPages);
+            if (ok) {
+                s.code[i] = tpage[e] * BLOCK_ROWS + tidx[e] % BLOCK_ROWS;
+                s.addr[i] = (window ? p.ori : p.cmp) + (uint64_t)tpage[e] * (window ? p.oriStride : p.cmpStride) +
+                            (uint64_t)((tidx[e] % BLOCK_ROWS) * D);
+            }
+        }
+        if (RATIO == 4) {
+#pragma unroll
+            for (int e = 0; e < 2; ++e)
+                if (cslot[e] >= 0 && cpage[e] >= 0) {
+                    s.code[cslot[e]] = cpage[e] * BLOCK_ROWS + ix[e] % BLOCK_ROWS;
+                    s.addr[cslot[e]] = p.cmp + (uint64_t)cpage[e] * p.cmpStride + (uint64_t)((ix[e] % BLOCK_ROWS) * D);
                 }
-            }
         }
-        __syncthreads();
-    };
+        __syncthreads();   // codes visible; staged Q codes consumed
 
-    // K rows of resident tile `slot` into the B-operand registers:
-    // kq[8 kb + j] = bytes 64 j + 16 g .. + 15 of key 32 wave + 16 kb + n.
-    v4i kq[16];
-    auto load_tile = [&](int slot, int kind) {
-        const uint64_t base = kind ? p.cmp : p.ori;
-        const uint64_t stride = kind ? p.cmpStride : p.oriStride;
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-            const int code = s.code[slot * N + 32 * wave + 16 * kb + n];
-            const uint64_t a = base + (uint64_t)(code >> 5) * stride + (uint64_t)(code & 31) * D + 16 * g;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) kq[8 * kb + j] = code >= 0 ? *gptr<v4i>(a + 64 * j) : v4i{0, 0, 0, 0};
-        }
-    };
+        issue_tile(0, 0);
+        if (ntiles > 1) issue_tile(1, 1);
 
-    v4i qa[8];            // Q codes as MFMA A operands, per 64-byte D block
-    float asc[2] = {0.0f, 0.0f};
-    float sc[8];          // channel scale of this lane's output columns
-    int cur_kind = -1;
-    const uint32_t qw[8] = {(uint32_t)q0.x, (uint32_t)q0.y, (uint32_t)q0.z, (uint32_t)q0.w,
-                            (uint32_t)q1.x, (uint32_t)q1.y, (uint32_t)q1.z, (uint32_t)q1.w};
-
-    // Q folding and residual split for cache kind `kind` (reference.py:274-279).
-    // Runs while no tile is in registers: before the first tile and at the
-    // one switch from the window tile to compressed tiles.
-    auto encode_q = [&](int kind) {
-        const float *scale = s.scale[kind];
-        // The packed BF16 words stay packed until here (an opaque copy keeps
-        // the compiler from hoisting eight expanded floats out of the loop).
-        uint32_t w[8] = {qw[0], qw[1], qw[2], qw[3], qw[4], qw[5], qw[6], qw[7]};
-        asm volatile("" : "+v"(w[0]), "+v"(w[1]), "+v"(w[2]), "+v"(w[3]));
-        asm volatile("" : "+v"(w[4]), "+v"(w[5]), "+v"(w[6]), "+v"(w[7]));
-        float f[16];
-        float amax = 0.0f;
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            f[e] = bf16_to_f32((w[e >> 1] >> (16 * (e & 1))) & 0xffffu) * scale[qd0 + e];
-            amax = fmaxf(amax, fabsf(f[e]));
-        }
-#pragma unroll
-        for (int o = 1; o < 32; o <<= 1) amax = fmaxf(amax, __shfl_xor(amax, o));   // the head's 32 lanes
-        float alpha = amax * (float)(1.0 / 127.0);
-        alpha = alpha < 1e-12f ? 1e-12f : alpha;
-        const float inv = 1.0f / alpha;
-        uint32_t hiw[4] = {0, 0, 0, 0}, low[4] = {0, 0, 0, 0};
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-            const float x = clamp127(f[e] * inv);
-            const float hi = __builtin_rintf(x);
-            const float lo = __builtin_rintf((x - hi) * 127.0f);
-            hiw[e >> 2] |= ((uint32_t)(int32_t)hi & 0xffu) << (8 * (e & 3));
-            low[e >> 2] |= ((uint32_t)(int32_t)lo & 0xffu) << (8 * (e & 3));
-        }
-        int8_t *stage = s.v;
-        *reinterpret_cast<v4i *>(stage + row_of(qh, 0) * D + qd0) = v4i{(int)hiw[0], (int)hiw[1], (int)hiw[2], (int)hiw[3]};
-        *reinterpret_cast<v4i *>(stage + row_of(qh, 1) * D + qd0) = v4i{(int)low[0], (int)low[1], (int)low[2], (int)low[3]};
-        if ((tid & 31) == 0) s.asc[qh] = alpha * p.softmaxScale;
-        if (DEBUG) {
-            if (dbg.qcodes) {
-                int8_t *qc = reinterpret_cast<int8_t *>(dbg.qcodes) + (((int64_t)t * 2 + kind) * 16) * D;
-                *reinterpret_cast<v4i *>(qc + qh * D + qd0) = v4i{(int)hiw[0], (int)hiw[1], (int)hiw[2], (int)hiw[3]};
-                *reinterpret_cast<v4i *>(qc + (8 + qh) * D + qd0) = v4i{(int)low[0], (int)low[1], (int)low[2], (int)low[3]};
-            }
-            if (dbg.alpha && (tid & 31) == 0)
-                reinterpret_cast<float *>(dbg.alpha)[((int64_t)t * 2 + kind) * 8 + qh] = alpha;
-        }
-        __syncthreads();
-#pragma unroll
-        for (int jj = 0; jj < 8; ++jj) qa[jj] = *reinterpret_cast<const v4i *>(stage + n * D + 64 * jj + 16 * g);
-        asc[0] = s.asc[2 * g];
-        asc[1] = s.asc[2 * g + 1];
-#pragma unroll
-        for (int jj = 0; jj < 8; ++jj) sc[jj] = s.scale[kind][c0 + 16 * jj + n];
-        cur_kind = kind;
-        __syncthreads();
-    };
-
-    for (int first = 0; first < my_tiles; first += CODE_TILES) {
-        build_codes(first);
-        const int ntiles = my_tiles - first < CODE_TILES ? my_tiles - first : CODE_TILES;
-        {
-            const int kind0 = part + S * first >= m.t0;
-            if (kind0 != cur_kind) encode_q(kind0);
-            load_tile(0, kind0);
-        }
         for (int i = 0; i < ntiles; ++i) {
             const int k = part + S * (first + i);
-            const int kind = k < m.t0 ? 0 : 1;
+            const int kind = k >= m.t0 ? 1 : 0;
             const int start = (k - (kind ? m.t0 : 0)) * N;
             const int klen = kind ? m.list_len : m.ori_count;
+            const int buf = i & 1;
+            // Outstanding DMA: tile i, and tile 1 while tile 0 is awaited.
+            if (!DEBUG && i == 0 && ntiles > 1) vm_wait<DMA_PER_TILE>();
+            else vm_wait<0>();
+            lds_barrier();   // every wave's DMA of tile i has landed; every wave is done with tile i - 1
+            if (i >= 1 && i + 1 < ntiles) issue_tile(i + 1, buf ^ 1);
+            const int8_t *tb = s.tile[buf];
+            const int key = 16 * wave + n;   // this lane's key in QK and softmax
 
-            // ---- QK: S[16 rows][32 keys of this wave] (reference.py:286-289) ----
-            v4i sacc[2];
+            // ---- QK: S[16 rows][16 keys of this wave] (reference.py:286-289) ----
+            v4i sacc = {0, 0, 0, 0};
+            {
+                const int sl = slot_of(key);
+                v4i b[8];
 #pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
-                v4i acc = {0, 0, 0, 0};
+                for (int j = 0; j < 8; ++j) b[j] = *reinterpret_cast<const v4i *>(tb + tile_offset(sl, 4 * j + g));
+                if (kind) {
 #pragma unroll
-                for (int j = 0; j < 8; ++j) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(qa[j], kq[8 * kb + j], acc, 0, 0, 0);
-                sacc[kb] = acc;
+                    for (int j = 0; j < 8; ++j) sacc = __builtin_amdgcn_mfma_i32_16x16x64_i8(qa1[j], b[j], sacc, 0, 0, 0);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) sacc = __builtin_amdgcn_mfma_i32_16x16x64_i8(qa0[j], b[j], sacc, 0, 0, 0);
+                }
             }
-            // ---- the same rows become the V tile ----
-            bool valid[2];
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
-                const int key = 32 * wave + 16 * kb + n;
-                valid[kb] = s.code[i * N + key] >= 0;
-                int8_t *row = s.v + vrow(key) + 16 * g;
-#pragma unroll
-                for (int j = 0; j < 8; ++j) *reinterpret_cast<v4i *>(row + 64 * j) = kq[8 * kb + j];
-            }
-            // Prefetch the next tile into the same registers while softmax and
-            // PV run (a kind change re-encodes Q first, at the end of the tile).
-            const bool more = i + 1 < ntiles;
-            const int next_kind = part + S * (first + i + 1) >= m.t0;
-            if (more && next_kind == cur_kind) load_tile(i + 1, next_kind);
+            const bool valid = s.code[i * N + key] >= 0;
+            float asc[2];
+            asc[0] = s.asc[kind][2 * g];
+            asc[1] = s.asc[kind][2 * g + 1];
 
             // ---- logits, running max (reference.py:288-303) ----
-            float lg[2][2], tmax[2];
+            float lg[2];
 #pragma unroll
             for (int hh = 0; hh < 2; ++hh) {
-#pragma unroll
-                for (int kb = 0; kb < 2; ++kb) {
-                    const int key = 32 * wave + 16 * kb + n;
-                    const int32_t hi = sacc[kb][2 * hh], lo = sacc[kb][2 * hh + 1];
-                    float dots = (float)hi;
-                    dots = dots + (float)lo * (float)(1.0 / 127.0);
-                    float l = dots * asc[hh];
-                    lg[kb][hh] = valid[kb] ? l : -1e30f;
-                    if (DEBUG && dbg.scores && start + key < klen) {
-                        int32_t *drow = reinterpret_cast<int32_t *>(dbg.scores) + ((int64_t)t * positions + (kind ? 128 : 0) + start + key) * 16;
-                        drow[2 * g + hh] = hi;
-                        drow[8 + 2 * g + hh] = lo;
-                    }
+                const int32_t hi = sacc[2 * hh], lo = sacc[2 * hh + 1];
+                float dots = (float)hi;
+                dots = dots + (float)lo * (float)(1.0 / 127.0);
+                const float l = dots * asc[hh];
+                lg[hh] = valid ? l : -1e30f;
+                if (DEBUG && dbg.scores && start + key < klen) {
+                    // masked rows are zero rows in the reference (reference.py:283-286)
+                    int32_t *drow = reinterpret_cast<int32_t *>(dbg.scores) + ((int64_t)t * positions + (kind ? 128 : 0) + start + key) * 16;
+                    drow[2 * g + hh] = valid ? hi : 0;
+                    drow[8 + 2 * g + hh] = valid ? lo : 0;
                 }
-                tmax[hh] = row16_max(fmaxf(lg[0][hh], lg[1][hh]));
+                const float tmax = row16_max(lg[hh]);
+                if (n == 0) s.red[0][2 * g + hh][wave] = tmax;
             }
-            if (n == 0) {
-                s.red[0][wave][2 * g] = tmax[0];
-                s.red[0][wave][2 * g + 1] = tmax[1];
-            }
-            __syncthreads();
-            float mnew[2], factor[2], wsum[2];
+            lds_barrier();
+            float mnew[2], factor[2];
 #pragma unroll
             for (int hh = 0; hh < 2; ++hh) {
                 const int h = 2 * g + hh;
-                float mm = mx[hh];
-#pragma unroll
-                for (int w = 0; w < WAVES; ++w) mm = fmaxf(mm, s.red[0][w][h]);
+                const f32x4 a = *reinterpret_cast<const f32x4 *>(&s.red[0][h][0]);
+                const f32x4 b = *reinterpret_cast<const f32x4 *>(&s.red[0][h][4]);
+                const float mm = fmaxf(fmaxf(fmaxf(mx[hh], a.x), fmaxf(a.y, a.z)),
+                                       fmaxf(fmaxf(a.w, b.x), fmaxf(fmaxf(b.y, b.z), b.w)));
                 mnew[hh] = mm;
-                factor[hh] = sk_expf(mx[hh] - mnew[hh]);
+                factor[hh] = sk_expf_nonpos(mx[hh] - mnew[hh]);
             }
             // ---- weights, pairwise tile sum, P codes (reference.py:304-312) ----
 #pragma unroll
             for (int hh = 0; hh < 2; ++hh) {
-                float part_sum[2];
-#pragma unroll
-                for (int kb = 0; kb < 2; ++kb) {
-                    const int key = 32 * wave + 16 * kb + n;
-                    const float w = sk_expf(lg[kb][hh] - mnew[hh]);
-                    const float x = w * 127.0f;
-                    const float ph = __builtin_rintf(x);
-                    const float pl = __builtin_rintf((x - ph) * 127.0f);
-                    s.p[row_of(2 * g + hh, 0) * PROW + key] = (int8_t)(int32_t)ph;
-                    s.p[row_of(2 * g + hh, 1) * PROW + key] = (int8_t)(int32_t)pl;
-                    if (DEBUG && dbg.probs && start + key < klen) {
-                        int8_t *drow = reinterpret_cast<int8_t *>(dbg.probs) + ((int64_t)t * positions + (kind ? 128 : 0) + start + key) * 16;
-                        drow[2 * g + hh] = (int8_t)(int32_t)ph;
-                        drow[8 + 2 * g + hh] = (int8_t)(int32_t)pl;
-                    }
-                    part_sum[kb] = row16_tree_sum(w);
+                const float w = sk_expf_nonpos(lg[hh] - mnew[hh]);
+                const float x = w * 127.0f;
+                const float ph = __builtin_rintf(x);
+                const float pl = __builtin_rintf((x - ph) * 127.0f);
+                s.p[row_of(2 * g + hh, 0) * PROW + key] = (int8_t)(int32_t)ph;
+                s.p[row_of(2 * g + hh, 1) * PROW + key] = (int8_t)(int32_t)pl;
+                if (DEBUG && dbg.probs && start + key < klen) {
+                    int8_t *drow = reinterpret_cast<int8_t *>(dbg.probs) + ((int64_t)t * positions + (kind ? 128 : 0) + start + key) * 16;
+                    drow[2 * g + hh] = (int8_t)(int32_t)ph;
+                    drow[8 + 2 * g + hh] = (int8_t)(int32_t)pl;
                 }
-                wsum[hh] = part_sum[0] + part_sum[1];   // this wave's 32 keys
+                const float wsum = row16_tree_sum(w);   // this wave's 16 keys
+                if (n == 0) s.red[1][2 * g + hh][wave] = wsum;
             }
-            if (n == 0) {
-                s.red[1][wave][2 * g] = wsum[0];
-                s.red[1][wave][2 * g + 1] = wsum[1];
-            }
-            __syncthreads();
+            lds_barrier();
 #pragma unroll
             for (int hh = 0; hh < 2; ++hh) {
-                // Pairwise over the four 32-key blocks.
+                // Pairwise over the eight 16-key blocks.
                 const int h = 2 * g + hh;
-                const float tile_sum = (s.red[1][0][h] + s.red[1][1][h]) + (s.red[1][2][h] + s.red[1][3][h]);
+                const f32x4 a = *reinterpret_cast<const f32x4 *>(&s.red[1][h][0]);
+                const f32x4 b = *reinterpret_cast<const f32x4 *>(&s.red[1][h][4]);
+                const float tile_sum = ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w));
                 den[hh] = den[hh] * factor[hh] + tile_sum;
             }
 
-            // ---- PV: [16 rows][this wave's 128 columns] (reference.py:310-316) ----
-            v4i vacc[8];
+            // ---- PV: [16 rows][this wave's 64 columns] (reference.py:310-316) ----
+            v4i vacc[4];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) vacc[j] = v4i{0, 0, 0, 0};
-            lds_i8 *vbase = (lds_i8 *)(s.v);   // generic -> LDS address space
+            for (int j = 0; j < 4; ++j) vacc[j] = v4i{0, 0, 0, 0};
+            const lds_i8 *vbase = (const lds_i8 *)(tb);   // generic -> LDS address space
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
                 // A: P row n, keys 64 kb + 16 g .. + 15.  B: two transposed
                 // 8-key reads; lanes 2r / 2r+1 address the two 8-column halves
                 // of key row r, lane n receives column n of the 16-column block.
                 const v4i pa = *reinterpret_cast<const v4i *>(s.p + n * PROW + 64 * kb + 16 * g);
-                const int krow = 64 * kb + 16 * g + (n >> 1);
-                const int lo_addr = vrow(krow) + c0 + 8 * (n & 1);
-                const int hi_addr = vrow(krow + 8) + c0 + 8 * (n & 1);
+                const int sl_lo = slot_of(64 * kb + 16 * g + (n >> 1));
+                const int sl_hi = slot_of(64 * kb + 16 * g + 8 + (n >> 1));
+                v2i b0[4], b1[4];
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const v2i b0 = __builtin_amdgcn_ds_read_tr8_b64_v2i32(reinterpret_cast<lds_v2i *>(vbase + lo_addr + 16 * j));
-                    const v2i b1 = __builtin_amdgcn_ds_read_tr8_b64_v2i32(reinterpret_cast<lds_v2i *>(vbase + hi_addr + 16 * j));
-                    const v4i vb = {b0.x, b0.y, b1.x, b1.y};
+                for (int j = 0; j < 4; ++j) {
+                    const int chunk = 4 * wave + j;
+                    b0[j] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i *)(vbase + tile_offset(sl_lo, chunk) + 8 * (n & 1)));
+                    b1[j] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i *)(vbase + tile_offset(sl_hi, chunk) + 8 * (n & 1)));
+                }
+                __builtin_amdgcn_sched_barrier(0);   // all reads in flight before the first MFMA waits
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const v4i vb = {b0[j].x, b0[j].y, b1[j].x, b1[j].y};
                     vacc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(pa, vb, vacc[j], 0, 0, 0);
                 }
             }
             if (DEBUG && dbg.values && k < (int)dbg.tileCapacity) {
                 int32_t *vout = reinterpret_cast<int32_t *>(dbg.values) + ((int64_t)t * dbg.tileCapacity + k) * 16 * D;
 #pragma unroll
-                for (int j = 0; j < 8; ++j)
+                for (int j = 0; j < 4; ++j)
 #pragma unroll
                     for (int hh = 0; hh < 2; ++hh) {
                         vout[(2 * g + hh) * D + c0 + 16 * j + n] = vacc[j][2 * hh];
                         vout[(8 + 2 * g + hh) * D + c0 + 16 * j + n] = vacc[j][2 * hh + 1];
                     }
             }
+            float sc[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) sc[j] = s.scale[kind][c0 + 16 * j + n];
 #pragma unroll
             for (int hh = 0; hh < 2; ++hh) {
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
+                for (int j = 0; j < 4; ++j) {
                     float dots = (float)vacc[j][2 * hh];
                     dots = dots + (float)vacc[j][2 * hh + 1] * (float)(1.0 / 127.0);
                     const float pv = dots * sc[j] * (float)(1.0 / 127.0);
@@ -689,12 +767,8 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
                 }
                 mx[hh] = mnew[hh];
             }
-            __syncthreads();
-            if (more && next_kind != cur_kind) {
-                encode_q(next_kind);
-                load_tile(i + 1, next_kind);
-            }
         }
+        __syncthreads();   // tile buffers, P codes, sums and s.code are free again
     }
 
     if (S == 1) {
@@ -703,7 +777,7 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
         for (int hh = 0; hh < 2; ++hh) {
             const int h = 2 * g + hh;
 #pragma unroll
-            for (int j = 0; j < 8; ++j) out_row[h * D + c0 + 16 * j + n] = (uint16_t)f32_to_bf16(num[hh][j] / den[hh]);
+            for (int j = 0; j < 4; ++j) out_row[h * D + c0 + 16 * j + n] = (uint16_t)f32_to_bf16(num[hh][j] / den[hh]);
             if (lse_row && wave == 0 && n == 0) lse_row[h] = mx[hh] + logf(den[hh]);
         }
         return;
@@ -717,7 +791,7 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
         const int h = 2 * g + hh;
         const int base = ((part * HEADS + h) * PART_FLOATS) * 4;   // byte offset in the row's states
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
+        for (int j = 0; j < 4; ++j)
             state_store<SC1>(num[hh][j], states, base + (c0 + 16 * j + n) * 4);
         if (wave == 0 && n == 0) {
             state_store<SC1>(mx[hh], states, base + 512 * 4);
@@ -742,10 +816,10 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
     fold_row<SC1>(states, S, tid, out_row, lse_row);
 }
 
-// Partition merge as a second launch (merge mode 1): one 256-thread group
+// Partition merge as a second launch (merge mode 1): one 512-thread group
 // per query row, the same fold as the attention kernel's last partition.
 // Rows that partition 0 marked as graph padding keep the zeros it wrote.
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(THREADS)
 c8_merge(const SharedKVArgs p, uint32_t splits)
 {
     const int t = blockIdx.x, S = (int)splits;
@@ -832,7 +906,7 @@ int launch_attention(hipStream_t stream, const SharedKVArgs *a, const SharedKVDe
     else
         hipLaunchKernelGGL((c8_attention<1, DEBUG>), dim3(grid), dim3(THREADS), 0, stream, *a, dbg, splits, items, fused);
     if (splits > 1 && !fused)
-        hipLaunchKernelGGL(c8_merge, dim3(a->tokens), dim3(256), 0, stream, *a, splits);
+        hipLaunchKernelGGL(c8_merge, dim3(a->tokens), dim3(THREADS), 0, stream, *a, splits);
     return (int)hipGetLastError();
 }
 

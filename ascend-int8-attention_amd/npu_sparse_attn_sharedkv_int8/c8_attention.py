@@ -12,11 +12,12 @@ capacity alone, so the plan (and hence the numerics) is a pure function of
   splits KV partitions; tile k is folded into partition k % splits and the
          partitions are merged by log-sum-exp in the same launch
 
-A query row is one work-group per partition, so splits is raised until the
-launch has about TARGET_GROUPS work-groups (one per MI355X compute unit;
-measured on the B=32 x T=2 C4 decode: 4 partitions of ~2-3 tiles beat 8
-partitions of ~1 tile, whose fixed per-work-group latency and merge traffic
-dominate).
+A query row is one work-group per partition (one work-group per compute
+unit: its two-tile LDS ring takes most of the CU's 160 KiB), so splits is
+raised until the launch has about TARGET_GROUPS work-groups.  Measured on the
+B=32 x T=2 C4 decode (9 tiles per row): 3 partitions of 3 tiles (192
+work-groups) beat 4 partitions of 2-3 tiles and 2 partitions of 4-5 tiles;
+more partitions than fit one wave of work-groups (256) queue behind it.
 """
 import copy
 import ctypes
@@ -34,7 +35,7 @@ MAX_SPLITS = 16
 WINDOW = 128
 BLOCK = 32
 MAX_TOPK = 1024
-TARGET_GROUPS = CORES
+TARGET_GROUPS = 3 * CORES // 4
 PARTIAL_FLOATS = 520       # per (token, partition, head): 512 numerator, max, denominator, pad
 
 VARIANT_SPARSE, VARIANT_DENSE, VARIANT_SPARSE_SMALL = 20, 21, 22

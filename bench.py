@@ -92,6 +92,9 @@ def main():
     ap.add_argument("--merge", type=int, default=0, help="0: fused partition merge, 1: separate merge launch")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="also run a plain device copy of MIB MiB four times (the reference kernel "
+                         "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
@@ -149,10 +152,14 @@ def main():
     mean_bytes = sum(bytes_per_launch[i % layers] for i in range(args.steps)) / args.steps
     achieved = mean_bytes / (ms_per_step * 1e-3) / 1e9
 
+    # HBM bytes per launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE
+    # (scaled by a plain copy's reading); the summary states the commands.
     traffic = None
-    traffic_file = ROOT / "profiles" / f"traffic_{args.workload}.json"
+    traffic_file = ROOT / "profiles" / f"traffic_{args.workload}.md"
     if traffic_file.exists():
-        traffic = json.loads(traffic_file.read_text()).get("bytes_per_launch")
+        for line in traffic_file.read_text().splitlines():
+            if line.startswith("bytes_per_launch:"):
+                traffic = int(line.split(":", 1)[1])
 
     record = {
         "metric": METRIC, "value": live_queries / (ms_per_step * 1e-3), "unit": "queries/s", "n_gpus": 1,
@@ -168,6 +175,15 @@ def main():
                      "frac": achieved / PEAK_HBM_GBS, "traffic": traffic,
                      "algorithmic_bytes_per_launch": mean_bytes},
     }
+    if args.copy_calibration:
+        n = args.copy_calibration << 20
+        src = torch.ones(n, dtype=torch.int8, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(4):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"[bench] copy calibration: 4 copies of {n} bytes (read {n // 1024} KiB, write {n // 1024} KiB each)")
+        del src, dst
     if not args.no_cpu:
         log(f"[bench] CPU baseline ({args.cpu_seconds:.0f} s sample)")
         record["cpu_baseline"] = cpu_baseline(dc, layers, splits, args.cpu_seconds)
