@@ -50,6 +50,7 @@ constexpr int PROW = N + 16;           // LDS row stride of the P codes
 constexpr int CODE_TILES = 12;         // tiles whose row codes are resident at once
 constexpr int MAX_LIST = 1024;         // C4 top-k capacity of the index list
 constexpr int PART_FLOATS = 520;       // per (row, split, head): 512 numerator, max, denominator
+constexpr int FOLD_SLOT = 514;         // partition 0, head 0: partitions to fold (merge launch), 0 = none
 constexpr int WINDOW = 128;
 constexpr int BLOCK_ROWS = 32;
 constexpr uint32_t MAX_SPLITS = 16;
@@ -252,10 +253,9 @@ __device__ __forceinline__ f32x4 state_load4(__amdgpu_buffer_rsrc_t r, int offse
 // Thread = (head tid / 64, columns 8 (tid % 64) .. + 7) of a 512-thread
 // group.  Partitions are folded in order.  MAXS bounds S at compile time so
 // every load is issued before any is used (offsets of partitions past S are
-// clamped to partition 0 and their values ignored).  Returns false, writing
-// nothing, for a row partition 0 marked as graph padding (denominator < 0).
+// clamped to partition 0 and their values ignored).
 template <int MAXS, int POLICY>
-__device__ __forceinline__ bool fold_states(const __amdgpu_buffer_rsrc_t states, int S, int tid,
+__device__ __forceinline__ void fold_states(const __amdgpu_buffer_rsrc_t states, int S, int tid,
                                             uint16_t *out_row, float *lse_row)
 {
     const int h = tid >> 6, col = (tid & 63) * 8;
@@ -271,7 +271,6 @@ __device__ __forceinline__ bool fold_states(const __amdgpu_buffer_rsrc_t states,
         v0[sp] = state_load4<POLICY>(states, at + col * 4);
         v1[sp] = state_load4<POLICY>(states, at + (col + 4) * 4);
     }
-    if (ds[0] < 0.0f) return false;
     float top = ms[0];
 #pragma unroll
     for (int sp = 1; sp < MAXS; ++sp) top = sp < S ? fmaxf(top, ms[sp]) : top;
@@ -299,7 +298,6 @@ __device__ __forceinline__ bool fold_states(const __amdgpu_buffer_rsrc_t states,
     for (int e = 0; e < 4; ++e) w[e] = f32_to_bf16(acc[2 * e] / dsum) | (f32_to_bf16(acc[2 * e + 1] / dsum) << 16);
     *reinterpret_cast<v4i *>(out_row + h * D + col) = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
     if (lse_row && (tid & 63) == 0) lse_row[h] = top + logf(dsum);
-    return true;
 }
 
 template <int POLICY>
@@ -393,8 +391,8 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
         if (part == 0) {
             reinterpret_cast<v4i *>(out_row)[tid] = v4i{0, 0, 0, 0};
             if (lse_row && tid < HEADS) lse_row[tid] = 0.0f;
-            if (S > 1 && !fused && tid < HEADS)
-                reinterpret_cast<float *>(p.partial)[((int64_t)t * S * HEADS + tid) * PART_FLOATS + 513] = -1.0f;
+            if (S > 1 && !fused && tid == 0)
+                reinterpret_cast<float *>(p.partial)[(int64_t)t * S * HEADS * PART_FLOATS + FOLD_SLOT] = 0.0f;
         }
         return;
     }
@@ -453,6 +451,13 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
     m.t0 = (m.ori_count + N - 1) / N;
     m.total = m.t0 + (m.list_len + N - 1) / N;
     const int my_tiles = m.total > part ? (m.total - part + S - 1) / S : 0;   // tiles part, part + S, ...
+    // Partitions that own no tile (part >= total) hold the initial state
+    // (max = sink <= every owning partition's max, numerator and denominator
+    // 0), which folds to exactly nothing: they publish nothing, and a row
+    // whose tiles all sit in partition 0 is finalized by it directly.  The
+    // numbers equal the fold over all S partitions bit for bit.
+    const int folded = S < m.total ? S : m.total;    // partitions that own tiles (>= 1: the window is never empty)
+    if (part >= folded) return;
 
     // ---- per-lane softmax state for heads 2g and 2g+1 ----
     float mx[2] = {sink0, sink1}, den[2], num[2][4];
@@ -771,7 +776,7 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
         __syncthreads();   // tile buffers, P codes, sums and s.code are free again
     }
 
-    if (S == 1) {
+    if (folded == 1) {
         // ---- finalize (reference.py:317-323 with one partition) ----
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
@@ -780,6 +785,8 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
             for (int j = 0; j < 4; ++j) out_row[h * D + c0 + 16 * j + n] = (uint16_t)f32_to_bf16(num[hh][j] / den[hh]);
             if (lse_row && wave == 0 && n == 0) lse_row[h] = mx[hh] + logf(den[hh]);
         }
+        if (S > 1 && !fused && tid == 0)
+            reinterpret_cast<float *>(p.partial)[(int64_t)t * S * HEADS * PART_FLOATS + FOLD_SLOT] = 0.0f;
         return;
     }
 
@@ -798,7 +805,10 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
             state_store<SC1>(den[hh], states, base + 513 * 4);
         }
     }
-    if (!fused) return;
+    if (!fused) {
+        if (part == 0 && tid == 0) state_store<SC1>((float)folded, states, FOLD_SLOT * 4);
+        return;
+    }
 
     // ---- the last partition of the row to finish folds all of them ----
     // Every state store above has completed (vmcnt 0) before the ticket is
@@ -810,23 +820,26 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
     uint32_t *tickets = reinterpret_cast<uint32_t *>(p.workspace);
     if (tid == 0) s.misc[5] = (int)__hip_atomic_fetch_add(&tickets[t], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
-    if (s.misc[5] != S - 1) return;
+    if (s.misc[5] != folded - 1) return;
     if (tid == 0) __hip_atomic_store(&tickets[t], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-    fold_row<SC1>(states, S, tid, out_row, lse_row);
+    fold_row<SC1>(states, folded, tid, out_row, lse_row);
 }
 
 // Partition merge as a second launch (merge mode 1): one 512-thread group
-// per query row, the same fold as the attention kernel's last partition.
-// Rows that partition 0 marked as graph padding keep the zeros it wrote.
+// per query row, the same fold as the attention kernel's last partition,
+// over the partitions that partition 0 recorded.  Rows it marked 0 (graph
+// padding, or finalized in the attention launch) keep what it wrote.
 __global__ void __launch_bounds__(THREADS)
 c8_merge(const SharedKVArgs p, uint32_t splits)
 {
     const int t = blockIdx.x, S = (int)splits;
     float *row_partial = reinterpret_cast<float *>(p.partial) + (int64_t)t * S * HEADS * PART_FLOATS;
+    const int folded = (int)row_partial[FOLD_SLOT];
+    if (folded < 2 || folded > S) return;
     uint16_t *out_row = reinterpret_cast<uint16_t *>(p.out) + (int64_t)t * HEADS * D;
     float *lse_row = p.lse ? reinterpret_cast<float *>(p.lse) + (int64_t)t * HEADS : nullptr;
-    fold_row<0>(row_states(row_partial), S, threadIdx.x, out_row, lse_row);
+    fold_row<0>(row_states(row_partial), folded, threadIdx.x, out_row, lse_row);
 }
 
 // ---- INT8 cache writer (cache_write.cpp:9-88): one wave per update row ----

@@ -41,21 +41,89 @@ def log(*a):
 
 
 def workload(name, rng):
-    """(seed, ratio, queries, lengths, page stride, description) of a launch."""
+    """(seed, ratio, queries, lengths, page stride, description) of a launch.
+    The BASELINE configs (seeds as recorded there: config 0 uses seed 0)."""
+    s = SERVING_STRIDE
     if name == "headline":
         lengths = rng.integers(2048, 65537, 32)
-        return (7, 4, [2] * 32, lengths, SERVING_STRIDE,
+        return (7, 4, [2] * 32, lengths, s,
                 "headline: C4 top-k1024 decode, B=32 x T=2 (main + draft), ctx~U[2048,65536]")
+    if name == "cfg0":
+        return (0, 128, [1], [4096], s, "config 0: C128 decode, B=1 x T=1, ctx 4096")
+    if name == "cfg1":
+        return (1, 4, [1], [16384], s, "config 1: C4 top-k1024 decode, B=1 x T=1, ctx 16384")
+    if name == "cfg2_c4":
+        lengths = rng.integers(2048, 65537, 16)
+        return (2, 4, [2] * 16, lengths, s, "config 2 C4 launch: 16 seqs x T=2, ctx~U[2048,65536]")
+    if name == "cfg2_c128":
+        lengths = rng.integers(2048, 65537, 16)
+        return (12, 128, [2] * 16, lengths, s, "config 2 C128 launch: 16 seqs x T=2, ctx~U[2048,65536]")
+    if name == "cfg3_prefill":
+        return (3, 4, [2048], [32768], s, "config 3: C4 chunked prefill, B=1 x T=2048 on a 30720 prefix")
+    if name == "cfg4_c4":
+        lengths = rng.integers(65536, 131073, 64)
+        return (4, 4, [1] * 64, lengths, s, "config 4 C4 layer: B=64 x T=1, ctx~U[65536,131072]")
+    if name == "cfg4_c128":
+        lengths = rng.integers(65536, 131073, 64)
+        return (14, 128, [1] * 64, lengths, s, "config 4 C128 layer: B=64 x T=1, ctx~U[65536,131072]")
     if name == "c128":
         lengths = rng.integers(2048, 65537, 32)
-        return (8, 128, [2] * 32, lengths, SERVING_STRIDE, "C128 decode, B=32 x T=2, ctx~U[2048,65536]")
-    if name == "c4_b64_long":
-        lengths = rng.integers(65536, 131073, 64)
-        return (4, 4, [1] * 64, lengths, SERVING_STRIDE, "config 4 C4 layer: B=64 x T=1, ctx~U[65536,131072]")
-    if name == "c128_b64_long":
-        lengths = rng.integers(65536, 131073, 64)
-        return (14, 128, [1] * 64, lengths, SERVING_STRIDE, "config 4 C128 layer: B=64 x T=1, ctx~U[65536,131072]")
+        return (8, 128, [2] * 32, lengths, s, "C128 decode, B=32 x T=2, ctx~U[2048,65536]")
     raise SystemExit(f"unknown workload {name}")
+
+
+WORKLOADS = ["headline", "cfg0", "cfg1", "cfg2_c4", "cfg2_c128", "cfg3_prefill", "cfg4_c4", "cfg4_c128", "c128",
+             "cfg4_writer"]
+
+
+def bench_writer(args, torch):
+    """Config 4's writer: 4096 BF16 rows quantised and scattered through a
+    random unique slot mapping into a stride-viewed block32 pool (page stride
+    622592 B), rotated over `--layers` update batches and pools."""
+    import numpy as np
+    from npu_sparse_attn_sharedkv_int8 import CacheQuantization, PreparedCacheWrite
+    rows, pages, stride = 4096, 1024, SERVING_STRIDE
+    layers = max(1, min(args.layers, stride // 16384))
+    gen = torch.Generator(device="cuda").manual_seed(4)
+    raw = torch.zeros(pages * stride, dtype=torch.int8, device="cuda")
+    ops = []
+    rng = np.random.default_rng(4)
+    for layer in range(layers):
+        cache = raw[layer * 16384:].as_strided((pages, 32, 1, 512), (stride, 512, 512, 1))
+        updates = torch.randn((rows, 512), generator=gen, device="cuda").bfloat16()
+        slots = torch.from_numpy(rng.choice(pages * 32, rows, replace=False).astype(np.int32)).cuda()
+        quant = CacheQuantization.calibrate([updates.float().cpu()])
+        ops.append(PreparedCacheWrite(cache, updates, slots, quant.inverse_scale.cuda()))
+    stream = torch.cuda.Stream()
+    with torch.cuda.stream(stream):
+        for i in range(args.warmup):
+            ops[i % layers].run()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            for i in range(args.steps):
+                ops[i % layers].run()
+        graph.replay()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        graph.replay()
+        end.record(stream)
+        torch.cuda.synchronize()
+    ms_per_step = start.elapsed_time(end) / args.steps
+    algorithmic = rows * (512 * 2 + 512 + 4) + 512 * 4
+    achieved = algorithmic / (ms_per_step * 1e-3) / 1e9
+    return {
+        "metric": "INT8 KV cache write rows/s + HBM GB/s, config 4 writer", "value": rows / (ms_per_step * 1e-3),
+        "unit": "rows/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_per_step,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "i8",
+        "data": "synthetic (GPU-generated, seeded)",
+        "config": {"workload": "config 4 writer: 4096 BF16 rows, random unique int32 slots, page stride 622592",
+                   "rows": rows, "pages": pages, "page_stride": stride, "layers_rotated": layers},
+        "latency_us_per_launch": ms_per_step * 1e3,
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": achieved / PEAK_HBM_GBS, "traffic": None, "algorithmic_bytes_per_launch": algorithmic},
+    }
 
 
 def cpu_baseline(dc, layers, splits, seconds):
@@ -86,7 +154,7 @@ def main():
     ap.add_argument("--steps", type=int, default=160)
     ap.add_argument("--warmup", type=int, default=32)
     ap.add_argument("--layers", type=int, default=16, help="layers rotated over (<= 38 in the page stride)")
-    ap.add_argument("--workload", default="headline")
+    ap.add_argument("--workload", default="headline", choices=WORKLOADS)
     ap.add_argument("--splits", type=int, default=None, help="override the host plan's KV partitions")
     ap.add_argument("--page-stride", type=int, default=None, help="override the workload's page stride (bytes)")
     ap.add_argument("--merge", type=int, default=0, help="0: fused partition merge, 1: separate merge launch")
@@ -107,6 +175,9 @@ def main():
     from tests.device_cases import DeviceCase
 
     torch.cuda.set_device(0)
+    if args.workload == "cfg4_writer":
+        print(json.dumps(bench_writer(args, torch)), flush=True)
+        return
     from npu_sparse_attn_sharedkv_int8.runtime import library
     if library().sharedkv_c8_set_merge_mode(args.merge):
         raise SystemExit(f"unknown merge mode {args.merge}")
@@ -161,8 +232,13 @@ def main():
             if line.startswith("bytes_per_launch:"):
                 traffic = int(line.split(":", 1)[1])
 
+    # int8 MFMA work the launch performs: per selected key, QK and PV over
+    # 16 rows (8 heads x {code, residual}) x 512 channels, 2 ops per MAC.
+    keys = dc.selected_keys(0)
+    int8_ops = keys * 16 * 512 * 2 * 2
+    metric = METRIC if args.workload == "headline" else f"INT8 sharedKV attention queries/s + HBM GB/s, {args.workload}"
     record = {
-        "metric": METRIC, "value": live_queries / (ms_per_step * 1e-3), "unit": "queries/s", "n_gpus": 1,
+        "metric": metric, "value": live_queries / (ms_per_step * 1e-3), "unit": "queries/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_per_step, "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "i8", "data": "synthetic (GPU-generated, seeded)",
         "config": {"workload": description, "batch": len(queries), "query_tokens": live_queries, "heads": 8,
@@ -174,6 +250,8 @@ def main():
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": achieved / PEAK_HBM_GBS, "traffic": traffic,
                      "algorithmic_bytes_per_launch": mean_bytes},
+        "mfma": {"int8_ops_per_launch": int8_ops, "achieved_tops": int8_ops / (ms_per_step * 1e-3) / 1e12,
+                 "peak_tops": 5000.0, "frac": int8_ops / (ms_per_step * 1e-3) / 1e12 / 5000.0},
     }
     if args.copy_calibration:
         n = args.copy_calibration << 20

@@ -272,10 +272,18 @@ def fp64_attention(case, ori_values=None, cmp_values=None):
         kv = ori_values(ori)
         if cmp is not None:
             kv = np.concatenate([kv, cmp_values(cmp)], 0)
-        logits = q[t] @ kv.T * case.softmax_scale
-        ext = np.concatenate([logits, case.sink.astype(np.float64)[:, None]], -1)
-        m = ext.max(-1, keepdims=True)
-        l = (m + np.log(np.exp(ext - m).sum(-1, keepdims=True)))[:, 0]
-        out[t] = np.exp(logits - l[:, None]) @ kv
-        lse[t] = l
+        out[t], lse[t] = fp64_rows(q[t], kv, case.sink, case.softmax_scale)
     return out, lse
+
+
+def fp64_rows(q, kv, sink, softmax_scale):
+    """reference.py:133-136 for one query token: softmax over the rows `kv`
+    plus one sink logit per head that enters the denominator only.
+    q [H, 512], kv [n, 512] (FP64 values); returns (out [H, 512], lse [H])."""
+    q = np.asarray(q, np.float64)
+    kv = np.asarray(kv, np.float64)
+    logits = q @ kv.T * softmax_scale
+    ext = np.concatenate([logits, np.asarray(sink, np.float64)[:, None]], -1)
+    m = ext.max(-1, keepdims=True)
+    l = (m + np.log(np.exp(ext - m).sum(-1, keepdims=True)))[:, 0]
+    return np.exp(logits - l[:, None]) @ kv, l

@@ -319,6 +319,19 @@ class DeviceCase:
                     cmp=self.cmp.host_kind(layer) if self.cmp else None, cmp_indices=self.indices[layer],
                     topk=m["topk"])
 
+    def selected_keys(self, layer=0):
+        """Keys attended over all query tokens: the SWA window rows plus the
+        compressed list (C4: valid top-k entries; C128: every visible entry)."""
+        m = self.meta
+        pos = m["positions"]
+        keys = int(np.minimum(pos + 1, m["window"]).sum())
+        if m["ratio"] == 4:
+            ids = self.indices[layer][:, 0]
+            keys += int(((ids >= 0) & (ids < ((pos + 1) // 4)[:, None])).sum())
+        elif m["ratio"] == 128:
+            keys += int(((pos + 1) // 128).sum())
+        return keys
+
     def algorithmic_bytes(self, layer=0, lse=False):
         """Bytes one launch must move at minimum: each distinct KV row of a
         sequence and kind once (512 B), Q, output (+LSE), the index list, the

@@ -95,6 +95,27 @@ def _golden(name):
     return np.load(Path(__file__).resolve().parent / "golden" / "vectors" / f"{name}.npz")
 
 
+@pytest.mark.parametrize("splits", [None, 1, 2])
+@pytest.mark.parametrize("i", range(8))
+def test_real_activations_match_checker(i, splits):
+    """The reference's captured activations (tests/fixtures/activations) with
+    the layer's frozen serving scales (data/scales_v1.pt), converted by
+    tests/golden/make_fixtures.py: bit-exact with the checker, and inside the
+    reference's gates against the sample's FP64 output (relative L2 < .04,
+    min head cosine > .999; tests/npu/test_attention.py:56, 110)."""
+    from pathlib import Path
+    z = np.load(Path(__file__).resolve().parent / "golden" / "vectors" / "activations.npz")
+    case = workloads.fixture_case(z, i)
+    say(f"[real activations] {z[f'{i}_layer']} ratio {int(z[f'{i}_ratio'])} splits={splits}")
+    out, lse, op = run_hip(case, splits=splits)
+    compare(case, out, lse, op.splits, tag=str(z[f"{i}_layer"]))
+    got = workloads.bf16_value(out[0]).astype(np.float64)
+    want = z[f"{i}_reference"]
+    rel = np.linalg.norm(got - want) / np.linalg.norm(want)
+    cos = ((got * want).sum(-1) / (np.linalg.norm(got, axis=-1) * np.linalg.norm(want, axis=-1))).min()
+    assert rel < 0.04 and cos > 0.999, (rel, cos)
+
+
 @pytest.mark.parametrize("name", ["c128_ctx4096", "c4_raw_holes", "c4_compact_mixed", "c128_mixed", "c4_dups"])
 def test_against_reference_vectors(name):
     """HIP output vs reference.py's own tiled_quantized_reference output with a

@@ -7,7 +7,11 @@ Sources of truth, in order:
   2. the reference's known-answer tests (tests/unit/test_reference.py of the
      reference checkout): rounding/clipping, shared sink denominator,
      padding indices, integer oracle vs FP64 attention;
-  3. what the mathematics fixes: exact integer dot products recomputed by
+  3. the reference's data fixtures (tests/fixtures/activations and the frozen
+     serving scales data/scales_v1.pt, converted by
+     tests/golden/make_fixtures.py): real captured activations with their
+     FP64 attention outputs, and the reference's accuracy gates on them;
+  4. what the mathematics fixes: exact integer dot products recomputed by
      brute force from the dumped codes and the gathered rows, the residual
      reconstruction bounds of the Q and P splits, the pairwise-sum tree,
      and exp against float64.
@@ -93,6 +97,48 @@ def test_fp64_attention_matches_reference_vectors(name):
     live = int(z["cu_q"][-1])
     np.testing.assert_allclose(out[:live], z["fp64_out"][:live], rtol=1e-6, atol=1e-6)
     np.testing.assert_allclose(lse[:live], z["fp64_lse"][:live], rtol=1e-6, atol=1e-6)
+
+
+# ------------------------------------------- reference data fixtures
+
+ACTIVATIONS = GOLDEN / "activations.npz"
+ACT_LAYERS = 11
+ACT_PATH_LAYERS = [0, 1, 2, 3, 4, 5, 6, 7]   # SWA128 + C4/C128 samples (the MTP samples use 133 explicit slots)
+
+
+def head_metrics(got, want):
+    """tests/support/attention_cases.py:9-14 of the reference."""
+    got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
+    a, b = got.reshape(-1, got.shape[-1]), want.reshape(-1, want.shape[-1])
+    cos = (a * b).sum(-1) / (np.linalg.norm(a, axis=-1) * np.linalg.norm(b, axis=-1))
+    return np.linalg.norm(got - want) / np.linalg.norm(want), cos.min()
+
+
+@pytest.mark.parametrize("i", range(ACT_LAYERS))
+def test_fp64_math_reproduces_fixture_reference(i):
+    """The FP64 attention of reference.py:133-136 on each captured sample
+    (query, original + compressed rows, sink) equals the sample's stored
+    `reference` output."""
+    z = np.load(ACTIVATIONS)
+    q = workloads.bf16_value(z[f"{i}_q"]).astype(np.float64)
+    kv = np.concatenate([workloads.bf16_value(z[f"{i}_ori"]), workloads.bf16_value(z[f"{i}_cmp"])]).astype(np.float64)
+    out, _ = ora.fp64_rows(q, kv, z[f"{i}_sink"], float(z[f"{i}_softmax_scale"]))
+    np.testing.assert_allclose(out, z[f"{i}_reference"], rtol=1e-10, atol=1e-12)
+
+
+@pytest.mark.parametrize("splits", [1, 2])
+@pytest.mark.parametrize("i", ACT_PATH_LAYERS)
+def test_int8_path_meets_reference_gates_on_real_activations(i, splits):
+    """The INT8 path (window + compressed rows encoded with the layer's frozen
+    serving scales) against the sample's FP64 output, with the reference's
+    gates: relative L2 < .04 and min head cosine > .999
+    (tests/npu/test_attention.py:56, 110 of the reference)."""
+    z = np.load(ACTIVATIONS)
+    case = workloads.fixture_case(z, i)
+    out, lse, _ = ora.tiled_attention(workloads.oracle_case(case), tile=128, splits=splits)
+    rel, cos = head_metrics(ora.bf16_to_f32(out[0]), z[f"{i}_reference"])
+    assert rel < 0.04 and cos > 0.999, (str(z[f"{i}_layer"]), rel, cos)
+    assert np.isfinite(lse).all()
 
 
 # ------------------------------------------------- reference known answers

@@ -43,9 +43,11 @@ def encode(values, scale):
 
 
 class Kind:
-    """One paged INT8 cache kind (original or compressed)."""
+    """One paged INT8 cache kind (original or compressed).  `rows`, when
+    given, maps (batch, logical row) to that row's BF16 bits; the other rows
+    of touched pages are zero.  `scale` then is the frozen scale to encode with."""
 
-    def __init__(self, name, needed, rng, page_stride, table_width, pool_factor=1.25):
+    def __init__(self, name, needed, rng, page_stride, table_width, pool_factor=1.25, rows=None, scale=None):
         self.name = name
         batch = len(needed)
         touched = [sorted(set(int(i) // BLOCK for i in rows)) for rows in needed]
@@ -60,10 +62,16 @@ class Kind:
                 k += 1
         self.pages = pages
         self.page_stride = page_stride
-        outliers = rng.choice(DIM, 16, replace=False)
-        self.values_bits = kv_rows(rng, pages * BLOCK, outliers)          # BF16 source rows
+        if rows is None:
+            outliers = rng.choice(DIM, 16, replace=False)
+            self.values_bits = kv_rows(rng, pages * BLOCK, outliers)          # BF16 source rows
+        else:
+            self.values_bits = np.zeros((pages * BLOCK, DIM), dtype=np.uint16)
+            for (b, logical), bits in rows.items():
+                physical_page = self.table[b, logical // BLOCK]
+                self.values_bits[physical_page * BLOCK + logical % BLOCK] = bits
         values = bf16_value(self.values_bits)
-        self.scale = frozen_scale(values)
+        self.scale = frozen_scale(values) if scale is None else np.asarray(scale, dtype=np.float32)
         codes = encode(values, self.scale)
         self.pool = np.zeros(pages * page_stride, dtype=np.int8)
         view = self.pool.reshape(pages, page_stride)[:, :BLOCK * DIM]
@@ -142,3 +150,40 @@ def oracle_case(case):
                     cmp_table=cmp.table if cmp else None, cmp_scale=cmp.scale if cmp else None,
                     cmp_indices=case["cmp_indices"], ratio=case["ratio"], window=case["window"],
                     softmax_scale=case["softmax_scale"])
+
+
+def fixture_case(z, i, seed=0, page_stride=BLOCK * DIM):
+    """One query token built from real-activation fixture layer `i`
+    (tests/golden/vectors/activations.npz, converted from the reference's
+    tests/fixtures/activations): the token sits at position n - 1 of a
+    sequence of n = 508 tokens, so its SWA128 window is the fixture's 128
+    original rows and its compressed list is the fixture's compressed rows
+    (all (n // ratio) visible entries; the C4 top-k holds every one of them).
+    Rows are encoded with the layer's frozen serving scales."""
+    ratio = int(z[f"{i}_ratio"])
+    ori_bits, cmp_bits = z[f"{i}_ori"], z[f"{i}_cmp"]
+    window = ori_bits.shape[0]
+    if window != 128 or ratio == 1:
+        raise ValueError("only the SWA128 + compressed samples map onto this path")
+    length = 508
+    count = length // ratio
+    assert cmp_bits.shape[0] == count
+    rng = np.random.default_rng(seed)
+    pos = length - 1
+    first = pos + 1 - window
+    ori_rows = {(0, first + r): ori_bits[r] for r in range(window)}
+    ori = Kind("ori", [range(first, pos + 1)], rng, page_stride, (length + BLOCK - 1) // BLOCK,
+               rows=ori_rows, scale=z[f"{i}_ori_scale"])
+    cmp_rows = {(0, r): cmp_bits[r] for r in range(count)}
+    cmp = Kind("cmp", [range(count)], rng, page_stride, (count + BLOCK - 1) // BLOCK,
+               rows=cmp_rows, scale=z[f"{i}_cmp_scale"])
+    indices = None
+    topk = 0
+    if ratio == 4:
+        topk = 1024
+        indices = np.full((1, 1, topk), -1, dtype=np.int32)
+        indices[0, 0, :count] = np.arange(count)
+    q = z[f"{i}_q"].reshape(1, 8, DIM)
+    return dict(q=q, ori=ori, cu_q=np.array([0, 1], np.int32), seq_lens=np.array([length], np.int32),
+                sink=z[f"{i}_sink"].astype(np.float32), ratio=ratio, window=128,
+                softmax_scale=float(z[f"{i}_softmax_scale"]), cmp=cmp, cmp_indices=indices, topk=topk)
