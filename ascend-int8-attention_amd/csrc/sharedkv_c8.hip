@@ -75,13 +75,14 @@ __device__ __forceinline__ const __attribute__((address_space(1))) T *gptr(uint6
 
 __device__ __forceinline__ float bf16_to_f32(uint32_t bits) { return __uint_as_float(bits << 16); }
 
-// Round to nearest even (torch's .bfloat16()).
-__device__ __forceinline__ uint32_t f32_to_bf16(float x)
+// Two floats to packed BF16 with one v_cvt_pk_bf16_f32: round to nearest
+// even, NaN to the quiet NaN with the upper payload bits kept.  This equals
+// torch's .bfloat16() (and the CPU checker's bit-level rounding) for every
+// 32-bit input.
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi)
 {
-    uint32_t u = __float_as_uint(x);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return u >> 16;
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
 }
 
 // exp(x) for x <= 0 (or NaN), the only arguments the softmax and the merge
@@ -93,9 +94,13 @@ __device__ __forceinline__ uint32_t f32_to_bf16(float x)
 // codes derived from them agree bit for bit.
 __device__ __forceinline__ float sk_expf_nonpos(float x)
 {
-    if (!(x >= -87.0f)) return x != x ? x : 0.0f;
-    float n = __builtin_rintf(x * 1.44269504088896341f);
-    float r = __builtin_fmaf(-n, 0.693145751953125f, x);
+    // Evaluated without a branch: the series runs on a clamped argument and
+    // the result is selected, which keeps both exponentials of a lane in one
+    // instruction stream.
+    const bool in_range = x >= -87.0f;
+    const float xr = in_range ? x : -87.0f;
+    float n = __builtin_rintf(xr * 1.44269504088896341f);
+    float r = __builtin_fmaf(-n, 0.693145751953125f, xr);
     r = __builtin_fmaf(-n, 1.42860682030941723212e-6f, r);
     float p = 1.0f / 40320.0f;
     p = __builtin_fmaf(p, r, 1.0f / 5040.0f);
@@ -106,7 +111,8 @@ __device__ __forceinline__ float sk_expf_nonpos(float x)
     p = __builtin_fmaf(p, r, 0.5f);
     p = __builtin_fmaf(p, r, 1.0f);
     p = __builtin_fmaf(p, r, 1.0f);
-    return __builtin_ldexpf(p, (int)n);
+    const float e = __builtin_ldexpf(p, (int)n);
+    return in_range ? e : (x != x ? x : 0.0f);
 }
 
 __device__ __forceinline__ float clamp127(float x) { return fminf(fmaxf(x, -127.0f), 127.0f); }
@@ -137,6 +143,25 @@ __device__ __forceinline__ float row16_tree_sum(float x)
     x = x + dpp<DPP_HALF_MIRROR>(x);
     return x + dpp<DPP_MIRROR>(x);
 }
+// Order-preserving integer key of a float (for non-NaN values: a < b as
+// floats iff key(a) < key(b) as signed integers, with -0 below +0).  Maxima
+// over keys need no NaN quieting and fuse with DPP lane moves.
+__device__ __forceinline__ int fkey(float f)
+{
+    const int b = __float_as_int(f);
+    return b ^ ((b >> 31) & 0x7fffffff);
+}
+__device__ __forceinline__ float fkey_value(int k) { return __int_as_float(k ^ ((k >> 31) & 0x7fffffff)); }
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int x) { return __builtin_amdgcn_mov_dpp(x, CTRL, 0xF, 0xF, true); }
+__device__ __forceinline__ int row16_max_key(int x)
+{
+    x = max(x, dpp_i<DPP_XOR1>(x));
+    x = max(x, dpp_i<DPP_XOR2>(x));
+    x = max(x, dpp_i<DPP_HALF_MIRROR>(x));
+    return max(x, dpp_i<DPP_MIRROR>(x));
+}
+
 // Maximum over the 64 lanes of a wave (the same value in every lane).
 __device__ __forceinline__ float wave_max(float x)
 {
@@ -204,7 +229,8 @@ static_assert(DMA_PER_TILE == 8, "vm_wait<8> covers one tile in flight");
 
 // Small arrays first, so their LDS offsets fit instruction offset fields.
 struct alignas(16) Shared {
-    float red[2][HEADS][WAVES];     // per-wave max / sum exchange
+    int32_t redmax[HEADS][WAVES];   // per-wave tile maxima (fkey)
+    float redsum[HEADS][WAVES];     // per-wave weight sums
     float asc[2][HEADS];            // alpha * softmax_scale per kind
     int32_t scan[WAVES];
     int32_t misc[8];
@@ -295,7 +321,7 @@ __device__ __forceinline__ void fold_states(const __amdgpu_buffer_rsrc_t states,
         }
     uint32_t w[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) w[e] = f32_to_bf16(acc[2 * e] / dsum) | (f32_to_bf16(acc[2 * e + 1] / dsum) << 16);
+    for (int e = 0; e < 4; ++e) w[e] = pack_bf16(acc[2 * e] / dsum, acc[2 * e + 1] / dsum);
     *reinterpret_cast<v4i *>(out_row + h * D + col) = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
     if (lse_row && (tid & 63) == 0) lse_row[h] = top + logf(dsum);
 }
@@ -304,7 +330,9 @@ template <int POLICY>
 __device__ __forceinline__ void fold_row(const __amdgpu_buffer_rsrc_t states, int S, int tid, uint16_t *out_row,
                                          float *lse_row)
 {
-    if (S <= 4) fold_states<4, POLICY>(states, S, tid, out_row, lse_row);
+    if (S <= 2) fold_states<2, POLICY>(states, S, tid, out_row, lse_row);
+    else if (S == 3) fold_states<3, POLICY>(states, S, tid, out_row, lse_row);
+    else if (S == 4) fold_states<4, POLICY>(states, S, tid, out_row, lse_row);
     else if (S <= 8) fold_states<8, POLICY>(states, S, tid, out_row, lse_row);
     else fold_states<16, POLICY>(states, S, tid, out_row, lse_row);
 }
@@ -534,13 +562,19 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
     // operations per wave for vm_wait.
     auto issue_tile = [&](int i, int buf) {
         const int h = lane >> 5, c = lane & 31;
-        const uint64_t *rows = s.addr + i * N + 16 * wave + 8 * h;   // keys 16 wave + 8 h + r
+        // All eight row addresses are read before the first copy is issued
+        // (each copy is a compiler barrier for LDS accesses).
+        typedef uint64_t u64x2 __attribute__((ext_vector_type(2)));
+        const u64x2 *rows = reinterpret_cast<const u64x2 *>(s.addr + i * N + 16 * wave + 8 * h);   // keys 16 wave + 8 h + r
+        u64x2 ra[DMA_PER_TILE / 2];
+#pragma unroll
+        for (int r = 0; r < DMA_PER_TILE / 2; ++r) ra[r] = rows[r];
         const uint32_t dst = (uint32_t)(uintptr_t)(lds_i8 *)(s.tile[buf]) + 16 * wave * D;
         const int hx = (h ^ wave) & 1;
 #pragma unroll
         for (int r = 0; r < DMA_PER_TILE; ++r) {
             const int chunk = c ^ r ^ (hx << 3);   // swz(16 wave + 2 r + h)
-            dma16(rows[r] + (uint32_t)(chunk << 4), (uint32_t)uni((int)(dst + 2 * r * D)));
+            dma16(ra[r >> 1][r & 1] + (uint32_t)(chunk << 4), (uint32_t)uni((int)(dst + 2 * r * D)));
         }
     };
 
@@ -678,20 +712,28 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
                     drow[2 * g + hh] = valid ? hi : 0;
                     drow[8 + 2 * g + hh] = valid ? lo : 0;
                 }
-                const float tmax = row16_max(lg[hh]);
-                if (n == 0) s.red[0][2 * g + hh][wave] = tmax;
+                const int tmax = row16_max_key(fkey(lg[hh]));
+                if (n == 0) s.redmax[2 * g + hh][wave] = tmax;
             }
             lds_barrier();
             float mnew[2], factor[2];
 #pragma unroll
             for (int hh = 0; hh < 2; ++hh) {
                 const int h = 2 * g + hh;
-                const f32x4 a = *reinterpret_cast<const f32x4 *>(&s.red[0][h][0]);
-                const f32x4 b = *reinterpret_cast<const f32x4 *>(&s.red[0][h][4]);
-                const float mm = fmaxf(fmaxf(fmaxf(mx[hh], a.x), fmaxf(a.y, a.z)),
-                                       fmaxf(fmaxf(a.w, b.x), fmaxf(fmaxf(b.y, b.z), b.w)));
-                mnew[hh] = mm;
-                factor[hh] = sk_expf_nonpos(mx[hh] - mnew[hh]);
+                const v4i a = *reinterpret_cast<const v4i *>(&s.redmax[h][0]);
+                const v4i b = *reinterpret_cast<const v4i *>(&s.redmax[h][4]);
+                const int k = max(max(max(fkey(mx[hh]), a.x), max(a.y, a.z)), max(max(a.w, b.x), max(max(b.y, b.z), b.w)));
+                mnew[hh] = fkey_value(k);
+            }
+            {
+                // One exponential per lane: even lanes take head 2g, odd lanes
+                // head 2g+1; each lane gets the other head's factor from its
+                // neighbour.
+                const bool odd = n & 1;
+                const float mine = sk_expf_nonpos(odd ? mx[1] - mnew[1] : mx[0] - mnew[0]);
+                const float other = dpp<DPP_XOR1>(mine);
+                factor[0] = odd ? other : mine;
+                factor[1] = odd ? mine : other;
             }
             // ---- weights, pairwise tile sum, P codes (reference.py:304-312) ----
 #pragma unroll
@@ -708,15 +750,15 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
                     drow[8 + 2 * g + hh] = (int8_t)(int32_t)pl;
                 }
                 const float wsum = row16_tree_sum(w);   // this wave's 16 keys
-                if (n == 0) s.red[1][2 * g + hh][wave] = wsum;
+                if (n == 0) s.redsum[2 * g + hh][wave] = wsum;
             }
             lds_barrier();
 #pragma unroll
             for (int hh = 0; hh < 2; ++hh) {
                 // Pairwise over the eight 16-key blocks.
                 const int h = 2 * g + hh;
-                const f32x4 a = *reinterpret_cast<const f32x4 *>(&s.red[1][h][0]);
-                const f32x4 b = *reinterpret_cast<const f32x4 *>(&s.red[1][h][4]);
+                const f32x4 a = *reinterpret_cast<const f32x4 *>(&s.redsum[h][0]);
+                const f32x4 b = *reinterpret_cast<const f32x4 *>(&s.redsum[h][4]);
                 const float tile_sum = ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w));
                 den[hh] = den[hh] * factor[hh] + tile_sum;
             }
@@ -782,7 +824,7 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
         for (int hh = 0; hh < 2; ++hh) {
             const int h = 2 * g + hh;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) out_row[h * D + c0 + 16 * j + n] = (uint16_t)f32_to_bf16(num[hh][j] / den[hh]);
+            for (int j = 0; j < 4; ++j) out_row[h * D + c0 + 16 * j + n] = (uint16_t)pack_bf16(num[hh][j] / den[hh], 0.0f);
             if (lse_row && wave == 0 && n == 0) lse_row[h] = mx[hh] + logf(den[hh]);
         }
         if (S > 1 && !fused && tid == 0)
