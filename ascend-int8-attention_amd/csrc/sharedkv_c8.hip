@@ -354,8 +354,8 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
     const int32_t S = (int32_t)splits;
 
     // ---- prologue: every load that depends only on t, issued together ----
-    const int32_t *cu = reinterpret_cast<const int32_t *>(p.cuQ);
-    const int32_t *lens = reinterpret_cast<const int32_t *>(p.seqLens);
+    const __attribute__((address_space(1))) int32_t *cu = gptr<int32_t>(p.cuQ);
+    const __attribute__((address_space(1))) int32_t *lens = gptr<int32_t>(p.seqLens);
     const int batch_n = (int)p.batch;
     // Request b's (cu[b], cu[b+1], len[b]) for b = tid (more in the loops below).
     int my_cu0 = 0, my_cu1 = -1, my_len = 0;
@@ -377,12 +377,12 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
     int ix[2] = {-1, -1};
     if (RATIO == 4) {
         const int topk = (int)p.topk;
-        const int32_t *row_ix = reinterpret_cast<const int32_t *>(p.indices) + (int64_t)t * topk;
+        const __attribute__((address_space(1))) int32_t *row_ix = gptr<int32_t>(p.indices) + (int64_t)t * topk;
 #pragma unroll
         for (int i = 0; i < 2; ++i)
             if (tid * 2 + i < topk) ix[i] = row_ix[tid * 2 + i];
     }
-    const float *sinks = reinterpret_cast<const float *>(p.sinks);
+    const __attribute__((address_space(1))) float *sinks = gptr<float>(p.sinks);
     const float sink0 = sinks[2 * g], sink1 = sinks[2 * g + 1];
 
     // ---- live shape (attention_impl.h:121-137) and the row's request ----
@@ -407,6 +407,10 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
         }
     }
     __syncthreads();
+    // Every metadata load has landed: said explicitly (vmcnt(0)) so that the
+    // compiler's own wait tracking does not hold back the block-table reads
+    // issued next for these registers.
+    __builtin_amdgcn_s_waitcnt(0x0F70);
     const int end = live_batch ? uni(s.misc[2]) : 0;
     const int live_tokens = end <= 0 ? 0 : (end < (int)p.tokens ? end : (int)p.tokens);
     const int batch = uni(s.misc[1]);
@@ -433,6 +437,29 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
     m.ori_count = m.position + 1 - m.first_ori;
     if (m.ori_count < 0) m.ori_count = 0;
     m.count = RATIO == 1 ? 0 : (m.position + 1) / RATIO;
+    // Global-space views: flat loads would also hold the LDS counter that the
+    // fence-free barriers below wait on.
+    const __attribute__((address_space(1))) int32_t *otab = gptr<int32_t>(p.oriTable) + (int64_t)m.batch * p.oriTableWidth;
+    const __attribute__((address_space(1))) int32_t *ctab = gptr<int32_t>(p.cmpTable) + (int64_t)m.batch * p.cmpTableWidth;
+    // C4: every block-table read of the row (the window tile, held by
+    // partition 0, and the thread's two index entries) is issued here, so
+    // the compaction scan below runs while they are in flight.  A C4 row
+    // has at most 1 + MAX_LIST / N <= CODE_TILES tiles: one chunk of codes.
+    int wpage = -1, widx = -1, cpage_raw[2] = {-1, -1};
+    if (RATIO == 4) {
+        if (part == 0 && tid < m.ori_count) {
+            const int idx = m.first_ori + tid;
+            if (idx / BLOCK_ROWS < (int)p.oriTableWidth) {
+                widx = idx;
+                wpage = otab[idx / BLOCK_ROWS];
+            }
+        }
+#pragma unroll
+        for (int e = 0; e < 2; ++e)
+            if (ix[e] >= 0 && ix[e] < m.count && ix[e] / BLOCK_ROWS < (int)p.cmpTableWidth)
+                cpage_raw[e] = ctab[ix[e] / BLOCK_ROWS];
+    }
+    static_assert(1 + MAX_LIST / N <= CODE_TILES, "a C4 row's codes fit one chunk");
     int ipos[2] = {-1, -1};   // list position of each owned C4 entry (-1: none)
     if (RATIO == 4) {
         const int topk = (int)p.topk;
@@ -451,7 +478,7 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
                 if (lane >= o) incl += y;
             }
             if (lane == 63) s.scan[wave] = incl;
-            __syncthreads();
+            lds_barrier();                    // no fence: the table reads stay in flight
             int at = incl - mine, total = 0;
 #pragma unroll
             for (int w = 0; w < WAVES; ++w) {
@@ -498,8 +525,6 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
 
     const int positions = 128 + (int)dbg.cmpCapacity;
     const int c0 = 64 * wave;       // this wave's 64 PV output columns: c0 + 16 j + n
-    const int32_t *otab = reinterpret_cast<const int32_t *>(p.oriTable) + (int64_t)m.batch * p.oriTableWidth;
-    const int32_t *ctab = reinterpret_cast<const int32_t *>(p.cmpTable) + (int64_t)m.batch * p.cmpTableWidth;
 
     // Q folding and residual split for both kinds (reference.py:274-279),
     // done once while the block-table reads of the first chunk are in
@@ -596,6 +621,13 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
             const int i = tid + e * THREADS;
             tidx[e] = -1;
             tpage[e] = -1;
+            if (RATIO == 4) {                 // read before the compaction scan
+                if (e == 0) {
+                    tidx[0] = widx;
+                    tpage[0] = wpage;
+                }
+                continue;
+            }
             if (i >= ntiles * N) continue;
             const int k = part + S * (first + i / N), r = i % N;
             if (k < m.t0) {
@@ -614,7 +646,7 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
                 }
             }
         }
-        int cpage[2] = {-1, -1}, cslot[2] = {-1, -1};
+        int cslot[2] = {-1, -1};
         if (RATIO == 4) {
 #pragma unroll
             for (int e = 0; e < 2; ++e) {
@@ -624,7 +656,6 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
                 const int i = (k - part) / S - first;
                 if (i < 0 || i >= ntiles || ix[e] / BLOCK_ROWS >= (int)p.cmpTableWidth) continue;
                 cslot[e] = i * N + ipos[e] % N;
-                cpage[e] = ctab[ix[e] / BLOCK_ROWS];
             }
         }
         if (first == 0) {
@@ -638,6 +669,13 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
         } else {
             lds_barrier();
         }
+        // The table values are first touched here, after the Q encode: keep
+        // the compiler from hoisting their uses (and the wait for the reads)
+        // above it.
+#pragma unroll
+        for (int e = 0; e < PER; ++e) asm volatile("" : "+v"(tpage[e]));
+#pragma unroll
+        for (int e = 0; e < 2; ++e) asm volatile("" : "+v"(cpage_raw[e]));
 #pragma unroll
         for (int e = 0; e < PER; ++e) {
             if (tidx[e] < 0) continue;
@@ -653,9 +691,9 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
         if (RATIO == 4) {
 #pragma unroll
             for (int e = 0; e < 2; ++e)
-                if (cslot[e] >= 0 && cpage[e] >= 0) {
-                    s.code[cslot[e]] = cpage[e] * BLOCK_ROWS + ix[e] % BLOCK_ROWS;
-                    s.addr[cslot[e]] = p.cmp + (uint64_t)cpage[e] * p.cmpStride + (uint64_t)((ix[e] % BLOCK_ROWS) * D);
+                if (cslot[e] >= 0 && cpage_raw[e] >= 0) {
+                    s.code[cslot[e]] = cpage_raw[e] * BLOCK_ROWS + ix[e] % BLOCK_ROWS;
+                    s.addr[cslot[e]] = p.cmp + (uint64_t)cpage_raw[e] * p.cmpStride + (uint64_t)((ix[e] % BLOCK_ROWS) * D);
                 }
         }
         __syncthreads();   // codes visible; staged Q codes consumed
