@@ -204,9 +204,23 @@ def test_baseline_configs(index):
         torch.cuda.empty_cache()
 
 
-def test_padded_graph_rows_are_zero_and_guards_hold():
+@pytest.mark.parametrize("mode", [0, 1])
+def test_padded_graph_rows_are_zero_and_guards_hold(mode):
     """Capacity rows past the live tokens (seq_len 0 / cu_q sentinel) are
-    zero-filled; bytes around the output and LSE are untouched."""
+    zero-filled; bytes around the output and LSE are untouched; with either
+    merge placement (the separate merge launch must leave padded rows and
+    rows finalized by one partition alone)."""
+    import torch
+    from npu_sparse_attn_sharedkv_int8 import PreparedAttention
+    from npu_sparse_attn_sharedkv_int8.runtime import library
+    assert library().sharedkv_c8_set_merge_mode(mode) == 0
+    try:
+        _padded_rows_case()
+    finally:
+        library().sharedkv_c8_set_merge_mode(0)
+
+
+def _padded_rows_case():
     import torch
     from npu_sparse_attn_sharedkv_int8 import PreparedAttention
     case = workloads.make_case(21, 4, [2, 1, 0, 0], [3000, 700, 0, 0], index_mode="mixed")
@@ -221,7 +235,7 @@ def test_padded_graph_rows_are_zero_and_guards_hold():
     guard_out = torch.full((6 + 2, 8, 512), 123, dtype=torch.bfloat16, device="cuda")
     guard_lse = torch.full((6 + 2, 8), 123, dtype=torch.float32, device="cuda")
     say("[padding] capacity 6, live 3")
-    op = PreparedAttention(dev, oscale, cscale, output=guard_out[1:-1], lse_output=guard_lse[1:-1])
+    op = PreparedAttention(dev, oscale, cscale, output=guard_out[1:-1], lse_output=guard_lse[1:-1], splits=4)
     op.run()
     torch.cuda.synchronize()
     assert (guard_out[[0, -1]].float().cpu() == 123).all() and (guard_lse[[0, -1]].cpu() == 123).all()
@@ -327,6 +341,13 @@ def test_merge_modes_match_checker(mode):
             say(f"[merge mode {mode}] splits={splits}")
             out, lse, op = run_hip(case, splits=splits)
             compare(case, out, lse, splits, tag=f"mode {mode} splits {splits}")
+        # Rows whose tiles all sit in partition 0 (no compressed rows yet) are
+        # finalized by it; the others fold fewer partitions than launched.
+        short = workloads.make_case(28, 128, [2, 1, 3], [60, 130, 900])
+        for splits in (3, 16):
+            say(f"[merge mode {mode}] short rows splits={splits}")
+            out, lse, op = run_hip(short, splits=splits)
+            compare(short, out, lse, splits, tag=f"mode {mode} short splits {splits}")
     finally:
         lib.sharedkv_c8_set_merge_mode(0)
 
