@@ -523,6 +523,25 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
         for (int j = 0; j < 4; ++j) num[hh][j] = 0.0f;
     }
 
+    // PV integers of the last computed tile, awaiting the FP32 epilogue
+    // (reference.py:313-316): num = num * factor + (V_hi + V_lo/127) * scale/127.
+    v4i held_acc[4];
+    float held_sc[4], held_factor[2];
+    bool held = false;
+    auto epilogue = [&]() {
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                float dots = (float)held_acc[j][2 * hh];
+                dots = dots + (float)held_acc[j][2 * hh + 1] * (float)(1.0 / 127.0);
+                const float pv = dots * held_sc[j] * (float)(1.0 / 127.0);
+                num[hh][j] = num[hh][j] * held_factor[hh] + pv;
+            }
+        }
+        held = false;
+    };
+
     const int positions = 128 + (int)dbg.cmpCapacity;
     const int c0 = 64 * wave;       // this wave's 64 PV output columns: c0 + 16 j + n
 
@@ -730,6 +749,7 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
                     for (int j = 0; j < 8; ++j) sacc = __builtin_amdgcn_mfma_i32_16x16x64_i8(qa0[j], b[j], sacc, 0, 0, 0);
                 }
             }
+            if (held) epilogue();            // the previous tile's, behind this tile's QK
             const bool valid = s.code[i * N + key] >= 0;
             float asc[2];
             asc[0] = s.asc[kind][2 * g];
@@ -838,23 +858,23 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
                         vout[(8 + 2 * g + hh) * D + c0 + 16 * j + n] = vacc[j][2 * hh + 1];
                     }
             }
-            float sc[4];
+            // The FP32 epilogue of this tile runs in the next tile's body,
+            // after its QK is issued, so its VALU work overlaps that tile's
+            // LDS reads and MFMAs (or after the last tile).
 #pragma unroll
-            for (int j = 0; j < 4; ++j) sc[j] = s.scale[kind][c0 + 16 * j + n];
-#pragma unroll
-            for (int hh = 0; hh < 2; ++hh) {
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    float dots = (float)vacc[j][2 * hh];
-                    dots = dots + (float)vacc[j][2 * hh + 1] * (float)(1.0 / 127.0);
-                    const float pv = dots * sc[j] * (float)(1.0 / 127.0);
-                    num[hh][j] = num[hh][j] * factor[hh] + pv;
-                }
-                mx[hh] = mnew[hh];
+            for (int j = 0; j < 4; ++j) {
+                held_acc[j] = vacc[j];
+                held_sc[j] = s.scale[kind][c0 + 16 * j + n];
             }
+            held_factor[0] = factor[0];
+            held_factor[1] = factor[1];
+            held = true;
+            mx[0] = mnew[0];
+            mx[1] = mnew[1];
         }
         __syncthreads();   // tile buffers, P codes, sums and s.code are free again
     }
+    if (held) epilogue();
 
     if (folded == 1) {
         // ---- finalize (reference.py:317-323 with one partition) ----
