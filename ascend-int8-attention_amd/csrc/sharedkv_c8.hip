@@ -604,23 +604,32 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
     // wave, always all 64 lanes (masked keys read a harmless in-bounds
     // address instead), so each tile is exactly DMA_PER_TILE vector-memory
     // operations per wave for vm_wait.
-    auto issue_tile = [&](int i, int buf) {
+    // Instructions [r0, r0 + count) of the tile's DMA.  The row addresses
+    // of a batch are read before its first copy is issued (each copy is a
+    // compiler barrier for LDS accesses).
+    auto issue_rows = [&](int i, int buf, int r0, int count) {
         const int h = lane >> 5, c = lane & 31;
-        // All eight row addresses are read before the first copy is issued
-        // (each copy is a compiler barrier for LDS accesses).
         typedef uint64_t u64x2 __attribute__((ext_vector_type(2)));
-        const u64x2 *rows = reinterpret_cast<const u64x2 *>(s.addr + i * N + 16 * wave + 8 * h);   // keys 16 wave + 8 h + r
+        const u64x2 *rows = reinterpret_cast<const u64x2 *>(s.addr + i * N + 16 * wave + 8 * h + r0);   // keys 16 wave + 8 h + r
         u64x2 ra[DMA_PER_TILE / 2];
 #pragma unroll
-        for (int r = 0; r < DMA_PER_TILE / 2; ++r) ra[r] = rows[r];
+        for (int r = 0; r < DMA_PER_TILE / 2; ++r)
+            if (2 * r < count) ra[r] = rows[r];
         const uint32_t dst = (uint32_t)(uintptr_t)(lds_i8 *)(s.tile[buf]) + 16 * wave * D;
         const int hx = (h ^ wave) & 1;
 #pragma unroll
-        for (int r = 0; r < DMA_PER_TILE; ++r) {
+        for (int k = 0; k < DMA_PER_TILE; ++k) {
+            if (k >= count) break;
+            const int r = r0 + k;
             const int chunk = c ^ r ^ (hx << 3);   // swz(16 wave + 2 r + h)
-            dma16(ra[r >> 1][r & 1] + (uint32_t)(chunk << 4), (uint32_t)uni((int)(dst + 2 * r * D)));
+            dma16(ra[k >> 1][k & 1] + (uint32_t)(chunk << 4), (uint32_t)uni((int)(dst + 2 * r * D)));
         }
     };
+    auto issue_tile = [&](int i, int buf) { issue_rows(i, buf, 0, DMA_PER_TILE); };
+    // The next tile's copies are spread over four points of the current
+    // tile's body, two instructions each, so no wave stalls behind a full
+    // tile's worth of queued copies.
+    constexpr int DMA_STEP = DMA_PER_TILE / 4;
 
     for (int first = 0; first < my_tiles; first += CODE_TILES) {
         const int ntiles = my_tiles - first < CODE_TILES ? my_tiles - first : CODE_TILES;
@@ -730,7 +739,8 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
             if (!DEBUG && i == 0 && ntiles > 1) vm_wait<DMA_PER_TILE>();
             else vm_wait<0>();
             lds_barrier();   // every wave's DMA of tile i has landed; every wave is done with tile i - 1
-            if (i >= 1 && i + 1 < ntiles) issue_tile(i + 1, buf ^ 1);
+            const bool stream_next = i >= 1 && i + 1 < ntiles;   // tiles 0 and 1 were issued up front
+            if (stream_next) issue_rows(i + 1, buf ^ 1, 0, DMA_STEP);
             const int8_t *tb = s.tile[buf];
             const int key = 16 * wave + n;   // this lane's key in QK and softmax
 
@@ -749,6 +759,7 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
                     for (int j = 0; j < 8; ++j) sacc = __builtin_amdgcn_mfma_i32_16x16x64_i8(qa0[j], b[j], sacc, 0, 0, 0);
                 }
             }
+            if (stream_next) issue_rows(i + 1, buf ^ 1, DMA_STEP, DMA_STEP);
             if (held) epilogue();            // the previous tile's, behind this tile's QK
             const bool valid = s.code[i * N + key] >= 0;
             float asc[2];
@@ -774,6 +785,7 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
                 if (n == 0) s.redmax[2 * g + hh][wave] = tmax;
             }
             lds_barrier();
+            if (stream_next) issue_rows(i + 1, buf ^ 1, 2 * DMA_STEP, DMA_STEP);
             float mnew[2], factor[2];
 #pragma unroll
             for (int hh = 0; hh < 2; ++hh) {
@@ -811,6 +823,7 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
                 if (n == 0) s.redsum[2 * g + hh][wave] = wsum;
             }
             lds_barrier();
+            if (stream_next) issue_rows(i + 1, buf ^ 1, 3 * DMA_STEP, DMA_STEP);
 #pragma unroll
             for (int hh = 0; hh < 2; ++hh) {
                 // Pairwise over the eight 16-key blocks.
