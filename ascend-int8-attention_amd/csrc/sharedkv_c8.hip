@@ -885,7 +885,7 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
             mx[0] = mnew[0];
             mx[1] = mnew[1];
         }
-        __syncthreads();   // tile buffers, P codes, sums and s.code are free again
+        if (first + CODE_TILES < my_tiles) __syncthreads();   // s.code and the tile buffers are rebuilt next
     }
     if (held) epilogue();
 
