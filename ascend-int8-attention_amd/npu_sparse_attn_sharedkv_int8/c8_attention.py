@@ -12,12 +12,14 @@ capacity alone, so the plan (and hence the numerics) is a pure function of
   splits KV partitions; tile k is folded into partition k % splits and the
          partitions are merged by log-sum-exp in the same launch
 
-A query row is one work-group per partition (one work-group per compute
-unit: its two-tile LDS ring takes most of the CU's 160 KiB), so splits is
-raised until the launch has about TARGET_GROUPS work-groups.  Measured on the
-B=32 x T=2 C4 decode (9 tiles per row): 3 partitions of 3 tiles (192
-work-groups) beat 4 partitions of 2-3 tiles and 2 partitions of 4-5 tiles;
-more partitions than fit one wave of work-groups (256) queue behind it.
+A query row is one work-group per partition, one work-group per compute unit
+(its two-tile LDS ring takes most of the CU's 160 KiB).  More partitions mean
+shorter partitions but a wider merge (each partition's state is written, and
+read back by the one that folds the row).  Measured on MI355X with 9-tile C4
+rows: 3 partitions beat 2, 4, 5, 6 and 8 for 32 and 64 query rows (B=32 x T=2:
+19.4 us at 3, 20.6 at 4; 16 seqs x T=2: 16.6 at 3, 17.2 at 6); a lone query
+row is fastest with 5 (13.3 us, against 14.4 at 9).  The launch keeps to one
+wave of work-groups: tokens * splits <= CORES.
 """
 import copy
 import ctypes
@@ -35,7 +37,9 @@ MAX_SPLITS = 16
 WINDOW = 128
 BLOCK = 32
 MAX_TOPK = 1024
-TARGET_GROUPS = 3 * CORES // 4
+SPLITS_FEW_ROWS = 5        # fewer than FEW_ROWS query rows
+SPLITS_MANY_ROWS = 3
+FEW_ROWS = 8
 PARTIAL_FLOATS = 520       # per (token, partition, head): 512 numerator, max, denominator, pad
 
 VARIANT_SPARSE, VARIANT_DENSE, VARIANT_SPARSE_SMALL = 20, 21, 22
@@ -66,7 +70,8 @@ def choose_splits(tokens, ratio, topk, max_seq_len=None):
     """KV partitions for a launch of `tokens` query rows (host-side plan)."""
     if tokens <= 0:
         return 1
-    wanted = (TARGET_GROUPS + tokens - 1) // tokens
+    wanted = SPLITS_FEW_ROWS if tokens < FEW_ROWS else SPLITS_MANY_ROWS
+    wanted = min(wanted, max(1, CORES // tokens))
     return max(1, min(wanted, max_tiles(ratio, topk, max_seq_len), MAX_SPLITS))
 
 
