@@ -337,7 +337,12 @@ __device__ __forceinline__ void fold_row(const __amdgpu_buffer_rsrc_t states, in
     else fold_states<16, POLICY>(states, S, tid, out_row, lse_row);
 }
 
-template <int RATIO, bool DEBUG>
+// SLOTS: the original kind is the explicit physical slot list of the row
+// (oriIndices [tokens][1][oriTopk], reference.py:236-239 and 285), every
+// entry in its list place, entries outside [0, oriPages * 32) masked, in
+// ceil(oriTopk / 128) tiles; otherwise it is the SWA window through the
+// block table.
+template <int RATIO, bool DEBUG, bool SLOTS>
 __global__ void __launch_bounds__(THREADS, 1)   // one work-group per CU: the 128 KiB tile ring fills the LDS
 c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uint32_t items, uint32_t fused)
 {
@@ -436,6 +441,10 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
     m.first_ori = m.position + 1 > WINDOW ? m.position + 1 - WINDOW : 0;
     m.ori_count = m.position + 1 - m.first_ori;
     if (m.ori_count < 0) m.ori_count = 0;
+    if (SLOTS) {
+        m.first_ori = 0;
+        m.ori_count = (int)p.oriTopk;
+    }
     m.count = RATIO == 1 ? 0 : (m.position + 1) / RATIO;
     // Global-space views: flat loads would also hold the LDS counter that the
     // fence-free barriers below wait on.
@@ -444,10 +453,13 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
     // C4: every block-table read of the row (the window tile, held by
     // partition 0, and the thread's two index entries) is issued here, so
     // the compaction scan below runs while they are in flight.  A C4 row
-    // has at most 1 + MAX_LIST / N <= CODE_TILES tiles: one chunk of codes.
+    // has at most 1 + MAX_LIST / N <= CODE_TILES tiles: one chunk of codes
+    // (explicit slots read theirs per chunk, below).
+    const __attribute__((address_space(1))) int32_t *oslots =
+        gptr<int32_t>(p.oriIndices) + (int64_t)t * p.oriTopk;
     int wpage = -1, widx = -1, cpage_raw[2] = {-1, -1};
     if (RATIO == 4) {
-        if (part == 0 && tid < m.ori_count) {
+        if (!SLOTS && part == 0 && tid < m.ori_count) {
             const int idx = m.first_ori + tid;
             if (idx / BLOCK_ROWS < (int)p.oriTableWidth) {
                 widx = idx;
@@ -649,7 +661,7 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
             const int i = tid + e * THREADS;
             tidx[e] = -1;
             tpage[e] = -1;
-            if (RATIO == 4) {                 // read before the compaction scan
+            if (RATIO == 4 && !SLOTS) {       // read before the compaction scan
                 if (e == 0) {
                     tidx[0] = widx;
                     tpage[0] = wpage;
@@ -658,7 +670,13 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
             }
             if (i >= ntiles * N) continue;
             const int k = part + S * (first + i / N), r = i % N;
-            if (k < m.t0) {
+            if (SLOTS && k < m.t0) {
+                const int j = k * N + r;      // place in the slot list
+                if (j < m.ori_count) {
+                    tidx[e] = j;
+                    tpage[e] = oslots[j];     // the physical slot
+                }
+            } else if (k < m.t0) {
                 if (r < m.ori_count) {
                     const int idx = m.first_ori + r;
                     if (idx / BLOCK_ROWS < (int)p.oriTableWidth) {
@@ -709,6 +727,14 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
             if (tidx[e] < 0) continue;
             const int i = tid + e * THREADS;
             const bool window = part + S * (first + i / N) < m.t0;
+            if (SLOTS && window) {
+                const int slot = tpage[e];
+                if (slot >= 0 && (uint32_t)slot < p.oriPages * BLOCK_ROWS) {
+                    s.code[i] = slot;
+                    s.addr[i] = p.ori + (uint64_t)(slot / BLOCK_ROWS) * p.oriStride + (uint64_t)((slot % BLOCK_ROWS) * D);
+                }
+                continue;
+            }
             const bool ok = tpage[e] >= 0 && (!window || (uint32_t)tpage[e] < p.oriPages);
             if (ok) {
                 s.code[i] = tpage[e] * BLOCK_ROWS + tidx[e] % BLOCK_ROWS;
@@ -997,7 +1023,12 @@ int check_attention(const SharedKVArgs *a)
 {
     if (!a || a->heads != HEADS || (a->ratio != 1 && a->ratio != 4 && a->ratio != 128) || a->window != WINDOW)
         return 1;
-    if (a->oriBlock != BLOCK_ROWS || a->oriIndices) return 1;
+    if (a->oriBlock != BLOCK_ROWS) return 1;
+    // Explicit original slots: at most MAX_LIST per row; slot capacity
+    // oriPages * 32 stays below 2^31.
+    if (a->oriIndices && (a->oriTopk == 0 || a->oriTopk > MAX_LIST || (a->oriIndices & 3) ||
+                          (uint64_t)a->oriPages * BLOCK_ROWS >= (1ull << 31)))
+        return 1;
     if (!a->q || !a->ori || !a->oriScale || !a->oriTable || !a->cuQ || !a->seqLens || !a->sinks || !a->out)
         return 1;
     if (a->batch == 0 || a->oriPages == 0) return 1;
@@ -1025,12 +1056,21 @@ int launch_attention(hipStream_t stream, const SharedKVArgs *a, const SharedKVDe
     const uint32_t items = a->tokens * splits;
     const uint32_t grid = (items + 7u) & ~7u;
     const uint32_t fused = splits > 1 && g_merge_mode == 0;
-    if (a->ratio == 4)
-        hipLaunchKernelGGL((c8_attention<4, DEBUG>), dim3(grid), dim3(THREADS), 0, stream, *a, dbg, splits, items, fused);
+    // Debug dumps hold one original tile (list places 0..127) per row.
+    if (DEBUG && a->oriIndices && a->oriTopk > N) return (int)hipErrorInvalidValue;
+    if (a->oriIndices) {
+        if (a->ratio == 4)
+            hipLaunchKernelGGL((c8_attention<4, DEBUG, true>), dim3(grid), dim3(THREADS), 0, stream, *a, dbg, splits, items, fused);
+        else if (a->ratio == 128)
+            hipLaunchKernelGGL((c8_attention<128, DEBUG, true>), dim3(grid), dim3(THREADS), 0, stream, *a, dbg, splits, items, fused);
+        else
+            hipLaunchKernelGGL((c8_attention<1, DEBUG, true>), dim3(grid), dim3(THREADS), 0, stream, *a, dbg, splits, items, fused);
+    } else if (a->ratio == 4)
+        hipLaunchKernelGGL((c8_attention<4, DEBUG, false>), dim3(grid), dim3(THREADS), 0, stream, *a, dbg, splits, items, fused);
     else if (a->ratio == 128)
-        hipLaunchKernelGGL((c8_attention<128, DEBUG>), dim3(grid), dim3(THREADS), 0, stream, *a, dbg, splits, items, fused);
+        hipLaunchKernelGGL((c8_attention<128, DEBUG, false>), dim3(grid), dim3(THREADS), 0, stream, *a, dbg, splits, items, fused);
     else
-        hipLaunchKernelGGL((c8_attention<1, DEBUG>), dim3(grid), dim3(THREADS), 0, stream, *a, dbg, splits, items, fused);
+        hipLaunchKernelGGL((c8_attention<1, DEBUG, false>), dim3(grid), dim3(THREADS), 0, stream, *a, dbg, splits, items, fused);
     if (splits > 1 && !fused)
         hipLaunchKernelGGL(c8_merge, dim3(a->tokens), dim3(THREADS), 0, stream, *a, splits);
     return (int)hipGetLastError();

@@ -9,9 +9,10 @@ for the reference runs unchanged with device tensors on "cuda" (HIP).
 
 Everything is validated and every buffer is allocated here, outside graph
 capture; run() only launches the HIP kernel on the caller's current stream.
-The only kernel family in this build is the C8 one (c8_attention.py); the
-reference's legacy Ascend variants (R1-only plans, explicit original slots,
-H != 8) have no counterpart and are rejected with ValueError.
+The only kernel family in this build is the C8 one (c8_attention.py).  It
+also serves what the reference routes to its legacy Ascend variants for
+window-only (ratio 1) launches and explicit original slots (draft/MTP
+ori_indices); H != 8 is rejected with ValueError.
 """
 import torch
 
@@ -124,8 +125,9 @@ class PreparedAttention:
             self.blocks, self.splits, self.variant = 0, 1, None
             self.args = None
             return
+        ori_topk = case.ori_indices.shape[-1] if case.ori_indices is not None else 0
         self.splits = splits if splits is not None else c8_attention.choose_splits(
-            tokens, case.ratio, case.cmp_indices.shape[-1] if case.ratio == 4 else 0, max_seq_len)
+            tokens, case.ratio, case.cmp_indices.shape[-1] if case.ratio == 4 else 0, max_seq_len, ori_topk)
 
         ptr = lambda t: t.data_ptr() if t is not None else 0  # noqa: E731
         cmp = case.cmp if case.ratio != 1 else None
@@ -150,7 +152,7 @@ class PreparedAttention:
                              "use implementation='auto' with SHAREDKV_C8_DECODE=1")
         if not c8_attention.supported(self):
             raise ValueError("This ABI is outside the C8 path (needs 8 heads, ratio 1/4/128, window 128, "
-                             "block32 pages, no explicit original slots, top-k <= 1024)")
+                             "block32 pages, top-k <= 1024, at most 1024 explicit original slots)")
         prepared = c8_attention.prepare(self, scratch_allocator=scratch_allocator)
         self.__dict__.update(prepared.__dict__)
 

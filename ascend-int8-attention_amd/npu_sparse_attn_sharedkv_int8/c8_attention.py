@@ -54,9 +54,10 @@ def enabled():
     return value == "1"
 
 
-def max_tiles(ratio, topk, max_seq_len=None):
-    """Upper bound on a query's tile count (window tile + compressed tiles)."""
-    window_tiles = (WINDOW + TILE - 1) // TILE
+def max_tiles(ratio, topk, max_seq_len=None, ori_topk=0):
+    """Upper bound on a query's tile count (window or explicit-slot tiles +
+    compressed tiles)."""
+    window_tiles = (max(WINDOW, ori_topk) + TILE - 1) // TILE
     if ratio == 4:
         return window_tiles + (min(topk, MAX_TOPK) + TILE - 1) // TILE
     if ratio == 128:
@@ -66,25 +67,26 @@ def max_tiles(ratio, topk, max_seq_len=None):
     return window_tiles
 
 
-def choose_splits(tokens, ratio, topk, max_seq_len=None):
+def choose_splits(tokens, ratio, topk, max_seq_len=None, ori_topk=0):
     """KV partitions for a launch of `tokens` query rows (host-side plan)."""
     if tokens <= 0:
         return 1
     wanted = SPLITS_FEW_ROWS if tokens < FEW_ROWS else SPLITS_MANY_ROWS
     wanted = min(wanted, max(1, CORES // tokens))
-    return max(1, min(wanted, max_tiles(ratio, topk, max_seq_len), MAX_SPLITS))
+    return max(1, min(wanted, max_tiles(ratio, topk, max_seq_len, ori_topk), MAX_SPLITS))
 
 
 def supported(entry):
-    """C8 ABI: 8 heads, ratio 1/4/128, window 128, block32 pages, no explicit
-    original slots, top-k <= 1024 (reference c8_attention.py:56-71 requires
-    top-k == 1024 and ratio 4/128; the HIP kernel is general over both)."""
+    """C8 ABI: 8 heads, ratio 1/4/128, window 128, block32 pages, top-k <=
+    1024, at most 1024 explicit original slots (reference c8_attention.py:56-71
+    requires top-k == 1024, ratio 4/128 and no explicit slots, leaving the
+    rest to its legacy kernels; the HIP kernel covers them)."""
     if not getattr(entry, "blocks", 0) or getattr(entry, "args", None) is None:
         return False
     p = entry.args
     return (p.heads == HEADS and p.tokens > 0 and p.batch > 0 and p.ratio in (1, 4, 128)
             and p.window == WINDOW and p.oriBlock == BLOCK and (p.ratio == 1 or p.cmpBlock == BLOCK)
-            and not p.oriIndices and (p.ratio != 4 or 0 < p.topk <= MAX_TOPK)
+            and (not p.oriIndices or 0 < p.oriTopk <= MAX_TOPK) and (p.ratio != 4 or 0 < p.topk <= MAX_TOPK)
             and 1 <= p.splits <= MAX_SPLITS and p.oriStride % 16 == 0 and p.cmpStride % 16 == 0)
 
 

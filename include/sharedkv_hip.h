@@ -35,7 +35,10 @@ extern "C" {
  *   pages past it are masked), workspace (one uint32 merge ticket per query
  *   row, sharedkv_c8_workspace_bytes; zero before the first launch, and each
  *   launch leaves it zero, so launches that may overlap need their own).
- * oriIndices must be 0 (explicit original slots are not on this path). */
+ * oriIndices (INT32 [tokens][1][oriTopk], oriTopk <= 1024, or 0): explicit
+ * physical original slots (page = slot / 32, row = slot % 32, no table)
+ * replacing the window; entries outside [0, oriPages * 32) are masked in
+ * place (reference.py:236-239, sparse_gather.h:22-78). */
 typedef struct SharedKVArgs {
     uint64_t q, ori, cmp, oriScale, cmpScale, oriTable, cmpTable, indices;
     uint64_t cuQ, seqLens, sinks, out, workspace, lse;

@@ -134,6 +134,8 @@ class Case:
     softmax_scale: float = 1 / math.sqrt(DIM)
     block: int = 32
     extra: dict = field(default_factory=dict)
+    ori_indices: np.ndarray = None  # int32 [T, 1, K] physical original slots (reference.py:73)
+    ori_pages: int = 0              # pages of the original pool (slot capacity = pages * block)
 
 
 class _Case(ctypes.Structure):
@@ -147,6 +149,7 @@ class _Case(ctypes.Structure):
         ("sink", ctypes.c_void_p), ("ori_scale", ctypes.c_void_p), ("cmp_scale", ctypes.c_void_p),
         ("tokens", ctypes.c_int32), ("heads", ctypes.c_int32), ("block", ctypes.c_int32),
         ("ratio", ctypes.c_int32), ("window", ctypes.c_int32), ("softmax_scale", ctypes.c_float),
+        ("ori_slots", ctypes.c_void_p), ("ori_topk", ctypes.c_int32), ("ori_pages", ctypes.c_int32),
     ]
 
 
@@ -175,14 +178,18 @@ def tiled_attention(case, tile=128, splits=1, return_lse=True, joint_dense=False
                 cmp=_c(case.cmp, np.int8), ct=_c(case.cmp_table, np.int32),
                 ix=_c(case.cmp_indices, np.int32), cu=_c(case.cu_q, np.int32),
                 sl=_c(case.seq_lens, np.int32), sink=_c(case.sink, np.float32),
-                os=_c(case.ori_scale, np.float32), cs=_c(case.cmp_scale, np.float32))
+                os=_c(case.ori_scale, np.float32), cs=_c(case.cmp_scale, np.float32),
+                oi=_c(case.ori_indices, np.int32))
     topk = keep["ix"].shape[-1] if keep["ix"] is not None else 0
+    ori_topk = keep["oi"].shape[-1] if keep["oi"] is not None else 0
+    if keep["oi"] is not None and not case.ori_pages:
+        raise ValueError("explicit original slots need ori_pages")
     c = _Case(_ptr(q), _ptr(keep["ori"]), case.ori_stride, _ptr(keep["ot"]), keep["ot"].shape[1],
               _ptr(keep["cmp"]), case.cmp_stride, _ptr(keep["ct"]),
               keep["ct"].shape[1] if keep["ct"] is not None else 0, _ptr(keep["ix"]), topk,
               _ptr(keep["cu"]), _ptr(keep["sl"]), len(keep["sl"]), _ptr(keep["sink"]),
               _ptr(keep["os"]), _ptr(keep["cs"]), T, H, case.block, case.ratio, case.window,
-              case.softmax_scale)
+              case.softmax_scale, _ptr(keep["oi"]), ori_topk, case.ori_pages)
     plan = _Plan(tile, splits, int(joint_dense), int(joint_sparse), joint_tile_limit, int(dense_c4))
     out = np.zeros((T, H, DIM), dtype=np.uint16)
     lse = np.zeros((T, H), dtype=np.float32) if return_lse else None
@@ -234,6 +241,13 @@ def gather_rows(pool, stride, table, batch, indices, block=32):
     return pool[offsets[:, None] + np.arange(DIM)[None, :]]
 
 
+def gather_slots(pool, stride, slots, block=32):
+    """reference.py:88-90 on a flat byte pool: physical slots, no table."""
+    slots = np.asarray(slots, dtype=np.int64)
+    offsets = (slots // block) * stride + (slots % block) * DIM
+    return pool[offsets[:, None] + np.arange(DIM)[None, :]]
+
+
 def selected_rows(case):
     """reference.py:93-126: yields (token, original rows, compressed rows or None)."""
     for b in range(len(case.seq_lens)):
@@ -243,8 +257,14 @@ def selected_rows(case):
             raise ValueError("Query length cannot exceed sequence length")
         for t in range(begin, end):
             position = length - (end - begin) + (t - begin)
-            ori_idx = np.arange(max(0, position - case.window + 1), position + 1)
-            ori = gather_rows(case.ori, case.ori_stride, case.ori_table, b, ori_idx, case.block)
+            if case.ori_indices is None:
+                ori_idx = np.arange(max(0, position - case.window + 1), position + 1)
+                ori = gather_rows(case.ori, case.ori_stride, case.ori_table, b, ori_idx, case.block)
+            else:
+                # reference.py:112-115: valid physical slots, in order, no table.
+                slots = case.ori_indices[t, 0].astype(np.int64)
+                slots = slots[(slots >= 0) & (slots < case.ori_pages * case.block)]
+                ori = gather_slots(case.ori, case.ori_stride, slots, case.block)
             cmp = None
             if case.ratio != 1:
                 count = (position + 1) // case.ratio

@@ -160,11 +160,13 @@ int64_t sko_cache_write(int8_t *cache, int64_t pages, int64_t page_size, int64_t
 /* Attention                                                            */
 /* ------------------------------------------------------------------ */
 
-/* reference.py:82-85 gather: logical row -> physical page via the block table. */
+/* reference.py:82-85 gather: logical row -> physical page via the block
+ * table; without a table (reference.py:88-90 gather_slots) the index is a
+ * physical slot. */
 static const int8_t *row_address(const int8_t *cache, int64_t stride, const int32_t *table,
                                  int32_t width, int32_t block, int32_t batch, int64_t index)
 {
-    int64_t page = table[(int64_t)batch * width + index / block];
+    int64_t page = table ? table[(int64_t)batch * width + index / block] : index / block;
     return cache + page * stride + (index % block) * D;
 }
 
@@ -292,16 +294,24 @@ static void attend_token(const sko_case *c, const sko_plan *pl, int32_t b, int32
     kind_list lists[2];
     int kinds = 1;
 
-    /* Kind 0: SWA window, reference.py:232-234. */
+    /* Kind 0: SWA window, reference.py:232-234, or the explicit physical
+     * slots of reference.py:236-239 (every entry keeps its place; entries
+     * outside [0, pages * block) are holes). */
     int64_t first = position + 1 - c->window;
     if (first < 0) first = 0;
-    int32_t ori_count = (int32_t)(position + 1 - first);
-    lists[0] = (kind_list){c->ori, c->ori_stride, c->ori_table, c->ori_table_width, c->ori_scale,
-                           ori_count, malloc(sizeof(int64_t) * (ori_count ? ori_count : 1)),
+    int32_t ori_count = c->ori_slots ? c->ori_topk : (int32_t)(position + 1 - first);
+    lists[0] = (kind_list){c->ori, c->ori_stride, c->ori_slots ? NULL : c->ori_table, c->ori_table_width,
+                           c->ori_scale, ori_count, malloc(sizeof(int64_t) * (ori_count ? ori_count : 1)),
                            malloc(ori_count ? ori_count : 1), NULL};
     for (int32_t i = 0; i < ori_count; ++i) {
-        lists[0].index[i] = first + i;
-        lists[0].valid[i] = 1;
+        if (c->ori_slots) {
+            int64_t slot = c->ori_slots[(int64_t)t * c->ori_topk + i];
+            lists[0].index[i] = slot;
+            lists[0].valid[i] = slot >= 0 && slot < (int64_t)c->ori_pages * c->block;
+        } else {
+            lists[0].index[i] = first + i;
+            lists[0].valid[i] = 1;
+        }
     }
 
     /* Kind 1: compressed rows, reference.py:242-253. */
@@ -547,7 +557,8 @@ int sko_tiled_attention(const sko_case *c, const sko_plan *pl, uint16_t *out, fl
     if (pl->tile <= 0 || (pl->tile & (pl->tile - 1)) || pl->splits <= 0) return -3;
     if (c->ratio != 1 && (!c->cmp || !c->cmp_table || !c->cmp_scale)) return -4;
     if (c->ratio == 4 && (!c->cmp_indices || c->topk <= 0)) return -5;
-    if (dbg && c->window > 128) return -6;
+    if (dbg && (c->window > 128 || (c->ori_slots && c->ori_topk > 128))) return -6;
+    if (c->ori_slots && (c->ori_topk <= 0 || c->ori_pages <= 0)) return -9;
     int32_t total = c->cu_q[c->batch];
     if (total > c->tokens) return -7;
     /* Flatten (batch, token) pairs so OpenMP can split tokens evenly. */

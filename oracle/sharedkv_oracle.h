@@ -63,6 +63,12 @@ typedef struct {
     const float *cmp_scale;         /* [512] */
     int32_t tokens, heads, block, ratio, window;
     float softmax_scale;
+    /* reference.py:73 ori_indices: explicit physical original slots
+     * [tokens][1][ori_topk] (page = slot / block, row = slot % block, no
+     * block table) replacing the window; NULL for the window. */
+    const int32_t *ori_slots;
+    int32_t ori_topk;
+    int32_t ori_pages;              /* slots at or past ori_pages * block are holes */
 } sko_case;
 
 /* Tiling parameters of reference.py:210-212 that fix the numerics. */

@@ -43,11 +43,15 @@ def to_device(case, device="cuda"):
         cmp_scale = torch.from_numpy(case["cmp"].scale).to(device)
     if case["cmp_indices"] is not None:
         indices = torch.from_numpy(case["cmp_indices"]).to(device)
+    ori_indices = case.get("ori_indices")
+    if ori_indices is not None:
+        ori_indices = torch.from_numpy(ori_indices).to(device)
     dev = SharedKVCase(
         q=torch_bf16(case["q"], device), ori=ori, ori_block_table=torch.from_numpy(case["ori"].table).to(device),
         cu_q=torch.from_numpy(case["cu_q"]).to(device), seq_lens=torch.from_numpy(case["seq_lens"]).to(device),
         sink=torch.from_numpy(case["sink"]).to(device), cmp=cmp, cmp_block_table=cmp_table,
-        cmp_indices=indices, ratio=case["ratio"], window=case["window"], softmax_scale=case["softmax_scale"])
+        cmp_indices=indices, ratio=case["ratio"], window=case["window"], softmax_scale=case["softmax_scale"],
+        ori_indices=ori_indices)
     return dev, torch.from_numpy(case["ori"].scale).to(device), cmp_scale, keep
 
 
@@ -133,6 +137,8 @@ def query_subcase(case, rows):
         sub["cmp"] = _kind_rows(case["cmp"], batch)
     if case["cmp_indices"] is not None:
         sub["cmp_indices"] = np.ascontiguousarray(case["cmp_indices"][rows])
+    if case.get("ori_indices") is not None:
+        sub["ori_indices"] = np.ascontiguousarray(case["ori_indices"][rows])   # physical: no table
     return sub
 
 

@@ -90,6 +90,46 @@ def test_default_plan_matches_checker(name, seed, ratio, queries, lengths, mode)
     compare(case, out, lse, op.splits, tag=name)
 
 
+SLOT_CASES = [
+    # The reference's draft-slot shape (tests/npu/test_attention.py:37): window only,
+    # four requests of five draft tokens, 256 slots per token.
+    ("r1_draft", 51, 1, [5, 5, 5, 5], [8192, 700, 300, 4000], "draft", 256),
+    ("c4_draft", 52, 4, [3, 2], [9000, 2000], "draft", 256),
+    ("c128_shuffled", 53, 128, [2, 3], [5000, 900], "shuffled", 256),
+    ("r1_pool", 54, 1, [2, 1], [300, 90], "pool", 384),
+    # 8 slot tiles + 8 C4 tiles: with one partition, two chunks of row codes.
+    ("c4_pool_wide", 55, 4, [2], [20000], "pool", 1024),
+]
+
+
+@pytest.mark.parametrize("splits", [None, 1, 3])
+@pytest.mark.parametrize("name,seed,ratio,queries,lengths,slots,topk", SLOT_CASES, ids=[c[0] for c in SLOT_CASES])
+def test_explicit_original_slots_match_checker(name, seed, ratio, queries, lengths, slots, topk, splits):
+    """Explicit physical original slots (draft/MTP ori_indices,
+    reference.py:236-239, 285): holes masked in place, no block table."""
+    case = workloads.make_case(seed, ratio, queries, lengths, ori_slots=slots, ori_topk=topk)
+    say(f"[slots] {name} splits={splits}")
+    out, lse, op = run_hip(case, splits=splits)
+    compare(case, out, lse, op.splits, tag=name)
+
+
+@pytest.mark.parametrize("mode,ratio", [("window", 1), ("shuffled", 128), ("pool", 4)])
+def test_explicit_slot_partials_bit_exact(mode, ratio):
+    """Debug entry with one slot tile: Q codes, int32 QK partials, P codes
+    and int32 PV partials equal the checker's."""
+    case = workloads.make_case(56, ratio, [1, 1], [700, 3000], ori_slots=mode, ori_topk=128)
+    say(f"[slots debug] {mode} ratio={ratio}")
+    out, lse, dumps, op, (cap, tiles) = run_hip_debug(case, splits=2)
+    ref, ref_lse, rd = run_oracle(case, 2, debug=True, cmp_capacity=cap, tile_capacity=tiles)
+    used = kinds_with_rows(case)
+    for key in ("qcodes", "alpha"):
+        np.testing.assert_array_equal(dumps[key][used], rd[key][used], err_msg=key)
+    for key in ("scores", "probs", "values"):
+        np.testing.assert_array_equal(dumps[key], rd[key], err_msg=key)
+    assert (out == ref).all()
+    np.testing.assert_allclose(lse, ref_lse, rtol=0, atol=2e-6)
+
+
 def _golden(name):
     from pathlib import Path
     return np.load(Path(__file__).resolve().parent / "golden" / "vectors" / f"{name}.npz")

@@ -295,6 +295,59 @@ def test_integer_partials_by_brute_force(ratio, mode):
             np.testing.assert_array_equal(dbg["values"][t, number], p.T @ kv)
 
 
+@pytest.mark.parametrize("ratio", [1, 4, 128])
+def test_window_slots_reproduce_the_window_path(ratio):
+    """Explicit original slots (reference.py:236-239, 285) listing a query's
+    own window rows in window order, then -1, put the same rows in the same
+    tile places as the window path: identical bits."""
+    lengths = [300, 2000] if ratio != 1 else [90, 700]
+    plain = workloads.make_case(41, ratio, [3, 1], lengths)
+    slots = workloads.make_case(41, ratio, [3, 1], lengths, ori_slots="window", ori_topk=128)
+    assert slots["ori_indices"] is not None and (slots["ori_indices"] >= 0).sum() > 0
+    for splits in (1, 3):
+        a, la, _ = ora.tiled_attention(workloads.oracle_case(plain), splits=splits)
+        b, lb, _ = ora.tiled_attention(workloads.oracle_case(slots), splits=splits)
+        np.testing.assert_array_equal(a, b)
+        np.testing.assert_array_equal(la, lb)
+
+
+@pytest.mark.parametrize("ratio,mode", [(1, "draft"), (4, "draft"), (128, "shuffled"), (1, "shuffled")])
+def test_slot_path_close_to_fp64_attention(ratio, mode):
+    """Draft slots see the request's later rows too; shuffled slots carry
+    holes, slots past the pool and a repeated slot.  The integer path stays
+    within the reference's statistical gate of FP64 attention over the
+    valid slots in order (reference.py:112-115)."""
+    case = workloads.make_case(43, ratio, [4, 2], [600, 1500], ori_slots=mode, ori_topk=256)
+    c = workloads.oracle_case(case)
+    out, lse, _ = ora.tiled_attention(c, splits=2)
+    ref, ref_lse = ora.fp64_attention(c)
+    got = ora.bf16_to_f32(out).astype(np.float64)
+    assert np.linalg.norm(got - ref) / np.linalg.norm(ref) < 0.01
+    np.testing.assert_allclose(lse, ref_lse, rtol=2e-4, atol=2e-4)
+    if mode == "draft":
+        # Token 0 of request 0 sees rows up to the request's end: more than the window.
+        assert (case["ori_indices"][0, 0] >= 0).sum() == 600 - (596 + 1 - 128)
+
+
+def test_slot_integer_partials_by_brute_force():
+    """QK int32 partials of explicit slots equal the codes times the rows at
+    page = slot / 32, row = slot % 32 (no block table); holes score 0."""
+    case = workloads.make_case(47, 128, [1, 1], [700, 300], ori_slots="shuffled", ori_topk=128)
+    c = workloads.oracle_case(case)
+    out, lse, dbg = ora.tiled_attention(c, splits=1, debug=True)
+    kd = case["ori"]
+    for t in range(2):
+        qc = dbg["qcodes"][t, 0].astype(np.int64)
+        for j, slot in enumerate(case["ori_indices"][t, 0]):
+            s = dbg["scores"][t, j]
+            if 0 <= slot < kd.pages * 32:
+                row = ora.gather_slots(kd.pool, kd.page_stride, [slot])[0].astype(np.int64)
+                np.testing.assert_array_equal(s[:8], qc[:8] @ row)
+                np.testing.assert_array_equal(s[8:], qc[8:] @ row)
+            else:
+                assert not s.any()
+
+
 def test_subcase_rows_reproduce_full_case_rows():
     """query_subcase (used to check large GPU launches on a row sample) keeps
     each row's selection, so the checker gives identical bits."""

@@ -79,12 +79,23 @@ class Kind:
 
 
 def make_case(seed, ratio, queries, lengths, topk=1024, heads=8, window=128,
-              page_stride=BLOCK * DIM, index_mode="uniform", softmax_scale=1 / math.sqrt(DIM)):
+              page_stride=BLOCK * DIM, index_mode="uniform", softmax_scale=1 / math.sqrt(DIM),
+              ori_slots=None, ori_topk=256):
     """Returns (oracle-style dict, metadata).  index_mode for C4:
     'uniform'  top-k drawn without replacement from the visible range, sorted;
     'holes'    as uniform with every 7th entry -1 and every 11th out of range;
     'dups'     indices i // 2 (duplicates);
-    'mixed'    random with replacement plus -1 padding."""
+    'mixed'    random with replacement plus -1 padding.
+    ori_slots (explicit physical original slots, int32 [T, 1, ori_topk]):
+    'window'   the physical slots of the query's own window rows, then -1
+               (the same list, in the same places, as the window path);
+    'draft'    the slots of logical rows max(0, pos - 127) .. len - 1 of the
+               request, then -1 (tests/support/serving_shapes.py:96-105 of
+               the reference: a draft token sees the whole draft);
+    'shuffled' as 'draft', in a random order, with every 5th entry -1, every
+               13th past the pool and a few repeated slots;
+    'pool'     ori_topk slots drawn anywhere in the pool (physical slots need
+               not belong to the request), 10 % of them -1 or past the pool."""
     rng = np.random.default_rng(seed)
     batch = len(queries)
     cu = np.zeros(batch + 1, dtype=np.int32)
@@ -105,7 +116,7 @@ def make_case(seed, ratio, queries, lengths, topk=1024, heads=8, window=128,
     ori = Kind("ori", ori_needed, rng, page_stride, (int(seq.max()) + BLOCK - 1) // BLOCK)
 
     out = dict(q=q, ori=ori, cu_q=cu, seq_lens=seq, sink=sink, ratio=ratio, window=window,
-               softmax_scale=softmax_scale, cmp=None, cmp_indices=None, topk=0)
+               softmax_scale=softmax_scale, cmp=None, cmp_indices=None, topk=0, ori_indices=None)
     if ratio != 1:
         indices = None
         cmp_needed = [[] for _ in range(batch)]
@@ -136,6 +147,31 @@ def make_case(seed, ratio, queries, lengths, topk=1024, heads=8, window=128,
         width = (int(seq.max()) // ratio + BLOCK - 1) // BLOCK
         cmp = Kind("cmp", cmp_needed, rng, page_stride, width)
         out.update(cmp=cmp, cmp_indices=indices, topk=topk if ratio == 4 else 0)
+    if ori_slots is not None:
+        slots = np.full((tokens, 1, ori_topk), -1, dtype=np.int32)
+        capacity = ori.pages * BLOCK
+        for b, t, pos in positions:
+            if ori_slots == "pool":
+                row = rng.integers(0, capacity, ori_topk)
+                bad = rng.random(ori_topk) < 0.1
+                row[bad] = np.where(rng.random(int(bad.sum())) < 0.5, -1, capacity + 3)
+                slots[t, 0] = row
+                continue
+            last = pos if ori_slots == "window" else int(seq[b]) - 1
+            logical = np.arange(max(0, pos + 1 - window), last + 1)
+            row = ori.table[b, logical // BLOCK].astype(np.int64) * BLOCK + logical % BLOCK
+            if ori_slots == "shuffled":
+                row = rng.permutation(row)
+                if len(row) > 3:
+                    row[1] = row[3]                 # a repeated slot
+                row[::5] = -1
+                row[2::13] = capacity + 7           # past the pool
+            elif ori_slots not in ("window", "draft"):
+                raise ValueError(ori_slots)
+            if len(row) > ori_topk:
+                raise ValueError("ori_topk too small for the request")
+            slots[t, 0, :len(row)] = row
+        out["ori_indices"] = slots
     return out
 
 
@@ -149,7 +185,8 @@ def oracle_case(case):
                     cmp=cmp.pool if cmp else None, cmp_stride=cmp.page_stride if cmp else 0,
                     cmp_table=cmp.table if cmp else None, cmp_scale=cmp.scale if cmp else None,
                     cmp_indices=case["cmp_indices"], ratio=case["ratio"], window=case["window"],
-                    softmax_scale=case["softmax_scale"])
+                    softmax_scale=case["softmax_scale"], ori_indices=case.get("ori_indices"),
+                    ori_pages=case["ori"].pages)
 
 
 def fixture_case(z, i, seed=0, page_stride=BLOCK * DIM):
