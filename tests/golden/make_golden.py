@@ -40,6 +40,20 @@ CASES = [
      [(128, 1, 0, 0, 256), (64, 2, 0, 0, 256), (128, 1, 1, 0, 256)]),
     ("c4_dups", 4, 4, [1], [4400], "dups", 16384, [(128, 1, 0, 0, 256), (128, 3, 0, 0, 256)]),
 ]
+# Cases with other heads or explicit original slots:
+# (name, seed, ratio, queries, lengths, index mode, page stride, plans, heads, ori slot mode, slots per row)
+EXTRA = [
+    # More than eight heads: reference.py:221-222 turns the Q/P residuals off.
+    ("c128_heads16", 6, 128, [2, 1], [700, 2000], None, 16384, [(128, 1, 0, 0, 256), (128, 3, 0, 0, 256)],
+     16, None, 0),
+    ("c4_heads4", 7, 4, [1, 2], [3000, 1500], "uniform", 16384, [(128, 1, 0, 0, 256), (128, 2, 0, 0, 256)],
+     4, None, 0),
+    # Explicit physical original slots (reference.py:236-239, 285).
+    ("c1_slots_shuffled", 8, 1, [2, 1], [600, 300], None, 16384, [(128, 1, 0, 0, 256), (128, 2, 0, 0, 256)],
+     8, "shuffled", 256),
+    ("c4_slots_draft", 9, 4, [3], [5000], "uniform", 16384, [(128, 1, 0, 0, 256), (128, 3, 0, 0, 256)],
+     8, "draft", 256),
+]
 
 
 def torch_case(torch, ref, case):
@@ -54,7 +68,8 @@ def torch_case(torch, ref, case):
         sink=torch.from_numpy(case["sink"]),
         cmp=cache(cmp) if cmp else None, cmp_block_table=torch.from_numpy(cmp.table) if cmp else None,
         cmp_indices=torch.from_numpy(case["cmp_indices"]) if case["cmp_indices"] is not None else None,
-        ratio=case["ratio"], window=case["window"], softmax_scale=case["softmax_scale"])
+        ratio=case["ratio"], window=case["window"], softmax_scale=case["softmax_scale"],
+        ori_indices=torch.from_numpy(case["ori_indices"]) if case.get("ori_indices") is not None else None)
 
 
 def bits(t, torch):
@@ -65,6 +80,7 @@ def main():
     parser = argparse.ArgumentParser()
     parser.add_argument("--reference", default="/root/reference")
     parser.add_argument("--out", default=str(HERE / "vectors"))
+    parser.add_argument("--only", nargs="*", help="write only these cases")
     args = parser.parse_args()
     sys.path.insert(0, args.reference)
     import torch
@@ -74,9 +90,12 @@ def main():
     out_dir = Path(args.out)
     out_dir.mkdir(parents=True, exist_ok=True)
     meta = dict(cpu_capability=torch.backends.cpu.get_cpu_capability(), torch=torch.__version__)
-    for name, seed, ratio, queries, lengths, mode, stride, plans in CASES:
+    cases = [c + (8, None, 0) for c in CASES] + EXTRA
+    for name, seed, ratio, queries, lengths, mode, stride, plans, heads, slots, slot_count in cases:
+        if args.only and name not in args.only:
+            continue
         case = workloads.make_case(seed, ratio, queries, lengths, index_mode=mode or "uniform",
-                                   page_stride=stride)
+                                   page_stride=stride, heads=heads, ori_slots=slots, ori_topk=slot_count)
         tc = torch_case(torch, ref, case)
         oq = ref.CacheQuantization(torch.from_numpy(case["ori"].scale))
         cq = ref.CacheQuantization(torch.from_numpy(case["cmp"].scale)) if case["cmp"] else None
@@ -94,6 +113,8 @@ def main():
                           cmp_scale=case["cmp"].scale, cmp_inverse=cq.inverse_scale.numpy())
         if case["cmp_indices"] is not None:
             record["cmp_indices"] = case["cmp_indices"]
+        if case.get("ori_indices") is not None:
+            record.update(ori_indices=case["ori_indices"], ori_pages=case["ori"].pages)
         record["plans"] = np.asarray(plans, dtype=np.int32)
         for i, (tile, splits, jd, js, limit) in enumerate(plans):
             o, l = ref.tiled_quantized_reference(tc, oq, cq, tile_size=tile, splits=splits, return_lse=True,
@@ -109,6 +130,8 @@ def main():
         np.savez_compressed(out_dir / f"{name}.npz", **record)
         print(name, {k: v.shape for k, v in record.items() if hasattr(v, "shape") and k.startswith("out")})
 
+    if args.only:
+        return
     # joint_quantized_row on explicit rows, with and without a bias.
     rng = np.random.default_rng(11)
     q = workloads.bf16_bits(rng.standard_normal((8, 512), dtype=np.float32))

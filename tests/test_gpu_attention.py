@@ -136,7 +136,7 @@ def _golden(name):
 
 
 @pytest.mark.parametrize("splits", [None, 1, 2])
-@pytest.mark.parametrize("i", range(8))
+@pytest.mark.parametrize("i", range(11))
 def test_real_activations_match_checker(i, splits):
     """The reference's captured activations (tests/fixtures/activations) with
     the layer's frozen serving scales (data/scales_v1.pt), converted by

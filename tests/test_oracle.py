@@ -39,7 +39,9 @@ def golden_case(z):
                     cmp_table=z["cmp_table"] if has("cmp_table") else None,
                     cmp_scale=z["cmp_scale"] if has("cmp_scale") else None,
                     cmp_indices=z["cmp_indices"] if has("cmp_indices") else None,
-                    ratio=int(z["ratio"]), window=int(z["window"]), softmax_scale=float(z["softmax_scale"]))
+                    ratio=int(z["ratio"]), window=int(z["window"]), softmax_scale=float(z["softmax_scale"]),
+                    ori_indices=z["ori_indices"] if has("ori_indices") else None,
+                    ori_pages=int(z["ori_pages"]) if has("ori_pages") else 0)
 
 
 def bf16_ulps(a_bits, b_bits):
@@ -103,7 +105,7 @@ def test_fp64_attention_matches_reference_vectors(name):
 
 ACTIVATIONS = GOLDEN / "activations.npz"
 ACT_LAYERS = 11
-ACT_PATH_LAYERS = [0, 1, 2, 3, 4, 5, 6, 7]   # SWA128 + C4/C128 samples (the MTP samples use 133 explicit slots)
+ACT_PATH_LAYERS = list(range(ACT_LAYERS))    # SWA128 + C4/C128 samples, and MTP samples on 133 explicit slots
 
 
 def head_metrics(got, want):

@@ -196,11 +196,26 @@ def fixture_case(z, i, seed=0, page_stride=BLOCK * DIM):
     sequence of n = 508 tokens, so its SWA128 window is the fixture's 128
     original rows and its compressed list is the fixture's compressed rows
     (all (n // ratio) visible entries; the C4 top-k holds every one of them).
-    Rows are encoded with the layer's frozen serving scales."""
+    The MTP samples (ratio 1, 133 original rows) list their rows as explicit
+    physical original slots (the draft path's ori_indices), in the sample's
+    order, padded with -1 to 256.  Rows are encoded with the layer's frozen
+    serving scales."""
     ratio = int(z[f"{i}_ratio"])
     ori_bits, cmp_bits = z[f"{i}_ori"], z[f"{i}_cmp"]
     window = ori_bits.shape[0]
-    if window != 128 or ratio == 1:
+    if ratio == 1:
+        rng = np.random.default_rng(seed)
+        n = window
+        ori = Kind("ori", [range(n)], rng, page_stride, (n + BLOCK - 1) // BLOCK,
+                   rows={(0, r): ori_bits[r] for r in range(n)}, scale=z[f"{i}_ori_scale"])
+        logical = np.arange(n)
+        slots = np.full((1, 1, 256), -1, dtype=np.int32)
+        slots[0, 0, :n] = ori.table[0, logical // BLOCK] * BLOCK + logical % BLOCK
+        return dict(q=z[f"{i}_q"].reshape(1, 8, DIM), ori=ori, cu_q=np.array([0, 1], np.int32),
+                    seq_lens=np.array([n], np.int32), sink=z[f"{i}_sink"].astype(np.float32), ratio=1,
+                    window=128, softmax_scale=float(z[f"{i}_softmax_scale"]), cmp=None, cmp_indices=None,
+                    topk=0, ori_indices=slots)
+    if window != 128:
         raise ValueError("only the SWA128 + compressed samples map onto this path")
     length = 508
     count = length // ratio
