@@ -42,7 +42,8 @@
 namespace {
 
 constexpr int D = 512;
-constexpr int HEADS = 8;
+constexpr int HEADS = 8;               // heads per work-group (one MFMA row block with residual rows)
+constexpr int MAX_HEADS = 128;
 constexpr int N = SHAREDKV_C8_TILE;    // keys per tile
 constexpr int THREADS = 512;           // 8 waves: two per SIMD
 constexpr int WAVES = THREADS / 64;
@@ -282,7 +283,7 @@ __device__ __forceinline__ f32x4 state_load4(__amdgpu_buffer_rsrc_t r, int offse
 // clamped to partition 0 and their values ignored).
 template <int MAXS, int POLICY>
 __device__ __forceinline__ void fold_states(const __amdgpu_buffer_rsrc_t states, int S, int tid,
-                                            uint16_t *out_row, float *lse_row)
+                                            uint16_t *out_row, float *lse_row, int heads)
 {
     const int h = tid >> 6, col = (tid & 63) * 8;
     const int head_base = h * PART_FLOATS * 4;
@@ -322,19 +323,20 @@ __device__ __forceinline__ void fold_states(const __amdgpu_buffer_rsrc_t states,
     uint32_t w[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) w[e] = pack_bf16(acc[2 * e] / dsum, acc[2 * e + 1] / dsum);
+    if (heads < HEADS && h >= heads) return;   // padding heads of the last group of eight
     *reinterpret_cast<v4i *>(out_row + h * D + col) = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
     if (lse_row && (tid & 63) == 0) lse_row[h] = top + logf(dsum);
 }
 
 template <int POLICY>
 __device__ __forceinline__ void fold_row(const __amdgpu_buffer_rsrc_t states, int S, int tid, uint16_t *out_row,
-                                         float *lse_row)
+                                         float *lse_row, int heads = HEADS)
 {
-    if (S <= 2) fold_states<2, POLICY>(states, S, tid, out_row, lse_row);
-    else if (S == 3) fold_states<3, POLICY>(states, S, tid, out_row, lse_row);
-    else if (S == 4) fold_states<4, POLICY>(states, S, tid, out_row, lse_row);
-    else if (S <= 8) fold_states<8, POLICY>(states, S, tid, out_row, lse_row);
-    else fold_states<16, POLICY>(states, S, tid, out_row, lse_row);
+    if (S <= 2) fold_states<2, POLICY>(states, S, tid, out_row, lse_row, heads);
+    else if (S == 3) fold_states<3, POLICY>(states, S, tid, out_row, lse_row, heads);
+    else if (S == 4) fold_states<4, POLICY>(states, S, tid, out_row, lse_row, heads);
+    else if (S <= 8) fold_states<8, POLICY>(states, S, tid, out_row, lse_row, heads);
+    else fold_states<16, POLICY>(states, S, tid, out_row, lse_row, heads);
 }
 
 // SLOTS: the original kind is the explicit physical slot list of the row
@@ -342,7 +344,13 @@ __device__ __forceinline__ void fold_row(const __amdgpu_buffer_rsrc_t states, in
 // entry in its list place, entries outside [0, oriPages * 32) masked, in
 // ceil(oriTopk / 128) tiles; otherwise it is the SWA window through the
 // block table.
-template <int RATIO, bool DEBUG, bool SLOTS>
+// ANYH: p.heads is any of 1..128.  A work-group takes one group of eight
+// heads of a query row (rows of the launch = tokens x ceil(heads / 8));
+// heads past p.heads in the last group are computed on zero Q and never
+// written.  Above eight heads the Q and P residual codes are zero
+// (reference.py:221-222: residual quantization only for <= 8 heads), which
+// leaves every other operation as it is.  Without ANYH, heads == 8.
+template <int RATIO, bool DEBUG, bool SLOTS, bool ANYH>
 __global__ void __launch_bounds__(THREADS, 1)   // one work-group per CU: the 128 KiB tile ring fills the LDS
 c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uint32_t items, uint32_t fused)
 {
@@ -354,7 +362,13 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
     const uint32_t G = gridDim.x;
     const uint32_t item = (blockIdx.x & 7u) * (G >> 3) + (blockIdx.x >> 3);
     if (item >= items) return;
-    const int32_t t = (int32_t)(item / splits);
+    const int H = ANYH ? (int)p.heads : HEADS;                   // heads of a query token
+    const int HG = ANYH ? (H + HEADS - 1) / HEADS : 1;           // groups of eight
+    const bool resid = !ANYH || H <= HEADS;
+    const int32_t qrow = (int32_t)(item / splits);               // (token, head group)
+    const int32_t t = ANYH ? qrow / HG : qrow;
+    const int32_t hbase = ANYH ? HEADS * (qrow % HG) : 0;
+    const int hlive = ANYH ? (H - hbase < HEADS ? H - hbase : HEADS) : HEADS;
     const int32_t part = (int32_t)(item % splits);
     const int32_t S = (int32_t)splits;
 
@@ -371,7 +385,8 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
     }
     // Q row t: 8 heads x 512 BF16; thread = head (= wave), channels lane * 8.
     const int qd0 = lane * 8;
-    const v4i qv = *gptr<v4i>(p.q + (((uint64_t)t * HEADS + wave) * D + qd0) * 2);
+    v4i qv = {0, 0, 0, 0};
+    if (!ANYH || wave < hlive) qv = *gptr<v4i>(p.q + (((uint64_t)t * H + hbase + wave) * D + qd0) * 2);
     // Scales of both kinds into LDS (kind = tid / 256, 2 channels per thread).
     {
         const int kind = tid >> 8, c = (tid & 255) * 2;
@@ -388,7 +403,8 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
             if (tid * 2 + i < topk) ix[i] = row_ix[tid * 2 + i];
     }
     const __attribute__((address_space(1))) float *sinks = gptr<float>(p.sinks);
-    const float sink0 = sinks[2 * g], sink1 = sinks[2 * g + 1];
+    const float sink0 = (!ANYH || 2 * g < hlive) ? sinks[hbase + 2 * g] : 0.0f;
+    const float sink1 = (!ANYH || 2 * g + 1 < hlive) ? sinks[hbase + 2 * g + 1] : 0.0f;
 
     // ---- live shape (attention_impl.h:121-137) and the row's request ----
     if (tid == 0) { s.misc[0] = 0; s.misc[1] = -1; s.misc[2] = 0; }
@@ -419,17 +435,17 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
     const int end = live_batch ? uni(s.misc[2]) : 0;
     const int live_tokens = end <= 0 ? 0 : (end < (int)p.tokens ? end : (int)p.tokens);
     const int batch = uni(s.misc[1]);
-    uint16_t *out_row = reinterpret_cast<uint16_t *>(p.out) + (int64_t)t * HEADS * D;
-    float *lse_row = p.lse ? reinterpret_cast<float *>(p.lse) + (int64_t)t * HEADS : nullptr;
+    uint16_t *out_row = reinterpret_cast<uint16_t *>(p.out) + ((int64_t)t * H + hbase) * D;
+    float *lse_row = p.lse ? reinterpret_cast<float *>(p.lse) + (int64_t)t * H + hbase : nullptr;
     if (t >= live_tokens || batch < 0) {
         // Graph padding rows are zero-filled (attention_impl.h:443-460); with
         // a separate merge launch, partition 0 also marks the row
         // (denominator -1) so that launch leaves it alone.
         if (part == 0) {
-            reinterpret_cast<v4i *>(out_row)[tid] = v4i{0, 0, 0, 0};
-            if (lse_row && tid < HEADS) lse_row[tid] = 0.0f;
+            if (!ANYH || tid < hlive * (D / 8)) reinterpret_cast<v4i *>(out_row)[tid] = v4i{0, 0, 0, 0};
+            if (lse_row && tid < hlive) lse_row[tid] = 0.0f;
             if (S > 1 && !fused && tid == 0)
-                reinterpret_cast<float *>(p.partial)[(int64_t)t * S * HEADS * PART_FLOATS + FOLD_SLOT] = 0.0f;
+                reinterpret_cast<float *>(p.partial)[(int64_t)qrow * S * HEADS * PART_FLOATS + FOLD_SLOT] = 0.0f;
         }
         return;
     }
@@ -585,7 +601,7 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
             for (int e = 0; e < 8; ++e) {
                 const float x = clamp127(f[e] * inv);
                 const float hi = __builtin_rintf(x);
-                const float lo = __builtin_rintf((x - hi) * 127.0f);
+                const float lo = resid ? __builtin_rintf((x - hi) * 127.0f) : 0.0f;
                 hiw[e >> 2] |= ((uint32_t)(int32_t)hi & 0xffu) << (8 * (e & 3));
                 low[e >> 2] |= ((uint32_t)(int32_t)lo & 0xffu) << (8 * (e & 3));
             }
@@ -837,7 +853,7 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
                 const float w = sk_expf_nonpos(lg[hh] - mnew[hh]);
                 const float x = w * 127.0f;
                 const float ph = __builtin_rintf(x);
-                const float pl = __builtin_rintf((x - ph) * 127.0f);
+                const float pl = resid ? __builtin_rintf((x - ph) * 127.0f) : 0.0f;
                 s.p[row_of(2 * g + hh, 0) * PROW + key] = (int8_t)(int32_t)ph;
                 s.p[row_of(2 * g + hh, 1) * PROW + key] = (int8_t)(int32_t)pl;
                 if (DEBUG && dbg.probs && start + key < klen) {
@@ -920,17 +936,18 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
             const int h = 2 * g + hh;
+            if (ANYH && h >= hlive) continue;
 #pragma unroll
             for (int j = 0; j < 4; ++j) out_row[h * D + c0 + 16 * j + n] = (uint16_t)pack_bf16(num[hh][j] / den[hh], 0.0f);
             if (lse_row && wave == 0 && n == 0) lse_row[h] = mx[hh] + logf(den[hh]);
         }
         if (S > 1 && !fused && tid == 0)
-            reinterpret_cast<float *>(p.partial)[(int64_t)t * S * HEADS * PART_FLOATS + FOLD_SLOT] = 0.0f;
+            reinterpret_cast<float *>(p.partial)[(int64_t)qrow * S * HEADS * PART_FLOATS + FOLD_SLOT] = 0.0f;
         return;
     }
 
     // ---- publish this partition: [num 512, max, den] per head ----
-    float *row_partial = reinterpret_cast<float *>(p.partial) + (int64_t)t * S * HEADS * PART_FLOATS;
+    float *row_partial = reinterpret_cast<float *>(p.partial) + (int64_t)qrow * S * HEADS * PART_FLOATS;
     const __amdgpu_buffer_rsrc_t states = row_states(row_partial);
 #pragma unroll
     for (int hh = 0; hh < 2; ++hh) {
@@ -957,28 +974,32 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     uint32_t *tickets = reinterpret_cast<uint32_t *>(p.workspace);
-    if (tid == 0) s.misc[5] = (int)__hip_atomic_fetch_add(&tickets[t], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) s.misc[5] = (int)__hip_atomic_fetch_add(&tickets[qrow], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
     if (s.misc[5] != folded - 1) return;
-    if (tid == 0) __hip_atomic_store(&tickets[t], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) __hip_atomic_store(&tickets[qrow], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-    fold_row<SC1>(states, folded, tid, out_row, lse_row);
+    fold_row<SC1>(states, folded, tid, out_row, lse_row, ANYH ? hlive : HEADS);
 }
 
 // Partition merge as a second launch (merge mode 1): one 512-thread group
-// per query row, the same fold as the attention kernel's last partition,
-// over the partitions that partition 0 recorded.  Rows it marked 0 (graph
-// padding, or finalized in the attention launch) keep what it wrote.
+// per (query token, group of eight heads), the same fold as the attention
+// kernel's last partition, over the partitions that partition 0 recorded.
+// Rows it marked 0 (graph padding, or finalized in the attention launch)
+// keep what it wrote.
 __global__ void __launch_bounds__(THREADS)
 c8_merge(const SharedKVArgs p, uint32_t splits)
 {
-    const int t = blockIdx.x, S = (int)splits;
-    float *row_partial = reinterpret_cast<float *>(p.partial) + (int64_t)t * S * HEADS * PART_FLOATS;
+    const int qrow = blockIdx.x, S = (int)splits;
+    const int H = (int)p.heads, HG = (H + HEADS - 1) / HEADS;
+    const int t = qrow / HG, hbase = HEADS * (qrow % HG);
+    float *row_partial = reinterpret_cast<float *>(p.partial) + (int64_t)qrow * S * HEADS * PART_FLOATS;
     const int folded = (int)row_partial[FOLD_SLOT];
     if (folded < 2 || folded > S) return;
-    uint16_t *out_row = reinterpret_cast<uint16_t *>(p.out) + (int64_t)t * HEADS * D;
-    float *lse_row = p.lse ? reinterpret_cast<float *>(p.lse) + (int64_t)t * HEADS : nullptr;
-    fold_row<0>(row_states(row_partial), folded, threadIdx.x, out_row, lse_row);
+    uint16_t *out_row = reinterpret_cast<uint16_t *>(p.out) + ((int64_t)t * H + hbase) * D;
+    float *lse_row = p.lse ? reinterpret_cast<float *>(p.lse) + (int64_t)t * H + hbase : nullptr;
+    fold_row<0>(row_states(row_partial), folded, threadIdx.x, out_row, lse_row,
+                H - hbase < HEADS ? H - hbase : HEADS);
 }
 
 // ---- INT8 cache writer (cache_write.cpp:9-88): one wave per update row ----
@@ -1021,7 +1042,8 @@ cache_write(const CacheWriteArgs a)
 
 int check_attention(const SharedKVArgs *a)
 {
-    if (!a || a->heads != HEADS || (a->ratio != 1 && a->ratio != 4 && a->ratio != 128) || a->window != WINDOW)
+    if (!a || a->heads == 0 || a->heads > MAX_HEADS || (a->ratio != 1 && a->ratio != 4 && a->ratio != 128) ||
+        a->window != WINDOW)
         return 1;
     if (a->oriBlock != BLOCK_ROWS) return 1;
     // Explicit original slots: at most MAX_LIST per row; slot capacity
@@ -1046,6 +1068,28 @@ int check_attention(const SharedKVArgs *a)
 
 int g_merge_mode = 0;   // 0: fused (last partition folds), 1: separate merge launch
 
+uint32_t head_groups(uint32_t heads) { return (heads + HEADS - 1) / HEADS; }
+
+template <bool DEBUG, bool ANYH>
+void launch_variant(hipStream_t stream, const SharedKVArgs *a, const SharedKVDebug &dbg, bool slots, uint32_t grid,
+                    uint32_t splits, uint32_t items, uint32_t fused)
+{
+    const dim3 g(grid), b(THREADS);
+    if (slots) {
+        if (a->ratio == 4)
+            hipLaunchKernelGGL((c8_attention<4, DEBUG, true, ANYH>), g, b, 0, stream, *a, dbg, splits, items, fused);
+        else if (a->ratio == 128)
+            hipLaunchKernelGGL((c8_attention<128, DEBUG, true, ANYH>), g, b, 0, stream, *a, dbg, splits, items, fused);
+        else
+            hipLaunchKernelGGL((c8_attention<1, DEBUG, true, ANYH>), g, b, 0, stream, *a, dbg, splits, items, fused);
+    } else if (a->ratio == 4)
+        hipLaunchKernelGGL((c8_attention<4, DEBUG, false, ANYH>), g, b, 0, stream, *a, dbg, splits, items, fused);
+    else if (a->ratio == 128)
+        hipLaunchKernelGGL((c8_attention<128, DEBUG, false, ANYH>), g, b, 0, stream, *a, dbg, splits, items, fused);
+    else
+        hipLaunchKernelGGL((c8_attention<1, DEBUG, false, ANYH>), g, b, 0, stream, *a, dbg, splits, items, fused);
+}
+
 template <bool DEBUG>
 int launch_attention(hipStream_t stream, const SharedKVArgs *a, const SharedKVDebug *debug)
 {
@@ -1053,26 +1097,19 @@ int launch_attention(hipStream_t stream, const SharedKVArgs *a, const SharedKVDe
     if (a->tokens == 0) return (int)hipSuccess;
     const SharedKVDebug dbg = debug ? *debug : SharedKVDebug{0, 0, 0, 0, 0, 0, 0};
     const uint32_t splits = a->splits;
-    const uint32_t items = a->tokens * splits;
+    const uint32_t rows = a->tokens * head_groups(a->heads);
+    const uint32_t items = rows * splits;
     const uint32_t grid = (items + 7u) & ~7u;
     const uint32_t fused = splits > 1 && g_merge_mode == 0;
-    // Debug dumps hold one original tile (list places 0..127) per row.
-    if (DEBUG && a->oriIndices && a->oriTopk > N) return (int)hipErrorInvalidValue;
-    if (a->oriIndices) {
-        if (a->ratio == 4)
-            hipLaunchKernelGGL((c8_attention<4, DEBUG, true>), dim3(grid), dim3(THREADS), 0, stream, *a, dbg, splits, items, fused);
-        else if (a->ratio == 128)
-            hipLaunchKernelGGL((c8_attention<128, DEBUG, true>), dim3(grid), dim3(THREADS), 0, stream, *a, dbg, splits, items, fused);
-        else
-            hipLaunchKernelGGL((c8_attention<1, DEBUG, true>), dim3(grid), dim3(THREADS), 0, stream, *a, dbg, splits, items, fused);
-    } else if (a->ratio == 4)
-        hipLaunchKernelGGL((c8_attention<4, DEBUG, false>), dim3(grid), dim3(THREADS), 0, stream, *a, dbg, splits, items, fused);
-    else if (a->ratio == 128)
-        hipLaunchKernelGGL((c8_attention<128, DEBUG, false>), dim3(grid), dim3(THREADS), 0, stream, *a, dbg, splits, items, fused);
+    // Debug dumps hold eight heads and one original tile (list places 0..127) per row.
+    if (DEBUG && (a->heads != HEADS || (a->oriIndices && a->oriTopk > N))) return (int)hipErrorInvalidValue;
+    const bool slots = a->oriIndices != 0;
+    if (!DEBUG && a->heads != HEADS)
+        launch_variant<false, true>(stream, a, dbg, slots, grid, splits, items, fused);
     else
-        hipLaunchKernelGGL((c8_attention<1, DEBUG, false>), dim3(grid), dim3(THREADS), 0, stream, *a, dbg, splits, items, fused);
+        launch_variant<DEBUG, false>(stream, a, dbg, slots, grid, splits, items, fused);
     if (splits > 1 && !fused)
-        hipLaunchKernelGGL(c8_merge, dim3(a->tokens), dim3(THREADS), 0, stream, *a, splits);
+        hipLaunchKernelGGL(c8_merge, dim3(rows), dim3(THREADS), 0, stream, *a, splits);
     return (int)hipGetLastError();
 }
 
@@ -1126,15 +1163,15 @@ int launch_cache_write(uint32_t blocks, void *stream, const CacheWriteArgs *a)
     return (int)hipGetLastError();
 }
 
-uint64_t sharedkv_c8_workspace_bytes(uint32_t tokens, uint32_t splits)
+uint64_t sharedkv_c8_workspace_bytes(uint32_t rows, uint32_t splits)
 {
     (void)splits;
-    return ((uint64_t)tokens * 4 + 255) / 256 * 256;
+    return ((uint64_t)rows * 4 + 255) / 256 * 256;
 }
 
-uint64_t sharedkv_c8_partial_bytes(uint32_t tokens, uint32_t splits)
+uint64_t sharedkv_c8_partial_bytes(uint32_t rows, uint32_t splits)
 {
-    return splits > 1 ? (uint64_t)tokens * splits * HEADS * PART_FLOATS * 4 : 0;
+    return splits > 1 ? (uint64_t)rows * splits * HEADS * PART_FLOATS * 4 : 0;
 }
 
 int sharedkv_c8_set_merge_mode(int mode)

@@ -11,8 +11,10 @@ Everything is validated and every buffer is allocated here, outside graph
 capture; run() only launches the HIP kernel on the caller's current stream.
 The only kernel family in this build is the C8 one (c8_attention.py).  It
 also serves what the reference routes to its legacy Ascend variants for
-window-only (ratio 1) launches and explicit original slots (draft/MTP
-ori_indices); H != 8 is rejected with ValueError.
+window-only (ratio 1) launches, explicit original slots (draft/MTP
+ori_indices) and head counts other than eight (groups of eight heads per
+work-group; above eight heads the Q/P residuals are off, as in the
+reference's model).
 """
 import torch
 
@@ -127,7 +129,8 @@ class PreparedAttention:
             return
         ori_topk = case.ori_indices.shape[-1] if case.ori_indices is not None else 0
         self.splits = splits if splits is not None else c8_attention.choose_splits(
-            tokens, case.ratio, case.cmp_indices.shape[-1] if case.ratio == 4 else 0, max_seq_len, ori_topk)
+            tokens * c8_attention.head_groups(heads), case.ratio,
+            case.cmp_indices.shape[-1] if case.ratio == 4 else 0, max_seq_len, ori_topk)
 
         ptr = lambda t: t.data_ptr() if t is not None else 0  # noqa: E731
         cmp = case.cmp if case.ratio != 1 else None
@@ -145,13 +148,13 @@ class PreparedAttention:
             window=case.window, topk=case.cmp_indices.shape[-1] if case.ratio == 4 else 0, splits=self.splits,
             oriTopk=case.ori_indices.shape[-1] if case.ori_indices is not None else 0, oriPages=case.ori.shape[0],
             softmaxScale=case.softmax_scale)
-        self.blocks = tokens * self.splits
+        self.blocks = tokens * c8_attention.head_groups(heads) * self.splits
 
         if implementation == "fallback" or (implementation == "auto" and not c8_attention.enabled()):
             raise ValueError("The legacy (non-C8) kernels are not part of the MI355X build; "
                              "use implementation='auto' with SHAREDKV_C8_DECODE=1")
         if not c8_attention.supported(self):
-            raise ValueError("This ABI is outside the C8 path (needs 8 heads, ratio 1/4/128, window 128, "
+            raise ValueError("This ABI is outside the C8 path (needs ratio 1/4/128, window 128, "
                              "block32 pages, top-k <= 1024, at most 1024 explicit original slots)")
         prepared = c8_attention.prepare(self, scratch_allocator=scratch_allocator)
         self.__dict__.update(prepared.__dict__)

@@ -30,7 +30,8 @@ import torch
 from .runtime import native_launcher, library
 
 CORES = 256                # MI355X compute units
-HEADS = 8
+HEADS = 8                  # heads per work-group; a launch takes 1..MAX_HEADS in groups of eight
+MAX_HEADS = 128
 DIM = 512
 TILE = 128                 # keys per tile; matches SHAREDKV_C8_TILE in the C ABI
 MAX_SPLITS = 16
@@ -77,44 +78,53 @@ def choose_splits(tokens, ratio, topk, max_seq_len=None, ori_topk=0):
 
 
 def supported(entry):
-    """C8 ABI: 8 heads, ratio 1/4/128, window 128, block32 pages, top-k <=
-    1024, at most 1024 explicit original slots (reference c8_attention.py:56-71
-    requires top-k == 1024, ratio 4/128 and no explicit slots, leaving the
-    rest to its legacy kernels; the HIP kernel covers them)."""
+    """C8 ABI: 1..128 heads, ratio 1/4/128, window 128, block32 pages, top-k
+    <= 1024, at most 1024 explicit original slots (reference
+    c8_attention.py:56-71 requires 8 heads, top-k == 1024, ratio 4/128 and no
+    explicit slots, leaving the rest to its legacy kernels; the HIP kernel
+    covers them)."""
     if not getattr(entry, "blocks", 0) or getattr(entry, "args", None) is None:
         return False
     p = entry.args
-    return (p.heads == HEADS and p.tokens > 0 and p.batch > 0 and p.ratio in (1, 4, 128)
+    return (1 <= p.heads <= MAX_HEADS and p.tokens > 0 and p.batch > 0 and p.ratio in (1, 4, 128)
             and p.window == WINDOW and p.oriBlock == BLOCK and (p.ratio == 1 or p.cmpBlock == BLOCK)
             and (not p.oriIndices or 0 < p.oriTopk <= MAX_TOPK) and (p.ratio != 4 or 0 < p.topk <= MAX_TOPK)
             and 1 <= p.splits <= MAX_SPLITS and p.oriStride % 16 == 0 and p.cmpStride % 16 == 0)
 
 
-def workspace_bytes(tokens, splits):
-    return int(library().sharedkv_c8_workspace_bytes(tokens, splits))
+def head_groups(heads):
+    return (heads + HEADS - 1) // HEADS
 
 
-def partial_shape(tokens, splits):
-    return (tokens, splits, HEADS, PARTIAL_FLOATS) if splits > 1 else (0,)
+def workspace_bytes(rows, splits):
+    """rows = query tokens x head groups of eight."""
+    return int(library().sharedkv_c8_workspace_bytes(rows, splits))
+
+
+def partial_shape(rows, splits):
+    return (rows, splits, HEADS, PARTIAL_FLOATS) if splits > 1 else (0,)
 
 
 def prepare(entry, *, scratch_allocator=None, shared_storage=False):
     """Bind scratch and the launcher; returns a prepared copy of `entry`.
 
-    workspace: one uint32 merge ticket per query row (the last partition of a
-    row to finish folds the row).  It is zeroed here, and every launch leaves
-    it zero again, so a workspace must not be shared by launches that can run
+    A row is a query token's group of eight heads (tokens x ceil(heads / 8)
+    rows; one row per token at 8 heads).
+    workspace: one uint32 merge ticket per row (the last partition of a row
+    to finish folds the row).  It is zeroed here, and every launch leaves it
+    zero again, so a workspace must not be shared by launches that can run
     concurrently (separate streams get separate scratch through
     scratch_allocator's (name, stream) key).
-    partial: FP32 [tokens, splits, 8, 520] partition states (splits > 1).
+    partial: FP32 [rows, splits, 8, 520] partition states (splits > 1).
     """
     if getattr(entry, "c8_dynamic", False) or not supported(entry):
         return entry
     p = entry.args
     device = entry.case.q.device
     allocate = scratch_allocator or (lambda name, shape, dtype, dev: torch.empty(shape, dtype=dtype, device=dev))
-    need_ws = workspace_bytes(p.tokens, p.splits)
-    shape = partial_shape(p.tokens, p.splits)
+    rows = p.tokens * head_groups(p.heads)
+    need_ws = workspace_bytes(rows, p.splits)
+    shape = partial_shape(rows, p.splits)
     need_partial = 1
     for extent in shape:
         need_partial *= extent
@@ -135,7 +145,7 @@ def prepare(entry, *, scratch_allocator=None, shared_storage=False):
     out.args.workspace = workspace.data_ptr()
     out.args.partial = partial.data_ptr() if (partial is not None and p.splits > 1) else 0
     out.workspace, out.partial = workspace, partial
-    out.blocks = p.tokens * p.splits
+    out.blocks = rows * p.splits
     out.argument_address = ctypes.addressof(out.args)
     small = p.ratio == 4 and p.tokens < 24
     out.variant = VARIANT_SPARSE_SMALL if small else (VARIANT_SPARSE if p.ratio == 4 else VARIANT_DENSE)

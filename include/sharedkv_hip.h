@@ -25,16 +25,19 @@ extern "C" {
 
 /* Attention arguments (csrc/kernels/c8/args.h:7-14).  Strides are bytes
  * between pages; tables address pages.  Fields this implementation reads:
- *   q (BF16 [tokens][8][512]), ori/cmp (INT8 pages [*, 32, 1, 512]),
- *   oriScale/cmpScale (FP32 [512]), oriTable/cmpTable (INT32 [batch][width]),
- *   indices (INT32 [tokens][1][topk], ratio 4), cuQ (INT32 [batch+1]),
- *   seqLens (INT32 [batch]), sinks (FP32 [8]), out (BF16 [tokens][8][512]),
- *   lse (FP32 [tokens][8] or 0), partial (FP32 [tokens][splits][8][520]
- *   partition states when splits > 1, see sharedkv_c8_partial_bytes),
- *   splits (KV partitions), oriPages (pool size of the window cache; rows on
- *   pages past it are masked), workspace (one uint32 merge ticket per query
- *   row, sharedkv_c8_workspace_bytes; zero before the first launch, and each
- *   launch leaves it zero, so launches that may overlap need their own).
+ *   q (BF16 [tokens][heads][512], heads 1..128), ori/cmp (INT8 pages
+ *   [*, 32, 1, 512]), oriScale/cmpScale (FP32 [512]), oriTable/cmpTable
+ *   (INT32 [batch][width]), indices (INT32 [tokens][1][topk], ratio 4), cuQ
+ *   (INT32 [batch+1]), seqLens (INT32 [batch]), sinks (FP32 [heads]), out
+ *   (BF16 [tokens][heads][512]), lse (FP32 [tokens][heads] or 0), partial
+ *   (FP32 [rows][splits][8][520] partition states when splits > 1, see
+ *   sharedkv_c8_partial_bytes), splits (KV partitions), oriPages (pool size
+ *   of the window cache; rows on pages past it are masked), workspace (one
+ *   uint32 merge ticket per row, sharedkv_c8_workspace_bytes; zero before the
+ *   first launch, and each launch leaves it zero, so launches that may
+ *   overlap need their own).  A row is one query token's group of eight
+ *   heads: rows = tokens * ceil(heads / 8).  Above eight heads the Q and P
+ *   residual codes are off (reference.py:221-222).
  * oriIndices (INT32 [tokens][1][oriTopk], oriTopk <= 1024, or 0): explicit
  * physical original slots (page = slot / 32, row = slot % 32, no table)
  * replacing the window; entries outside [0, oriPages * 32) are masked in
@@ -96,9 +99,10 @@ int sharedkv_c8_attention_debug(void *stream, const SharedKVArgs *args, const Sh
  * accepted for ABI compatibility; 0 launches nothing. */
 int launch_cache_write(uint32_t blocks, void *stream, const CacheWriteArgs *args);
 
-/* Scratch sizes in bytes for a launch with `tokens` query rows. */
-uint64_t sharedkv_c8_workspace_bytes(uint32_t tokens, uint32_t splits);
-uint64_t sharedkv_c8_partial_bytes(uint32_t tokens, uint32_t splits);
+/* Scratch sizes in bytes for a launch with `rows` = tokens * ceil(heads / 8)
+ * rows (the query token count at eight heads). */
+uint64_t sharedkv_c8_workspace_bytes(uint32_t rows, uint32_t splits);
+uint64_t sharedkv_c8_partial_bytes(uint32_t rows, uint32_t splits);
 
 /* Partition merge placement for launches with splits > 1 (process-wide).
  * Mode 0 (default): fused; the last partition of a query row to finish

@@ -130,6 +130,42 @@ def test_explicit_slot_partials_bit_exact(mode, ratio):
     np.testing.assert_allclose(lse, ref_lse, rtol=0, atol=2e-6)
 
 
+HEAD_CASES = [
+    ("h1_c4", 61, 4, [2, 1], [3000, 900], 1, None),
+    ("h4_c128", 62, 128, [1, 2], [5000, 700], 4, None),
+    ("h12_r1", 63, 1, [3], [400], 12, None),
+    ("h16_c4", 64, 4, [2, 2], [9000, 3000], 16, None),
+    ("h24_c128_slots", 65, 128, [2], [2000], 24, "shuffled"),
+    ("h128_c4", 66, 4, [1], [6000], 128, None),
+]
+
+
+@pytest.mark.parametrize("splits", [None, 1, 3])
+@pytest.mark.parametrize("name,seed,ratio,queries,lengths,heads,slots", HEAD_CASES, ids=[c[0] for c in HEAD_CASES])
+def test_head_counts_match_checker(name, seed, ratio, queries, lengths, heads, slots, splits):
+    """1..128 heads in groups of eight per work-group; above eight heads
+    without Q/P residuals (reference.py:221-222)."""
+    case = workloads.make_case(seed, ratio, queries, lengths, heads=heads, ori_slots=slots, ori_topk=256)
+    say(f"[heads] {name} splits={splits}")
+    out, lse, op = run_hip(case, splits=splits)
+    compare(case, out, lse, op.splits, tag=name)
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+def test_head_groups_with_both_merge_placements(mode):
+    from npu_sparse_attn_sharedkv_int8.runtime import library
+    lib = library()
+    try:
+        assert lib.sharedkv_c8_set_merge_mode(mode) == 0
+        case = workloads.make_case(67, 4, [2, 3], [4000, 2500], heads=20, index_mode="mixed")
+        for splits in (2, 5):
+            say(f"[heads merge mode {mode}] splits={splits}")
+            out, lse, op = run_hip(case, splits=splits)
+            compare(case, out, lse, splits, tag=f"heads 20 mode {mode} splits {splits}")
+    finally:
+        lib.sharedkv_c8_set_merge_mode(0)
+
+
 def _golden(name):
     from pathlib import Path
     return np.load(Path(__file__).resolve().parent / "golden" / "vectors" / f"{name}.npz")
@@ -156,7 +192,8 @@ def test_real_activations_match_checker(i, splits):
     assert rel < 0.04 and cos > 0.999, (rel, cos)
 
 
-@pytest.mark.parametrize("name", ["c128_ctx4096", "c4_raw_holes", "c4_compact_mixed", "c128_mixed", "c4_dups"])
+@pytest.mark.parametrize("name", ["c128_ctx4096", "c4_raw_holes", "c4_compact_mixed", "c128_mixed", "c4_dups",
+                                  "c128_heads16", "c4_heads4", "c1_slots_shuffled", "c4_slots_draft"])
 def test_against_reference_vectors(name):
     """HIP output vs reference.py's own tiled_quantized_reference output with a
     128-key plan: BASELINE tolerance (max-abs 2e-2, mean-abs 2e-3) and, where
@@ -172,17 +209,20 @@ def test_against_reference_vectors(name):
         q=torch.from_numpy(z["q"].view(np.int16)).to(dev).view(torch.bfloat16),
         ori=pool("ori_pool", int(z["ori_stride"])), ori_block_table=torch.from_numpy(z["ori_table"]).to(dev),
         cu_q=torch.from_numpy(z["cu_q"]).to(dev), seq_lens=torch.from_numpy(z["seq_lens"]).to(dev),
-        sink=torch.from_numpy(z["sink"]).to(dev), cmp=pool("cmp_pool", int(z["cmp_stride"])),
-        cmp_block_table=torch.from_numpy(z["cmp_table"]).to(dev),
+        sink=torch.from_numpy(z["sink"]).to(dev),
+        cmp=pool("cmp_pool", int(z["cmp_stride"])) if ratio != 1 else None,
+        cmp_block_table=torch.from_numpy(z["cmp_table"]).to(dev) if ratio != 1 else None,
         cmp_indices=torch.from_numpy(z["cmp_indices"]).to(dev) if "cmp_indices" in z.files else None,
-        ratio=ratio, window=int(z["window"]), softmax_scale=float(z["softmax_scale"]))
+        ratio=ratio, window=int(z["window"]), softmax_scale=float(z["softmax_scale"]),
+        ori_indices=torch.from_numpy(z["ori_indices"]).to(dev) if "ori_indices" in z.files else None)
     plans = [tuple(int(v) for v in p) for p in z["plans"]]
     for i, (tile, splits, jd, js, _) in enumerate(plans):
         if tile != 128 or jd or js:
             continue
         say(f"[reference vectors] {name} plan {i} splits={splits}")
         op = PreparedAttention(case, torch.from_numpy(z["ori_scale"]).to(dev),
-                               torch.from_numpy(z["cmp_scale"]).to(dev), splits=splits, return_lse=True)
+                               torch.from_numpy(z["cmp_scale"]).to(dev) if ratio != 1 else None, splits=splits,
+                               return_lse=True)
         op.run()
         torch.cuda.synchronize()
         got = bits_of(op.out)
@@ -244,8 +284,8 @@ def test_baseline_configs(index):
         torch.cuda.empty_cache()
 
 
-@pytest.mark.parametrize("mode", [0, 1])
-def test_padded_graph_rows_are_zero_and_guards_hold(mode):
+@pytest.mark.parametrize("mode,heads", [(0, 8), (1, 8), (0, 12), (1, 12)])
+def test_padded_graph_rows_are_zero_and_guards_hold(mode, heads):
     """Capacity rows past the live tokens (seq_len 0 / cu_q sentinel) are
     zero-filled; bytes around the output and LSE are untouched; with either
     merge placement (the separate merge launch must leave padded rows and
@@ -255,26 +295,26 @@ def test_padded_graph_rows_are_zero_and_guards_hold(mode):
     from npu_sparse_attn_sharedkv_int8.runtime import library
     assert library().sharedkv_c8_set_merge_mode(mode) == 0
     try:
-        _padded_rows_case()
+        _padded_rows_case(heads)
     finally:
         library().sharedkv_c8_set_merge_mode(0)
 
 
-def _padded_rows_case():
+def _padded_rows_case(heads=8):
     import torch
     from npu_sparse_attn_sharedkv_int8 import PreparedAttention
-    case = workloads.make_case(21, 4, [2, 1, 0, 0], [3000, 700, 0, 0], index_mode="mixed")
+    case = workloads.make_case(21, 4, [2, 1, 0, 0], [3000, 700, 0, 0], index_mode="mixed", heads=heads)
     live = int(case["cu_q"][-1])
     # Capacity of 6 query rows: append 3 NaN-poisoned padding rows.
-    q = np.concatenate([case["q"], np.full((3, 8, 512), 0x7FC0, np.uint16)])
+    q = np.concatenate([case["q"], np.full((3, heads, 512), 0x7FC0, np.uint16)])
     padded = dict(case, q=q, cmp_indices=np.concatenate([case["cmp_indices"],
                                                         np.full((3, 1, 1024), -1, np.int32)]))
     padded["cu_q"] = np.array([0, 2, 3, 6, 6], np.int32)      # graph pads a synthetic request
     padded["seq_lens"] = np.array([3000, 700, 0, 0], np.int32)
     dev, oscale, cscale, keep = to_device(padded)
-    guard_out = torch.full((6 + 2, 8, 512), 123, dtype=torch.bfloat16, device="cuda")
-    guard_lse = torch.full((6 + 2, 8), 123, dtype=torch.float32, device="cuda")
-    say("[padding] capacity 6, live 3")
+    guard_out = torch.full((6 + 2, heads, 512), 123, dtype=torch.bfloat16, device="cuda")
+    guard_lse = torch.full((6 + 2, heads), 123, dtype=torch.float32, device="cuda")
+    say(f"[padding] capacity 6, live 3, heads {heads}")
     op = PreparedAttention(dev, oscale, cscale, output=guard_out[1:-1], lse_output=guard_lse[1:-1], splits=4)
     op.run()
     torch.cuda.synchronize()
