@@ -387,12 +387,11 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
     const int qd0 = lane * 8;
     v4i qv = {0, 0, 0, 0};
     if (!ANYH || wave < hlive) qv = *gptr<v4i>(p.q + (((uint64_t)t * H + hbase + wave) * D + qd0) * 2);
-    // Scales of both kinds into LDS (kind = tid / 256, 2 channels per thread).
-    {
-        const int kind = tid >> 8, c = (tid & 255) * 2;
-        const uint64_t base = (kind && RATIO != 1) ? p.cmpScale : p.oriScale;
-        *reinterpret_cast<f32x2 *>(&s.scale[kind][c]) = *gptr<f32x2>(base + (uint64_t)c * 4);
-    }
+    // Scales of both kinds (kind = tid / 256, 2 channels per thread); they
+    // go to LDS once every prologue load has been issued, so no load below
+    // waits behind this one.
+    const f32x2 scale_pair = *gptr<f32x2>(((tid >> 8) && RATIO != 1 ? p.cmpScale : p.oriScale) +
+                                          (uint64_t)((tid & 255) * 2) * 4);
     // C4 index entries 2 tid, 2 tid + 1 of row t.
     int ix[2] = {-1, -1};
     if (RATIO == 4) {
@@ -432,6 +431,7 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
     // compiler's own wait tracking does not hold back the block-table reads
     // issued next for these registers.
     __builtin_amdgcn_s_waitcnt(0x0F70);
+    *reinterpret_cast<f32x2 *>(&s.scale[tid >> 8][(tid & 255) * 2]) = scale_pair;   // read after later barriers
     const int end = live_batch ? uni(s.misc[2]) : 0;
     const int live_tokens = end <= 0 ? 0 : (end < (int)p.tokens ? end : (int)p.tokens);
     const int batch = uni(s.misc[1]);
@@ -492,22 +492,21 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
     if (RATIO == 4) {
         const int topk = (int)p.topk;
         const bool compact = m.count < topk && topk <= MAX_LIST;   // reference.py:250
-        int ok[2], mine = 0;
+        bool ok[2];
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            ok[i] = ix[i] >= 0 && ix[i] < m.count;
-            mine += ok[i];
-        }
+        for (int i = 0; i < 2; ++i) ok[i] = ix[i] >= 0 && ix[i] < m.count;
         if (compact) {
-            int incl = mine;
-#pragma unroll
-            for (int o = 1; o < 64; o <<= 1) {
-                const int y = __shfl_up(incl, o);
-                if (lane >= o) incl += y;
-            }
-            if (lane == 63) s.scan[wave] = incl;
+            // Entry 2 tid + i goes to place (valid entries of lower lanes and
+            // waves) + (entry 0 of this lane, for i = 1): two ballots, counted
+            // below the lane with mbcnt.
+            const uint64_t v0 = __ballot(ok[0]), v1 = __ballot(ok[1]);
+            const int below = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(v0 >> 32),
+                                                             __builtin_amdgcn_mbcnt_lo((uint32_t)v0, 0u)) +
+                              (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(v1 >> 32),
+                                                             __builtin_amdgcn_mbcnt_lo((uint32_t)v1, 0u));
+            if (lane == 0) s.scan[wave] = __popcll(v0) + __popcll(v1);
             lds_barrier();                    // no fence: the table reads stay in flight
-            int at = incl - mine, total = 0;
+            int at = below, total = 0;
 #pragma unroll
             for (int w = 0; w < WAVES; ++w) {
                 at += w < wave ? s.scan[w] : 0;
@@ -574,17 +573,23 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
     const int c0 = 64 * wave;       // this wave's 64 PV output columns: c0 + 16 j + n
 
     // Q folding and residual split for both kinds (reference.py:274-279),
-    // done once while the block-table reads of the first chunk are in
-    // flight.  Thread = head `wave`, channels qd0 .. qd0 + 7.  Codes are
-    // staged in tile buffer 1 (before any tile lands there) and picked up
-    // in the MFMA A layout.
+    // done once while the first tile's rows are in flight.  Thread = head
+    // `wave`, channels qd0 .. qd0 + 7.  Codes are staged in tile buffer 1
+    // (before any tile is requested into it) and picked up in the MFMA A
+    // layout.
     v4i qa0[8], qa1[8];   // Q codes per 64-byte D block, window / compressed kind
+    // Its inputs pass through opaque copies, so the compiler computes the
+    // encode where it is called instead of ahead of the row codes.
     auto encode_q = [&](bool want0, bool want1) {
-        const uint32_t qw[4] = {(uint32_t)qv.x, (uint32_t)qv.y, (uint32_t)qv.z, (uint32_t)qv.w};
+        v4i qx = qv;
+        int lx = lane;
+        asm volatile("" : "+v"(qx), "+v"(lx));
+        const int qe0 = lx * 8, ne = lx & 15, ge = lx >> 4;
+        const uint32_t qw[4] = {(uint32_t)qx.x, (uint32_t)qx.y, (uint32_t)qx.z, (uint32_t)qx.w};
 #pragma unroll
         for (int kind = 0; kind < 2; ++kind) {
             if (!(kind ? want1 : want0)) continue;
-            const float *scale = s.scale[kind] + qd0;
+            const float *scale = s.scale[kind] + qe0;
             float f[8];
             float amax = 0.0f;
 #pragma unroll
@@ -606,14 +611,14 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
                 low[e >> 2] |= ((uint32_t)(int32_t)lo & 0xffu) << (8 * (e & 3));
             }
             int8_t *stage = s.tile[1] + kind * 16 * QSTAGE;
-            *reinterpret_cast<u32x2 *>(stage + row_of(wave, 0) * QSTAGE + qd0) = u32x2{hiw[0], hiw[1]};
-            *reinterpret_cast<u32x2 *>(stage + row_of(wave, 1) * QSTAGE + qd0) = u32x2{low[0], low[1]};
+            *reinterpret_cast<u32x2 *>(stage + row_of(wave, 0) * QSTAGE + qe0) = u32x2{hiw[0], hiw[1]};
+            *reinterpret_cast<u32x2 *>(stage + row_of(wave, 1) * QSTAGE + qe0) = u32x2{low[0], low[1]};
             if (lane == 0) s.asc[kind][wave] = alpha * p.softmaxScale;
             if (DEBUG) {
                 if (dbg.qcodes) {
                     int8_t *qc = reinterpret_cast<int8_t *>(dbg.qcodes) + (((int64_t)t * 2 + kind) * 16) * D;
-                    *reinterpret_cast<u32x2 *>(qc + wave * D + qd0) = u32x2{hiw[0], hiw[1]};
-                    *reinterpret_cast<u32x2 *>(qc + (8 + wave) * D + qd0) = u32x2{low[0], low[1]};
+                    *reinterpret_cast<u32x2 *>(qc + wave * D + qe0) = u32x2{hiw[0], hiw[1]};
+                    *reinterpret_cast<u32x2 *>(qc + (8 + wave) * D + qe0) = u32x2{low[0], low[1]};
                 }
                 if (dbg.alpha && lane == 0)
                     reinterpret_cast<float *>(dbg.alpha)[((int64_t)t * 2 + kind) * 8 + wave] = alpha;
@@ -623,8 +628,8 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
         const int8_t *st0 = s.tile[1], *st1 = s.tile[1] + 16 * QSTAGE;
 #pragma unroll
         for (int jj = 0; jj < 8; ++jj) {
-            qa0[jj] = want0 ? *reinterpret_cast<const v4i *>(st0 + n * QSTAGE + 64 * jj + 16 * g) : v4i{0, 0, 0, 0};
-            qa1[jj] = want1 ? *reinterpret_cast<const v4i *>(st1 + n * QSTAGE + 64 * jj + 16 * g) : v4i{0, 0, 0, 0};
+            qa0[jj] = want0 ? *reinterpret_cast<const v4i *>(st0 + ne * QSTAGE + 64 * jj + 16 * ge) : v4i{0, 0, 0, 0};
+            qa1[jj] = want1 ? *reinterpret_cast<const v4i *>(st1 + ne * QSTAGE + 64 * jj + 16 * ge) : v4i{0, 0, 0, 0};
         }
     };
 
@@ -720,24 +725,7 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
                 cslot[e] = i * N + ipos[e] % N;
             }
         }
-        if (first == 0) {
-            bool want0 = false, want1 = false;
-            for (int i = 0; i < my_tiles; ++i) {
-                const bool kind1 = part + S * i >= m.t0;
-                want0 |= !kind1;
-                want1 |= kind1;
-            }
-            encode_q(want0, want1);       // its barrier also orders the -1 fill before the writes below
-        } else {
-            lds_barrier();
-        }
-        // The table values are first touched here, after the Q encode: keep
-        // the compiler from hoisting their uses (and the wait for the reads)
-        // above it.
-#pragma unroll
-        for (int e = 0; e < PER; ++e) asm volatile("" : "+v"(tpage[e]));
-#pragma unroll
-        for (int e = 0; e < 2; ++e) asm volatile("" : "+v"(cpage_raw[e]));
+        lds_barrier();                    // the -1 fill is complete before the writes below
 #pragma unroll
         for (int e = 0; e < PER; ++e) {
             if (tidx[e] < 0) continue;
@@ -766,10 +754,30 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
                     s.addr[cslot[e]] = p.cmp + (uint64_t)cpage_raw[e] * p.cmpStride + (uint64_t)((ix[e] % BLOCK_ROWS) * D);
                 }
         }
-        __syncthreads();   // codes visible; staged Q codes consumed
+        lds_barrier();                    // codes visible
 
+        // Tile 0's rows are requested first; the Q encode (staged in tile
+        // buffer 1) and the tile loop's per-lane set-up run while they are in
+        // flight, then tile 1 follows into the freed buffer.
         issue_tile(0, 0);
+        if (first == 0) {
+            bool want0 = false, want1 = false;
+            for (int i = 0; i < my_tiles; ++i) {
+                const bool kind1 = part + S * i >= m.t0;
+                want0 |= !kind1;
+                want1 |= kind1;
+            }
+            encode_q(want0, want1);
+            lds_barrier();                // every wave holds its Q codes: buffer 1 is free
+        }
         if (ntiles > 1) issue_tile(1, 1);
+
+        // The tile loop's per-lane LDS addresses derive from an opaque copy
+        // of the lane index, so they are computed here, while the first rows
+        // are in flight, rather than ahead of the row codes.
+        int lane_x = lane;
+        asm volatile("" : "+v"(lane_x));
+        const int gx = lane_x >> 4, nx = lane_x & 15;
 
         for (int i = 0; i < ntiles; ++i) {
             const int k = part + S * (first + i);
@@ -784,7 +792,7 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
             const bool stream_next = i >= 1 && i + 1 < ntiles;   // tiles 0 and 1 were issued up front
             if (stream_next) issue_rows(i + 1, buf ^ 1, 0, DMA_STEP);
             const int8_t *tb = s.tile[buf];
-            const int key = 16 * wave + n;   // this lane's key in QK and softmax
+            const int key = 16 * wave + nx;   // this lane's key in QK and softmax
 
             // ---- QK: S[16 rows][16 keys of this wave] (reference.py:286-289) ----
             v4i sacc = {0, 0, 0, 0};
@@ -792,7 +800,7 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
                 const int sl = slot_of(key);
                 v4i b[8];
 #pragma unroll
-                for (int j = 0; j < 8; ++j) b[j] = *reinterpret_cast<const v4i *>(tb + tile_offset(sl, 4 * j + g));
+                for (int j = 0; j < 8; ++j) b[j] = *reinterpret_cast<const v4i *>(tb + tile_offset(sl, 4 * j + gx));
                 if (kind) {
 #pragma unroll
                     for (int j = 0; j < 8; ++j) sacc = __builtin_amdgcn_mfma_i32_16x16x64_i8(qa1[j], b[j], sacc, 0, 0, 0);
@@ -805,8 +813,8 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
             if (held) epilogue();            // the previous tile's, behind this tile's QK
             const bool valid = s.code[i * N + key] >= 0;
             float asc[2];
-            asc[0] = s.asc[kind][2 * g];
-            asc[1] = s.asc[kind][2 * g + 1];
+            asc[0] = s.asc[kind][2 * gx];
+            asc[1] = s.asc[kind][2 * gx + 1];
 
             // ---- logits, running max (reference.py:288-303) ----
             float lg[2];
@@ -820,18 +828,18 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
                 if (DEBUG && dbg.scores && start + key < klen) {
                     // masked rows are zero rows in the reference (reference.py:283-286)
                     int32_t *drow = reinterpret_cast<int32_t *>(dbg.scores) + ((int64_t)t * positions + (kind ? 128 : 0) + start + key) * 16;
-                    drow[2 * g + hh] = valid ? hi : 0;
-                    drow[8 + 2 * g + hh] = valid ? lo : 0;
+                    drow[2 * gx + hh] = valid ? hi : 0;
+                    drow[8 + 2 * gx + hh] = valid ? lo : 0;
                 }
                 const int tmax = row16_max_key(fkey(lg[hh]));
-                if (n == 0) s.redmax[2 * g + hh][wave] = tmax;
+                if (nx == 0) s.redmax[2 * gx + hh][wave] = tmax;
             }
             lds_barrier();
             if (stream_next) issue_rows(i + 1, buf ^ 1, 2 * DMA_STEP, DMA_STEP);
             float mnew[2], factor[2];
 #pragma unroll
             for (int hh = 0; hh < 2; ++hh) {
-                const int h = 2 * g + hh;
+                const int h = 2 * gx + hh;
                 const v4i a = *reinterpret_cast<const v4i *>(&s.redmax[h][0]);
                 const v4i b = *reinterpret_cast<const v4i *>(&s.redmax[h][4]);
                 const int k = max(max(max(fkey(mx[hh]), a.x), max(a.y, a.z)), max(max(a.w, b.x), max(max(b.y, b.z), b.w)));
@@ -841,7 +849,7 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
                 // One exponential per lane: even lanes take head 2g, odd lanes
                 // head 2g+1; each lane gets the other head's factor from its
                 // neighbour.
-                const bool odd = n & 1;
+                const bool odd = nx & 1;
                 const float mine = sk_expf_nonpos(odd ? mx[1] - mnew[1] : mx[0] - mnew[0]);
                 const float other = dpp<DPP_XOR1>(mine);
                 factor[0] = odd ? other : mine;
@@ -854,22 +862,22 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
                 const float x = w * 127.0f;
                 const float ph = __builtin_rintf(x);
                 const float pl = resid ? __builtin_rintf((x - ph) * 127.0f) : 0.0f;
-                s.p[row_of(2 * g + hh, 0) * PROW + key] = (int8_t)(int32_t)ph;
-                s.p[row_of(2 * g + hh, 1) * PROW + key] = (int8_t)(int32_t)pl;
+                s.p[row_of(2 * gx + hh, 0) * PROW + key] = (int8_t)(int32_t)ph;
+                s.p[row_of(2 * gx + hh, 1) * PROW + key] = (int8_t)(int32_t)pl;
                 if (DEBUG && dbg.probs && start + key < klen) {
                     int8_t *drow = reinterpret_cast<int8_t *>(dbg.probs) + ((int64_t)t * positions + (kind ? 128 : 0) + start + key) * 16;
-                    drow[2 * g + hh] = (int8_t)(int32_t)ph;
-                    drow[8 + 2 * g + hh] = (int8_t)(int32_t)pl;
+                    drow[2 * gx + hh] = (int8_t)(int32_t)ph;
+                    drow[8 + 2 * gx + hh] = (int8_t)(int32_t)pl;
                 }
                 const float wsum = row16_tree_sum(w);   // this wave's 16 keys
-                if (n == 0) s.redsum[2 * g + hh][wave] = wsum;
+                if (nx == 0) s.redsum[2 * gx + hh][wave] = wsum;
             }
             lds_barrier();
             if (stream_next) issue_rows(i + 1, buf ^ 1, 3 * DMA_STEP, DMA_STEP);
 #pragma unroll
             for (int hh = 0; hh < 2; ++hh) {
                 // Pairwise over the eight 16-key blocks.
-                const int h = 2 * g + hh;
+                const int h = 2 * gx + hh;
                 const f32x4 a = *reinterpret_cast<const f32x4 *>(&s.redsum[h][0]);
                 const f32x4 b = *reinterpret_cast<const f32x4 *>(&s.redsum[h][4]);
                 const float tile_sum = ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w));
@@ -883,18 +891,18 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
             const lds_i8 *vbase = (const lds_i8 *)(tb);   // generic -> LDS address space
 #pragma unroll
             for (int kb = 0; kb < 2; ++kb) {
-                // A: P row n, keys 64 kb + 16 g .. + 15.  B: two transposed
+                // A: P row nx, keys 64 kb + 16 gx .. + 15.  B: two transposed
                 // 8-key reads; lanes 2r / 2r+1 address the two 8-column halves
-                // of key row r, lane n receives column n of the 16-column block.
-                const v4i pa = *reinterpret_cast<const v4i *>(s.p + n * PROW + 64 * kb + 16 * g);
-                const int sl_lo = slot_of(64 * kb + 16 * g + (n >> 1));
-                const int sl_hi = slot_of(64 * kb + 16 * g + 8 + (n >> 1));
+                // of key row r, lane nx receives column nx of the 16-column block.
+                const v4i pa = *reinterpret_cast<const v4i *>(s.p + nx * PROW + 64 * kb + 16 * gx);
+                const int sl_lo = slot_of(64 * kb + 16 * gx + (nx >> 1));
+                const int sl_hi = slot_of(64 * kb + 16 * gx + 8 + (nx >> 1));
                 v2i b0[4], b1[4];
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const int chunk = 4 * wave + j;
-                    b0[j] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i *)(vbase + tile_offset(sl_lo, chunk) + 8 * (n & 1)));
-                    b1[j] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i *)(vbase + tile_offset(sl_hi, chunk) + 8 * (n & 1)));
+                    b0[j] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i *)(vbase + tile_offset(sl_lo, chunk) + 8 * (nx & 1)));
+                    b1[j] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i *)(vbase + tile_offset(sl_hi, chunk) + 8 * (nx & 1)));
                 }
                 __builtin_amdgcn_sched_barrier(0);   // all reads in flight before the first MFMA waits
 #pragma unroll
@@ -909,8 +917,8 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
                 for (int j = 0; j < 4; ++j)
 #pragma unroll
                     for (int hh = 0; hh < 2; ++hh) {
-                        vout[(2 * g + hh) * D + c0 + 16 * j + n] = vacc[j][2 * hh];
-                        vout[(8 + 2 * g + hh) * D + c0 + 16 * j + n] = vacc[j][2 * hh + 1];
+                        vout[(2 * gx + hh) * D + c0 + 16 * j + nx] = vacc[j][2 * hh];
+                        vout[(8 + 2 * gx + hh) * D + c0 + 16 * j + nx] = vacc[j][2 * hh + 1];
                     }
             }
             // The FP32 epilogue of this tile runs in the next tile's body,
@@ -919,7 +927,7 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 held_acc[j] = vacc[j];
-                held_sc[j] = s.scale[kind][c0 + 16 * j + n];
+                held_sc[j] = s.scale[kind][c0 + 16 * j + nx];
             }
             held_factor[0] = factor[0];
             held_factor[1] = factor[1];
