@@ -377,12 +377,10 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
     const __attribute__((address_space(1))) int32_t *lens = gptr<int32_t>(p.seqLens);
     const int batch_n = (int)p.batch;
     // Request b's (cu[b], cu[b+1], len[b]) for b = tid (more in the loops below).
-    int my_cu0 = 0, my_cu1 = -1, my_len = 0;
-    if (tid < batch_n) {
-        my_cu0 = cu[tid];
-        my_cu1 = cu[tid + 1];
-        my_len = lens[tid];
-    }
+    // Unconditional (threads past the batch read request 0 and ignore it),
+    // so the wait for these three loads leaves the later ones in flight.
+    const int mine_b = tid < batch_n ? tid : 0;
+    const int my_cu0 = cu[mine_b], my_cu1 = cu[mine_b + 1], my_len = lens[mine_b];
     // Q row t: 8 heads x 512 BF16; thread = head (= wave), channels lane * 8.
     const int qd0 = lane * 8;
     v4i qv = {0, 0, 0, 0};
