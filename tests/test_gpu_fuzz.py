@@ -1,0 +1,77 @@
+"""Seeded random launches against the CPU checker: mixed ratios, head counts,
+explicit original slots, C4 index modes, graph-capacity padding rows, KV
+partitions and both merge placements, all bit-exact (BF16 outputs) with the
+checker on the launch's own plan and LSE within 2e-6."""
+import sys
+
+import numpy as np
+import pytest
+
+from tests import workloads
+from tests.device_cases import run_hip, run_oracle
+
+pytestmark = pytest.mark.gpu
+
+CASES = 48
+
+
+def say(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def random_case(seed):
+    rng = np.random.default_rng(1000 + seed)
+    ratio = int(rng.choice([1, 4, 128]))
+    batch = int(rng.integers(1, 6))
+    queries = [int(q) for q in rng.integers(1, 5, batch)]
+    lengths = [int(max(q, rng.integers(1, 9000))) for q in queries]
+    heads = int(rng.choice([8, 8, 8, 4, 12, 16]))
+    mode = str(rng.choice(["uniform", "holes", "dups", "mixed"]))
+    slots = rng.random() < 0.25
+    slot_mode = str(rng.choice(["draft", "shuffled", "pool"])) if slots else None
+    splits = rng.choice([None, 1, 2, 3, 5])
+    merge = int(rng.integers(0, 2))
+    topk = int(rng.choice([1024, 512, 256]))
+    need = max(q + 128 for q in queries) if slot_mode in ("draft", "shuffled") else 0
+    ori_topk = 256 if need <= 256 else 384
+    case = workloads.make_case(seed, ratio, queries, lengths, topk=topk, heads=heads, index_mode=mode,
+                               ori_slots=slot_mode, ori_topk=ori_topk)
+    pad = int(rng.integers(1, 4)) if rng.random() < 0.3 else 0
+    if pad:
+        # Graph capacity: a synthetic request of `pad` NaN query rows with
+        # seq_len 0 after the live ones (zero-filled by the kernel).
+        live = int(case["cu_q"][-1])
+        case["q"] = np.concatenate([case["q"], np.full((pad, heads, 512), 0x7FC0, np.uint16)])
+        case["cu_q"] = np.concatenate([case["cu_q"], [live + pad]]).astype(np.int32)
+        case["seq_lens"] = np.concatenate([case["seq_lens"], [0]]).astype(np.int32)
+        case["ori"].table = np.concatenate([case["ori"].table, case["ori"].table[:1]])
+        if case["cmp"] is not None:
+            case["cmp"].table = np.concatenate([case["cmp"].table, case["cmp"].table[:1]])
+        for key in ("cmp_indices", "ori_indices"):
+            if case.get(key) is not None:
+                filler = np.full((pad,) + case[key].shape[1:], -1, np.int32)
+                case[key] = np.concatenate([case[key], filler])
+    return case, (None if splits is None else int(splits)), merge, dict(
+        ratio=ratio, queries=queries, lengths=lengths, heads=heads, mode=mode, slots=slot_mode, topk=topk,
+        pad=pad)
+
+
+@pytest.mark.parametrize("seed", range(CASES))
+def test_random_launch_matches_checker(seed):
+    from npu_sparse_attn_sharedkv_int8.runtime import library
+    case, splits, merge, desc = random_case(seed)
+    say(f"[fuzz {seed}] splits={splits} merge={merge} {desc}")
+    lib = library()
+    try:
+        assert lib.sharedkv_c8_set_merge_mode(merge) == 0
+        out, lse, op = run_hip(case, splits=splits)
+    finally:
+        lib.sharedkv_c8_set_merge_mode(0)
+    live = int(case["cu_q"][-1]) - desc["pad"]
+    if desc["pad"]:
+        assert not out[live:].any() and not lse[live:].any(), "padding rows are not zero"
+        case = dict(case, q=case["q"][:live], cu_q=case["cu_q"][:-1], seq_lens=case["seq_lens"][:-1])
+    ref, ref_lse, _ = run_oracle(case, op.splits)
+    diff = out[:live] != ref[:live]
+    assert not diff.any(), f"seed {seed}: {int(diff.sum())} BF16 mismatches of {diff.size}"
+    np.testing.assert_allclose(lse[:live], ref_lse[:live], rtol=0, atol=2e-6)
