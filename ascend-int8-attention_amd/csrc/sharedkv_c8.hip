@@ -112,7 +112,10 @@ __device__ __forceinline__ float sk_expf_nonpos(float x)
     p = __builtin_fmaf(p, r, 0.5f);
     p = __builtin_fmaf(p, r, 1.0f);
     p = __builtin_fmaf(p, r, 1.0f);
-    const float e = __builtin_ldexpf(p, (int)n);
+    float e = __builtin_ldexpf(p, (int)n);
+    // Keeps the series unconditional: without it the compiler turns the
+    // select below back into a branch around the series.
+    asm volatile("" : "+v"(e));
     return in_range ? e : (x != x ? x : 0.0f);
 }
 
