@@ -10,15 +10,18 @@
 //   cache writer    csrc/kernels/cache_write.cpp:9-88
 //
 // Design (one GPU, HBM bound).  One work-group of 8 waves (two per SIMD) per
-// (query row, KV partition), one work-group per CU; partition `part` owns
-// tiles part, part + S, ... of the row's key list (window rows, then
-// compressed rows, cut into 128-key tiles).
+// (query row, KV partition), one work-group per CU; a query row is one token
+// and eight of its heads (tokens with more heads take several rows).
+// Partition `part` owns tiles part, part + S, ... of the row's key list
+// (window rows or explicit original slots, then compressed rows, cut into
+// 128-key tiles).
 //   prologue   every independent load of the row (metadata, indices, Q, both
 //              scale vectors) is issued at once: one memory round trip
 //   addresses  the partition's rows become page codes (page * 32 + row in
-//              page, -1 = masked) in LDS: one round trip of block-table
-//              reads per chunk of tiles, during which Q is encoded for both
-//              cache kinds
+//              page, -1 = masked) and HBM addresses in LDS after one round
+//              trip of block-table reads (issued before the C4 compaction
+//              scan); the first tile is requested at once, and Q is encoded
+//              for both cache kinds while its rows are in flight
 //   tiles      rows go from HBM straight into a two-tile LDS ring by LDS DMA
 //              (whole 512-byte rows per instruction); the next tile is in
 //              flight while the current one is computed.  QK: each wave takes
