@@ -394,6 +394,16 @@ def test_splits_variants_match_checker():
         compare(case, out, lse, splits, tag=f"splits {splits}")
 
 
+def test_long_c128_rows_span_two_code_chunks():
+    """C128 rows longer than twelve tiles per partition (ctx 300000: 2343
+    compressed rows, 20 tiles) rebuild their row codes in a second chunk."""
+    case = workloads.make_case(29, 128, [1, 2], [300000, 180000])
+    for splits in (1, 2, 3):
+        say(f"[long c128] splits={splits}")
+        out, lse, op = run_hip(case, splits=splits)
+        compare(case, out, lse, splits, tag=f"long c128 splits {splits}")
+
+
 def test_empty_launch_is_a_no_op():
     import torch
     from npu_sparse_attn_sharedkv_int8 import PreparedAttention
