@@ -27,7 +27,9 @@ import os
 
 import torch
 
-from .runtime import native_launcher, library
+from types import SimpleNamespace
+
+from .runtime import SharedKVArgs, native_launcher, library
 
 CORES = 256                # MI355X compute units
 HEADS = 8                  # heads per work-group; a launch takes 1..MAX_HEADS in groups of eight
@@ -44,6 +46,13 @@ FEW_ROWS = 8
 PARTIAL_FLOATS = 520       # per (token, partition, head): 512 numerator, max, denominator, pad
 
 VARIANT_SPARSE, VARIANT_DENSE, VARIANT_SPARSE_SMALL = 20, 21, 22
+
+# A workspace of this size serves any launch of up to WORKSPACE_ROWS rows (one
+# uint32 merge ticket per row), for callers that size one shared workspace up
+# front as the reference's constant allows (c8_attention.py:27-30 there);
+# prepare() itself sizes each launch exactly (workspace_bytes).
+WORKSPACE_ROWS = 1 << 16
+WORKSPACE_BYTES = WORKSPACE_ROWS * 4
 
 
 def enabled():
@@ -90,6 +99,25 @@ def supported(entry):
             and p.window == WINDOW and p.oriBlock == BLOCK and (p.ratio == 1 or p.cmpBlock == BLOCK)
             and (not p.oriIndices or 0 < p.oriTopk <= MAX_TOPK) and (p.ratio != 4 or 0 < p.topk <= MAX_TOPK)
             and 1 <= p.splits <= MAX_SPLITS and p.oriStride % 16 == 0 and p.cmpStride % 16 == 0)
+
+
+def argument_type():
+    """The ctypes argument block (reference c8_attention.py:40-43)."""
+    return SharedKVArgs
+
+
+def host_module():
+    """The launcher object over the C ABI (the reference loads a pybind
+    module here, c8_attention.py:123-129)."""
+    return native_launcher()
+
+
+def native_host(queued=False):
+    """Launch entry of the C8 kernels (reference c8_attention.py:132-138);
+    queued and direct launches are the same HIP launch here."""
+    host = native_launcher()
+    return SimpleNamespace(attention=host.attention_queued if queued else host.attention,
+                           attention_args_size=host.attention_args_size, _owner=host)
 
 
 def head_groups(heads):

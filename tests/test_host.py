@@ -49,6 +49,19 @@ def test_argument_blocks_match_reference_layout():
     assert c.slotColumnStride.offset == 56 and c.tokens.offset == 64 and c.pairedSlots.offset == 80
 
 
+def test_module_helpers_match_reference_names():
+    """c8_attention exposes the reference module's helper names
+    (c8_attention.py:27-46,123-138 there) over the C ABI."""
+    lib = runtime.library()
+    assert c8_attention.argument_type() is runtime.SharedKVArgs
+    assert c8_attention.library() is lib
+    assert c8_attention.WORKSPACE_BYTES >= lib.sharedkv_c8_workspace_bytes(c8_attention.WORKSPACE_ROWS, 16)
+    for queued in (False, True):
+        host = c8_attention.native_host(queued)
+        assert host.attention_args_size == ctypes.sizeof(runtime.SharedKVArgs)
+        assert host._owner is c8_attention.host_module() and callable(host.attention)
+
+
 def test_scratch_sizes():
     lib = runtime.library()
     assert lib.sharedkv_c8_partial_bytes(64, 1) == 0
