@@ -1052,6 +1052,8 @@ cache_write(const CacheWriteArgs a)
     *reinterpret_cast<u32x2 *>(dst) = u32x2{packed[0], packed[1]};
 }
 
+uint32_t head_groups(uint32_t heads) { return (heads + HEADS - 1) / HEADS; }
+
 int check_attention(const SharedKVArgs *a)
 {
     if (!a || a->heads == 0 || a->heads > MAX_HEADS || (a->ratio != 1 && a->ratio != 4 && a->ratio != 128) ||
@@ -1072,6 +1074,8 @@ int check_attention(const SharedKVArgs *a)
     }
     if (a->ratio == 4 && (!a->indices || a->topk == 0 || a->topk > MAX_LIST)) return 1;
     if (a->splits == 0 || a->splits > MAX_SPLITS) return 1;
+    // Work-groups of the launch (rows x splits, rounded up to 8) fit the grid.
+    if ((uint64_t)a->tokens * head_groups(a->heads) * a->splits > 0x7ffffff8ull) return 1;
     if (a->splits > 1 && (!a->partial || !a->workspace)) return 1;
     if (a->oriStride % 16 || a->oriStride < BLOCK_ROWS * D) return 1;
     if ((a->q | a->ori | a->out | a->oriScale) & 15) return 1;
@@ -1079,8 +1083,6 @@ int check_attention(const SharedKVArgs *a)
 }
 
 int g_merge_mode = 0;   // 0: fused (last partition folds), 1: separate merge launch
-
-uint32_t head_groups(uint32_t heads) { return (heads + HEADS - 1) / HEADS; }
 
 template <bool DEBUG, bool ANYH>
 void launch_variant(hipStream_t stream, const SharedKVArgs *a, const SharedKVDebug &dbg, bool slots, uint32_t grid,

@@ -85,6 +85,20 @@ def test_launchers_reject_bad_blocks_without_a_device():
     assert lib.sharedkv_c8_set_merge_mode(0) == 0
 
 
+@pytest.mark.skipif(torch.cuda.is_available(), reason="placeholder addresses: host-side check only")
+def test_launch_rejects_grids_past_the_limit():
+    """tokens x ceil(heads / 8) x splits work-groups must fit one grid; a
+    launch past it is rejected before any HIP call."""
+    lib = runtime.library()
+    a = runtime.SharedKVArgs()
+    for name in ("q", "ori", "oriScale", "oriTable", "cuQ", "seqLens", "sinks", "out", "cmp", "cmpScale",
+                 "cmpTable", "indices", "partial", "workspace"):
+        setattr(a, name, 0x10000)
+    a.heads, a.ratio, a.window, a.oriBlock, a.cmpBlock, a.batch, a.oriPages = 128, 4, 128, 32, 32, 1, 1
+    a.topk, a.oriStride, a.cmpStride, a.tokens, a.splits = 1024, 16384, 16384, 1 << 23, 16
+    assert lib.launch_sharedkv_c8_sparse(1, None, ctypes.byref(a)) == 1
+
+
 def test_host_plan():
     assert c8_attention.max_tiles(4, 1024) == 9
     assert c8_attention.max_tiles(128, 0, 4096) == 2
