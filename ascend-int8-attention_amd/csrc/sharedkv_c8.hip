@@ -15,8 +15,10 @@
 // Partition `part` owns tiles part, part + S, ... of the row's key list
 // (window rows or explicit original slots, then compressed rows, cut into
 // 128-key tiles).
-//   prologue   every independent load of the row (metadata, indices, Q, both
-//              scale vectors) is issued at once: one memory round trip
+//   prologue   every load of the row that the selection needs (metadata,
+//              indices, Q) is issued at once from kernel arguments that the
+//              build preloads into SGPRs: one memory round trip, with the
+//              argument block read alongside; sinks and scales follow
 //   addresses  the partition's rows become page codes (page * 32 + row in
 //              page, -1 = masked) and HBM addresses in LDS after one round
 //              trip of block-table reads (issued before the C4 compaction
@@ -358,17 +360,20 @@ __device__ __forceinline__ void fold_row(const __amdgpu_buffer_rsrc_t states, in
 // leaves every other operation as it is.  Without ANYH, heads == 8.
 template <int RATIO, bool DEBUG, bool SLOTS, bool ANYH>
 __global__ void __launch_bounds__(THREADS, 1)   // one work-group per CU: the 128 KiB tile ring fills the LDS
-c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uint32_t items, uint32_t fused)
+c8_attention(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, const uint64_t cmp_indices,
+             const uint32_t batch_arg, const uint32_t topk_arg, const uint32_t heads_arg, const uint32_t splits,
+             const uint32_t items, const uint32_t grid, const SharedKVArgs p, const SharedKVDebug dbg,
+             const uint32_t fused)
 {
     __shared__ Shared s;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, n = lane & 15;
 
     // XCD-aware order: consecutive work items (the partitions of one row,
     // then the next row) stay on one XCD and share its L2.
-    const uint32_t G = gridDim.x;
+    const uint32_t G = grid;
     const uint32_t item = (blockIdx.x & 7u) * (G >> 3) + (blockIdx.x >> 3);
     if (item >= items) return;
-    const int H = ANYH ? (int)p.heads : HEADS;                   // heads of a query token
+    const int H = ANYH ? (int)heads_arg : HEADS;                 // heads of a query token
     const int HG = ANYH ? (H + HEADS - 1) / HEADS : 1;           // groups of eight
     const bool resid = !ANYH || H <= HEADS;
     const int32_t qrow = (int32_t)(item / splits);               // (token, head group)
@@ -378,10 +383,13 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
     const int32_t part = (int32_t)(item % splits);
     const int32_t S = (int32_t)splits;
 
-    // ---- prologue: every load that depends only on t, issued together ----
-    const __attribute__((address_space(1))) int32_t *cu = gptr<int32_t>(p.cuQ);
-    const __attribute__((address_space(1))) int32_t *lens = gptr<int32_t>(p.seqLens);
-    const int batch_n = (int)p.batch;
+    // ---- prologue: the loads the selection needs, issued together ----
+    // cu_q, seq_lens, q_base, cmp_indices, batch_arg, topk_arg, heads_arg,
+    // splits, items and grid are the leading kernel arguments (copies of
+    // argument-block fields) that arrive preloaded in SGPRs.
+    const __attribute__((address_space(1))) int32_t *cu = gptr<int32_t>(cu_q);
+    const __attribute__((address_space(1))) int32_t *lens = gptr<int32_t>(seq_lens);
+    const int batch_n = (int)batch_arg;
     // Request b's (cu[b], cu[b+1], len[b]) for b = tid (more in the loops below).
     // Unconditional (threads past the batch read request 0 and ignore it),
     // so the wait for these three loads leaves the later ones in flight.
@@ -390,24 +398,16 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
     // Q row t: 8 heads x 512 BF16; thread = head (= wave), channels lane * 8.
     const int qd0 = lane * 8;
     v4i qv = {0, 0, 0, 0};
-    if (!ANYH || wave < hlive) qv = *gptr<v4i>(p.q + (((uint64_t)t * H + hbase + wave) * D + qd0) * 2);
-    // Scales of both kinds (kind = tid / 256, 2 channels per thread); they
-    // go to LDS once every prologue load has been issued, so no load below
-    // waits behind this one.
-    const f32x2 scale_pair = *gptr<f32x2>(((tid >> 8) && RATIO != 1 ? p.cmpScale : p.oriScale) +
-                                          (uint64_t)((tid & 255) * 2) * 4);
+    if (!ANYH || wave < hlive) qv = *gptr<v4i>(q_base + (((uint64_t)t * H + hbase + wave) * D + qd0) * 2);
     // C4 index entries 2 tid, 2 tid + 1 of row t.
     int ix[2] = {-1, -1};
     if (RATIO == 4) {
-        const int topk = (int)p.topk;
-        const __attribute__((address_space(1))) int32_t *row_ix = gptr<int32_t>(p.indices) + (int64_t)t * topk;
+        const int topk = (int)topk_arg;
+        const __attribute__((address_space(1))) int32_t *row_ix = gptr<int32_t>(cmp_indices) + (int64_t)t * topk;
 #pragma unroll
         for (int i = 0; i < 2; ++i)
             if (tid * 2 + i < topk) ix[i] = row_ix[tid * 2 + i];
     }
-    const __attribute__((address_space(1))) float *sinks = gptr<float>(p.sinks);
-    const float sink0 = (!ANYH || 2 * g < hlive) ? sinks[hbase + 2 * g] : 0.0f;
-    const float sink1 = (!ANYH || 2 * g + 1 < hlive) ? sinks[hbase + 2 * g + 1] : 0.0f;
 
     // ---- live shape (attention_impl.h:121-137) and the row's request ----
     if (tid == 0) { s.misc[0] = 0; s.misc[1] = -1; s.misc[2] = 0; }
@@ -435,7 +435,6 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
     // compiler's own wait tracking does not hold back the block-table reads
     // issued next for these registers.
     __builtin_amdgcn_s_waitcnt(0x0F70);
-    *reinterpret_cast<f32x2 *>(&s.scale[tid >> 8][(tid & 255) * 2]) = scale_pair;   // read after later barriers
     const int end = live_batch ? uni(s.misc[2]) : 0;
     const int live_tokens = end <= 0 ? 0 : (end < (int)p.tokens ? end : (int)p.tokens);
     const int batch = uni(s.misc[1]);
@@ -453,6 +452,15 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
         }
         return;
     }
+    // Sinks and the scales of both kinds (kind = tid / 256, 2 channels per
+    // thread): their addresses come from the argument block, which is read
+    // while the metadata above is in flight, so they are requested only now;
+    // the scales go to LDS after the block-table reads have been issued.
+    const __attribute__((address_space(1))) float *sinks = gptr<float>(p.sinks);
+    const float sink0 = (!ANYH || 2 * g < hlive) ? sinks[hbase + 2 * g] : 0.0f;
+    const float sink1 = (!ANYH || 2 * g + 1 < hlive) ? sinks[hbase + 2 * g + 1] : 0.0f;
+    const f32x2 scale_pair = *gptr<f32x2>(((tid >> 8) && RATIO != 1 ? p.cmpScale : p.oriScale) +
+                                          (uint64_t)((tid & 255) * 2) * 4);
 
     // ---- selection (attention_impl.h:58-73, reference.py:228-253) ----
     Row m;
@@ -729,6 +737,7 @@ c8_attention(const SharedKVArgs p, const SharedKVDebug dbg, uint32_t splits, uin
                 cslot[e] = i * N + ipos[e] % N;
             }
         }
+        if (first == 0) *reinterpret_cast<f32x2 *>(&s.scale[tid >> 8][(tid & 255) * 2]) = scale_pair;
         lds_barrier();                    // the -1 fill is complete before the writes below
 #pragma unroll
         for (int e = 0; e < PER; ++e) {
@@ -1088,20 +1097,19 @@ template <bool DEBUG, bool ANYH>
 void launch_variant(hipStream_t stream, const SharedKVArgs *a, const SharedKVDebug &dbg, bool slots, uint32_t grid,
                     uint32_t splits, uint32_t items, uint32_t fused)
 {
-    const dim3 g(grid), b(THREADS);
-    if (slots) {
-        if (a->ratio == 4)
-            hipLaunchKernelGGL((c8_attention<4, DEBUG, true, ANYH>), g, b, 0, stream, *a, dbg, splits, items, fused);
-        else if (a->ratio == 128)
-            hipLaunchKernelGGL((c8_attention<128, DEBUG, true, ANYH>), g, b, 0, stream, *a, dbg, splits, items, fused);
-        else
-            hipLaunchKernelGGL((c8_attention<1, DEBUG, true, ANYH>), g, b, 0, stream, *a, dbg, splits, items, fused);
-    } else if (a->ratio == 4)
-        hipLaunchKernelGGL((c8_attention<4, DEBUG, false, ANYH>), g, b, 0, stream, *a, dbg, splits, items, fused);
+    auto kernel = &c8_attention<1, DEBUG, false, ANYH>;
+    if (slots)
+        kernel = a->ratio == 4 ? &c8_attention<4, DEBUG, true, ANYH>
+               : a->ratio == 128 ? &c8_attention<128, DEBUG, true, ANYH> : &c8_attention<1, DEBUG, true, ANYH>;
+    else if (a->ratio == 4)
+        kernel = &c8_attention<4, DEBUG, false, ANYH>;
     else if (a->ratio == 128)
-        hipLaunchKernelGGL((c8_attention<128, DEBUG, false, ANYH>), g, b, 0, stream, *a, dbg, splits, items, fused);
-    else
-        hipLaunchKernelGGL((c8_attention<1, DEBUG, false, ANYH>), g, b, 0, stream, *a, dbg, splits, items, fused);
+        kernel = &c8_attention<128, DEBUG, false, ANYH>;
+    // The leading scalar arguments are the ones the first loads need; the
+    // build preloads them into SGPRs (-amdgpu-kernarg-preload-count), so
+    // those loads do not wait for a read of the argument block.
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(THREADS), 0, stream, a->cuQ, a->seqLens, a->q, a->indices, a->batch,
+                       a->topk, a->heads, splits, items, grid, *a, dbg, fused);
 }
 
 template <bool DEBUG>
