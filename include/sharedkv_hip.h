@@ -80,8 +80,10 @@ typedef struct SharedKVDebug {
 
 /* C4 attention: SWA128 window plus top-k compressed rows (topk <= 1024).
  * Replaces launch_sharedkv_c8_sparse (c4.cpp:70-71).  `blocks` is accepted
- * for ABI compatibility; 0 launches nothing.  The grid is tokens * splits
- * work-groups (plus a tokens-wide merge grid in merge mode 1). */
+ * for ABI compatibility; 0 launches nothing.  The grid is rows * splits
+ * work-groups rounded up to a multiple of 8, rows = tokens * ceil(heads / 8)
+ * (plus a rows-wide merge grid in merge mode 1); a launch whose grid would
+ * pass 2^31 - 8 work-groups is rejected with hipErrorInvalidValue. */
 int launch_sharedkv_c8_sparse(uint32_t blocks, void *stream, const SharedKVArgs *args);
 
 /* Small-capacity C4 entry (c4_small.cpp:21-22); same kernel family here. */
