@@ -323,6 +323,56 @@ def _padded_rows_case(heads=8):
     compare(case, bits_of(op.out)[:live], op.lse.cpu().numpy()[:live], op.splits, tag="padding")
 
 
+def test_metadata_views_and_scratch_guards():
+    """Request metadata, block tables and indices passed as views at offset
+    pointers inside buffers filled with -777, and workspace / partition
+    scratch carved out of 0xA5-filled buffers: the results equal the checker,
+    nothing outside the views is touched, and the workspace is zero again
+    after each launch.  Flow of the reference's tests/npu/test_metadata_views.py
+    :14-58 and the guard bytes of tests/support/attention_cases.py:36-54."""
+    import dataclasses
+    import torch
+    from npu_sparse_attn_sharedkv_int8 import PreparedAttention
+    case = workloads.make_case(25, 4, [2, 1, 3], [5000, 900, 12000], index_mode="mixed")
+    dev, oscale, cscale, keep = to_device(case)
+    sentinels = []
+
+    def inside(t, pad=3):
+        """t copied into the middle of a -777-filled buffer (pad rows on each side)."""
+        big = torch.full((t.shape[0] + 2 * pad, *t.shape[1:]), -777, dtype=t.dtype, device=t.device)
+        big[pad:pad + t.shape[0]] = t
+        sentinels.append((big, pad, t.shape[0]))
+        return big[pad:pad + t.shape[0]]
+
+    views = dataclasses.replace(dev, cu_q=inside(dev.cu_q), seq_lens=inside(dev.seq_lens),
+                                ori_block_table=inside(dev.ori_block_table),
+                                cmp_block_table=inside(dev.cmp_block_table), cmp_indices=inside(dev.cmp_indices))
+    assert views.cu_q.data_ptr() != dev.cu_q.data_ptr() and views.cu_q.is_contiguous()
+    scratch = []
+
+    def allocator(name, shape, dtype, device):
+        n = int(np.prod(shape)) * torch.empty((), dtype=dtype).element_size()
+        raw = torch.full((n + 512,), 0xA5, dtype=torch.uint8, device=device)
+        scratch.append((name, raw, n))
+        return raw[256:256 + n].view(dtype).view(shape)
+
+    op = PreparedAttention(views, oscale, cscale, return_lse=True, splits=3, scratch_allocator=allocator)
+    assert {name for name, _, _ in scratch} == {"workspace", "partial"}
+    for rep in range(2):
+        say(f"[views] launch {rep}")
+        op.run()
+        torch.cuda.synchronize()
+        compare(case, bits_of(op.out), op.lse.cpu().numpy(), op.splits, tag=f"views {rep}")
+        for big, pad, rows in sentinels:
+            host = big.cpu()
+            assert (host[:pad] == -777).all() and (host[pad + rows:] == -777).all()
+        for name, raw, n in scratch:
+            host = raw.cpu()
+            assert (host[:256] == 0xA5).all() and (host[256 + n:] == 0xA5).all(), name
+            if name == "workspace":
+                assert (host[256:256 + n] == 0).all(), "merge tickets must return to zero"
+
+
 def test_graph_replay_with_changing_live_metadata():
     """One captured launch replayed while the device-side live metadata
     changes; every replay equals an eager launch on the same inputs."""
