@@ -436,6 +436,23 @@ def test_rebind_same_geometry():
     compare(b, bits_of(out_b), lse_b.cpu().numpy(), 4, tag="rebind-b")
 
 
+EDGE_SHAPES = [(7, 129), (13, 513), (49, 129), (65, 513), (97, 1023)]   # test_sparse_edges.py:31-33
+
+
+@pytest.mark.parametrize("mode", ("dups", "holes") + workloads.EDGE_MODES)
+def test_sparse_edge_selections_match_checker(mode):
+    """The reference's sparse-edge selections (tests/npu/test_sparse_edges.py
+    :52-75: duplicates, holes, empty, more selected entries than the causal
+    extent, a single key, one key twice, a permutation) over its batch x
+    length shapes, one query per request: BF16 bit-exact with the checker
+    and LSE within 2e-6, on the host plan's partitions."""
+    for i, (batch, length) in enumerate(EDGE_SHAPES):
+        say(f"[edges] {mode} batch={batch} length={length}")
+        case = workloads.make_case(600 + i, 4, [1] * batch, [length] * batch, index_mode=mode)
+        out, lse, op = run_hip(case)
+        compare(case, out, lse, op.splits, tag=f"{mode} {batch}x{length}")
+
+
 def test_splits_variants_match_checker():
     case = workloads.make_case(25, 4, [2, 1], [20000, 700], index_mode="holes")
     for splits in (1, 2, 5, 9, 16):

@@ -195,6 +195,36 @@ def test_integer_oracle_close_to_fp64_attention(ratio):
     np.testing.assert_allclose(lse, ref_lse, rtol=2e-4, atol=2e-4)
 
 
+@pytest.mark.parametrize("mode", workloads.EDGE_MODES)
+def test_edge_selections_close_to_fp64_attention(mode):
+    """The reference's sparse-edge selections (tests/npu/test_sparse_edges.py
+    :52-75) through the checker, one and three KV partitions: rel-L2 < 0.01
+    and LSE within 2e-4 of FP64 attention over the same multiset of rows
+    (duplicates count once per occurrence, reference.py:115-122)."""
+    case = workloads.make_case(31, 4, [1] * 6, [129, 513, 1023, 1500, 4200, 9000], index_mode=mode)
+    c = workloads.oracle_case(case)
+    ref, ref_lse = ora.fp64_attention(c)
+    for splits in (1, 3):
+        out, lse, _ = ora.tiled_attention(c, splits=splits)
+        got = ora.bf16_to_f32(out).astype(np.float64)
+        assert np.linalg.norm(got - ref) / np.linalg.norm(ref) < 0.01, (mode, splits)
+        np.testing.assert_allclose(lse, ref_lse, rtol=2e-4, atol=2e-4, err_msg=f"{mode} S={splits}")
+
+
+def test_empty_selection_reduces_to_the_window_path():
+    """A C4 row without a valid top-k entry is its window alone, whether the
+    list is compacted away (count < topk) or kept as in-place holes (count >=
+    topk: eight fully masked tiles): bit-exact with the window-only plan on
+    the same window rows and scales."""
+    case = workloads.make_case(32, 4, [1, 2], [700, 5000], index_mode="empty")
+    window_only = dict(case, ratio=1, cmp=None, cmp_indices=None, topk=0)
+    for splits in (1, 3):
+        out_c4, lse_c4, _ = ora.tiled_attention(workloads.oracle_case(case), splits=splits)
+        out_w, lse_w, _ = ora.tiled_attention(workloads.oracle_case(window_only), splits=1)
+        assert np.array_equal(out_c4, out_w), splits
+        assert np.array_equal(lse_c4, lse_w), splits
+
+
 # ---------------------------------------------------- mathematical pins
 
 def test_expf_against_float64():

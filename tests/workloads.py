@@ -78,6 +78,33 @@ class Kind:
         view[:] = codes.reshape(pages, BLOCK * DIM)
 
 
+# Sparse-edge selections of the reference's tests/npu/test_sparse_edges.py:52-75.
+EDGE_MODES = ("empty", "single", "one_key_duplicates", "extended_duplicates", "permutation")
+
+
+def edge_indices(mode, t, count, topk, rng):
+    """One query's C4 index row (length topk, -1 = hole) for an edge mode:
+    'empty'                no valid entry;
+    'single'               one key, t mod count, in the last place;
+    'one_key_duplicates'   that key in the first and the last place;
+    'extended_duplicates'  every other place holds (place / 2) mod count, i.e.
+                           more selected entries than the causal extent;
+    'permutation'          a random order of all min(topk, count) keys."""
+    row = np.full(topk, -1, np.int64)
+    if count <= 0 or mode == "empty":
+        return row
+    if mode in ("single", "one_key_duplicates"):
+        row[topk - 1] = t % count
+        if mode == "one_key_duplicates":
+            row[0] = t % count
+    elif mode == "extended_duplicates":
+        row[::2] = np.arange((topk + 1) // 2) % count
+    else:
+        extent = min(topk, count)
+        row[:extent] = rng.permutation(extent)
+    return row
+
+
 def make_case(seed, ratio, queries, lengths, topk=1024, heads=8, window=128,
               page_stride=BLOCK * DIM, index_mode="uniform", softmax_scale=1 / math.sqrt(DIM),
               ori_slots=None, ori_topk=256):
@@ -86,6 +113,7 @@ def make_case(seed, ratio, queries, lengths, topk=1024, heads=8, window=128,
     'holes'    as uniform with every 7th entry -1 and every 11th out of range;
     'dups'     indices i // 2 (duplicates);
     'mixed'    random with replacement plus -1 padding.
+    EDGE_MODES (edge_indices): the reference's sparse-edge selections.
     ori_slots (explicit physical original slots, int32 [T, 1, ori_topk]):
     'window'   the physical slots of the query's own window rows, then -1
                (the same list, in the same places, as the window path);
@@ -137,6 +165,8 @@ def make_case(seed, ratio, queries, lengths, topk=1024, heads=8, window=128,
                     n = min(topk, max(1, count))
                     ids = rng.integers(0, max(1, count), n) if count else np.full(n, -1)
                     ids[rng.random(n) < 0.2] = -1
+                elif index_mode in EDGE_MODES:
+                    ids = edge_indices(index_mode, t, count, topk, rng)
                 else:
                     raise ValueError(index_mode)
                 indices[t, 0, :len(ids)] = ids
