@@ -1026,28 +1026,36 @@ c8_merge(const SharedKVArgs p, uint32_t splits)
 // ---- INT8 cache writer (cache_write.cpp:9-88): one wave per update row ----
 template <typename Index, bool Paired>
 __global__ void __launch_bounds__(256)
-cache_write(const CacheWriteArgs a)
+cache_write(const uint64_t updates, const uint64_t inverse_scale, const uint64_t slot_base, const uint64_t update_stride,
+            const uint32_t slot_stride, const uint32_t slot_column_stride, const uint32_t tokens, const CacheWriteArgs a)
 {
+    // The leading arguments (copies of argument-block fields) arrive preloaded
+    // in SGPRs, so the row's loads do not wait for a read of the block.
     const int lane = threadIdx.x & 63;
     const uint32_t row = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (row >= a.tokens) return;
-    const Index *slots = reinterpret_cast<const Index *>(a.slots);
-    const int64_t first = (int64_t)slots[(uint64_t)row * a.slotStride];
+    if (row >= tokens) return;
+    // The row's values and the inverse scale are requested together with its
+    // slot (every row below `tokens` exists), so a row costs one memory round
+    // trip; rows the slot rules skip simply drop them.
+    const uint64_t src = updates + ((uint64_t)row * update_stride + lane * 8) * 2;
+    const uint64_t inv = inverse_scale + (uint64_t)(lane * 8) * 4;
+    const v4i x = *gptr<v4i>(src);
+    const f32x4 i0 = *gptr<f32x4>(inv);
+    const f32x4 i1 = *gptr<f32x4>(inv + 16);
+    const __attribute__((address_space(1))) Index *slots = gptr<Index>(slot_base);
+    const int64_t first = (int64_t)slots[(uint64_t)row * slot_stride];
+    const int64_t second = Paired ? (int64_t)slots[(uint64_t)row * slot_stride + slot_column_stride] : 0;
+    asm volatile("" :: "v"(x), "v"(i0), "v"(i1));   // all loads are in flight before the slot is tested
     if (first < 0) return;
     int64_t page, offset;
     if (Paired) {
         page = first;
-        offset = (int64_t)slots[(uint64_t)row * a.slotStride + a.slotColumnStride];
+        offset = second;
     } else {
         page = first / (int64_t)a.pageSize;
         offset = first % (int64_t)a.pageSize;
     }
     if (page >= (int64_t)a.pages || offset < 0 || offset >= (int64_t)a.pageSize) return;
-    const uint16_t *src = reinterpret_cast<const uint16_t *>(a.updates) + (uint64_t)row * a.updateStride + lane * 8;
-    const float *inv = reinterpret_cast<const float *>(a.inverseScale) + lane * 8;
-    const v4i x = *reinterpret_cast<const v4i *>(src);
-    const f32x4 i0 = *reinterpret_cast<const f32x4 *>(inv);
-    const f32x4 i1 = *reinterpret_cast<const f32x4 *>(inv + 4);
     const uint32_t w[4] = {(uint32_t)x.x, (uint32_t)x.y, (uint32_t)x.z, (uint32_t)x.w};
     const float iv[8] = {i0.x, i0.y, i0.z, i0.w, i1.x, i1.y, i1.z, i1.w};
     uint32_t packed[2] = {0, 0};
@@ -1172,16 +1180,14 @@ int launch_cache_write(uint32_t blocks, void *stream, const CacheWriteArgs *a)
         (a->pageStride % 8) || (a->cache & 7) || a->pageStride < (uint64_t)a->pageSize * D)
         return (int)hipErrorInvalidValue;
     if (a->pairedSlots && a->slotColumnStride == 0) return (int)hipErrorInvalidValue;
+    if (a->slotStride > UINT32_MAX || a->slotColumnStride > UINT32_MAX) return (int)hipErrorInvalidValue;
     if (a->tokens == 0) return (int)hipSuccess;
     const dim3 grid((a->tokens + 3) / 4);
     hipStream_t s = static_cast<hipStream_t>(stream);
-    if (a->int64Slots) {
-        if (a->pairedSlots) hipLaunchKernelGGL((cache_write<int64_t, true>), grid, dim3(256), 0, s, *a);
-        else hipLaunchKernelGGL((cache_write<int64_t, false>), grid, dim3(256), 0, s, *a);
-    } else {
-        if (a->pairedSlots) hipLaunchKernelGGL((cache_write<int32_t, true>), grid, dim3(256), 0, s, *a);
-        else hipLaunchKernelGGL((cache_write<int32_t, false>), grid, dim3(256), 0, s, *a);
-    }
+    auto kernel = a->int64Slots ? (a->pairedSlots ? &cache_write<int64_t, true> : &cache_write<int64_t, false>)
+                                : (a->pairedSlots ? &cache_write<int32_t, true> : &cache_write<int32_t, false>);
+    hipLaunchKernelGGL(kernel, grid, dim3(256), 0, s, a->updates, a->inverseScale, a->slots, a->updateStride,
+                       (uint32_t)a->slotStride, (uint32_t)a->slotColumnStride, a->tokens, *a);
     return (int)hipGetLastError();
 }
 
