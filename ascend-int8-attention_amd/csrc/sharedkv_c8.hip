@@ -288,7 +288,9 @@ __device__ __forceinline__ f32x4 state_load4(__amdgpu_buffer_rsrc_t r, int offse
 // Thread = (head tid / 64, columns 8 (tid % 64) .. + 7) of a 512-thread
 // group.  Partitions are folded in order.  MAXS bounds S at compile time so
 // every load is issued before any is used (offsets of partitions past S are
-// clamped to partition 0 and their values ignored).
+// clamped to partition 0 and their values ignored); fold_row instantiates it
+// exactly for the partition counts the host plan picks (up to 6), since every
+// clamped partition still costs its loads and its exponential.
 template <int MAXS, int POLICY>
 __device__ __forceinline__ void fold_states(const __amdgpu_buffer_rsrc_t states, int S, int tid,
                                             uint16_t *out_row, float *lse_row, int heads)
@@ -343,6 +345,8 @@ __device__ __forceinline__ void fold_row(const __amdgpu_buffer_rsrc_t states, in
     if (S <= 2) fold_states<2, POLICY>(states, S, tid, out_row, lse_row, heads);
     else if (S == 3) fold_states<3, POLICY>(states, S, tid, out_row, lse_row, heads);
     else if (S == 4) fold_states<4, POLICY>(states, S, tid, out_row, lse_row, heads);
+    else if (S == 5) fold_states<5, POLICY>(states, S, tid, out_row, lse_row, heads);
+    else if (S == 6) fold_states<6, POLICY>(states, S, tid, out_row, lse_row, heads);
     else if (S <= 8) fold_states<8, POLICY>(states, S, tid, out_row, lse_row, heads);
     else fold_states<16, POLICY>(states, S, tid, out_row, lse_row, heads);
 }

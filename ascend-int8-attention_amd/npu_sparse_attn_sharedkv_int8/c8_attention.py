@@ -40,9 +40,8 @@ MAX_SPLITS = 16
 WINDOW = 128
 BLOCK = 32
 MAX_TOPK = 1024
-SPLITS_FEW_ROWS = 5        # fewer than FEW_ROWS query rows
+SPLITS_FEW_ROWS = 5        # when rows x 5 work-groups fit one wave on the CUs
 SPLITS_MANY_ROWS = 3
-FEW_ROWS = 8
 PARTIAL_FLOATS = 520       # per (token, partition, head): 512 numerator, max, denominator, pad
 
 VARIANT_SPARSE, VARIANT_DENSE, VARIANT_SPARSE_SMALL = 20, 21, 22
@@ -81,7 +80,10 @@ def choose_splits(tokens, ratio, topk, max_seq_len=None, ori_topk=0):
     """KV partitions for a launch of `tokens` query rows (host-side plan)."""
     if tokens <= 0:
         return 1
-    wanted = SPLITS_FEW_ROWS if tokens < FEW_ROWS else SPLITS_MANY_ROWS
+    # Five partitions while rows x 5 work-groups fit one wave on the CUs (a
+    # row's nine tiles then take at most two per partition), else three; on
+    # MI355X this is the fastest of 2..6 at 1, 32 and 64 rows.
+    wanted = SPLITS_FEW_ROWS if tokens * SPLITS_FEW_ROWS <= CORES else SPLITS_MANY_ROWS
     wanted = min(wanted, max(1, CORES // tokens))
     return max(1, min(wanted, max_tiles(ratio, topk, max_seq_len, ori_topk), MAX_SPLITS))
 

@@ -104,7 +104,8 @@ def test_host_plan():
     assert c8_attention.max_tiles(128, 0, 4096) == 2
     assert c8_attention.max_tiles(1, 0) == 1
     assert c8_attention.choose_splits(64, 4, 1024) == 3
-    assert c8_attention.choose_splits(32, 4, 1024) == 3
+    assert c8_attention.choose_splits(32, 4, 1024) == 5       # 160 work-groups: one wave
+    assert c8_attention.choose_splits(51, 4, 1024) == 5 and c8_attention.choose_splits(52, 4, 1024) == 3
     assert c8_attention.choose_splits(1, 4, 1024) == 5
     assert c8_attention.choose_splits(100, 4, 1024) == 2       # one wave of work-groups
     assert c8_attention.choose_splits(4096, 4, 1024) == 1
