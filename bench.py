@@ -158,6 +158,7 @@ def main():
     ap.add_argument("--splits", type=int, default=None, help="override the host plan's KV partitions")
     ap.add_argument("--page-stride", type=int, default=None, help="override the workload's page stride (bytes)")
     ap.add_argument("--merge", type=int, default=0, help="0: fused partition merge, 1: separate merge launch")
+    ap.add_argument("--heads", type=int, default=8, help="query heads per token (the metric is quoted at 8)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -187,7 +188,7 @@ def main():
     layers = max(1, min(args.layers, stride // 16384))
     log(f"[bench] generating {description}; {layers} layers at page stride {stride}")
     t0 = time.perf_counter()
-    dc = DeviceCase(seed, ratio, queries, lengths, page_stride=stride, layers=layers)
+    dc = DeviceCase(seed, ratio, queries, lengths, page_stride=stride, layers=layers, heads=args.heads)
     torch.cuda.synchronize()
     log(f"[bench] generated in {time.perf_counter() - t0:.1f} s: ori pages {dc.ori.pages}, "
         f"cmp pages {dc.cmp.pages if dc.cmp else 0}")
@@ -235,13 +236,14 @@ def main():
     # int8 MFMA work the launch performs: per selected key, QK and PV over
     # 16 rows (8 heads x {code, residual}) x 512 channels, 2 ops per MAC.
     keys = dc.selected_keys(0)
-    int8_ops = keys * 16 * 512 * 2 * 2
-    metric = METRIC if args.workload == "headline" else f"INT8 sharedKV attention queries/s + HBM GB/s, {args.workload}"
+    int8_ops = keys * 16 * 512 * 2 * 2 * ((args.heads + 7) // 8)   # per group of eight heads
+    metric = (METRIC if args.workload == "headline" and args.heads == 8 else
+              f"INT8 sharedKV attention queries/s + HBM GB/s, {args.workload}, {args.heads} heads")
     record = {
         "metric": metric, "value": live_queries / (ms_per_step * 1e-3), "unit": "queries/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_per_step, "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "i8", "data": "synthetic (GPU-generated, seeded)",
-        "config": {"workload": description, "batch": len(queries), "query_tokens": live_queries, "heads": 8,
+        "config": {"workload": description, "batch": len(queries), "query_tokens": live_queries, "heads": args.heads,
                    "dim": 512, "ratio": ratio, "topk": 1024 if ratio == 4 else 0, "window": 128,
                    "page_stride": stride, "layers_rotated": layers, "tile": 128, "splits": splits,
                    "lse": False, "merge": "fused" if args.merge == 0 else "separate launch",

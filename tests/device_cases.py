@@ -277,6 +277,7 @@ class DeviceCase:
         counts = (positions + 1) // max(ratio, 1)
         self.q_bits = [workloads.bf16_bits(rng.standard_normal((tokens, heads, DIM), dtype=np.float32))
                        for _ in range(layers)]
+        self.heads = heads
         self.sink = np.linspace(-2, 2, heads, dtype=np.float32)
         self.indices = [c4_indices(rng, counts, topk) for _ in range(layers)] if ratio == 4 else [None] * layers
         ori_touched, cmp_touched = [], []
@@ -365,8 +366,9 @@ class DeviceCase:
             rows += len(ids)
             entries += len(np.unique(ids // block))
         tokens = len(m["positions"])
-        q_out = tokens * 8 * DIM * 2 * 2 + (tokens * 8 * 4 if lse else 0)
+        heads = self.heads
+        q_out = tokens * heads * DIM * 2 * 2 + (tokens * heads * 4 if lse else 0)
         index_bytes = ix.size * 4 if ix is not None else 0
-        scales = DIM * 4 * (2 if m["ratio"] != 1 else 1) + 8 * 4
+        scales = DIM * 4 * (2 if m["ratio"] != 1 else 1) + heads * 4
         meta = (len(m["cu_q"]) + len(m["seq_lens"])) * 4
         return rows * DIM + q_out + index_bytes + entries * 4 + scales + meta
