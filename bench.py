@@ -167,7 +167,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
-              "the per-sequence sharding plan is described in DESIGN.md", file=sys.stderr)
+              "the path shards by sequence, each GPU running this kernel on its own rows", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np
