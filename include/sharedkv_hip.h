@@ -98,7 +98,8 @@ int launch_sharedkv_c8_dense(uint32_t blocks, void *stream, const SharedKVArgs *
 int sharedkv_c8_attention_debug(void *stream, const SharedKVArgs *args, const SharedKVDebug *debug);
 
 /* Fused INT8 quantise + slot scatter (cache_write.cpp:71-80).  `blocks` is
- * accepted for ABI compatibility; 0 launches nothing. */
+ * accepted for ABI compatibility; 0 launches nothing.  slotStride and
+ * slotColumnStride must fit 32 bits (else hipErrorInvalidValue). */
 int launch_cache_write(uint32_t blocks, void *stream, const CacheWriteArgs *args);
 
 /* Scratch sizes in bytes for a launch with `rows` = tokens * ceil(heads / 8)
