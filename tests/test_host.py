@@ -97,6 +97,11 @@ def test_launch_rejects_grids_past_the_limit():
     a.heads, a.ratio, a.window, a.oriBlock, a.cmpBlock, a.batch, a.oriPages = 128, 4, 128, 32, 32, 1, 1
     a.topk, a.oriStride, a.cmpStride, a.tokens, a.splits = 1024, 16384, 16384, 1 << 23, 16
     assert lib.launch_sharedkv_c8_sparse(1, None, ctypes.byref(a)) == 1
+    # The writer passes slot strides as 32-bit kernel arguments.
+    w = runtime.CacheWriteArgs(cache=0x10000, updates=0x10000, slots=0x10000, inverseScale=0x10000,
+                               pageStride=16384, updateStride=512, slotStride=1 << 32, slotColumnStride=1,
+                               tokens=4, pages=1, pageSize=32)
+    assert lib.launch_cache_write(1, None, ctypes.byref(w)) == 1
 
 
 def test_host_plan():
