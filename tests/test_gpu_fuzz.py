@@ -1,7 +1,8 @@
 """Seeded random launches against the CPU checker: mixed ratios, head counts,
 explicit original slots, C4 index modes, graph-capacity padding rows, KV
-partitions and both merge placements, all bit-exact (BF16 outputs) with the
+partitions (1-8) and both merge placements, all bit-exact (BF16 outputs) with the
 checker on the launch's own plan and LSE within 2e-6."""
+import os
 import sys
 
 import numpy as np
@@ -12,7 +13,7 @@ from tests.device_cases import run_hip, run_oracle
 
 pytestmark = pytest.mark.gpu
 
-CASES = 48
+CASES = int(os.environ.get("SHAREDKV_FUZZ_CASES", "48"))   # more for a longer sweep
 
 
 def say(*a):
@@ -26,10 +27,10 @@ def random_case(seed):
     queries = [int(q) for q in rng.integers(1, 5, batch)]
     lengths = [int(max(q, rng.integers(1, 9000))) for q in queries]
     heads = int(rng.choice([8, 8, 8, 4, 12, 16]))
-    mode = str(rng.choice(["uniform", "holes", "dups", "mixed"]))
+    mode = str(rng.choice(["uniform", "holes", "dups", "mixed"] + list(workloads.EDGE_MODES)))
     slots = rng.random() < 0.25
     slot_mode = str(rng.choice(["draft", "shuffled", "pool"])) if slots else None
-    splits = rng.choice([None, 1, 2, 3, 5])
+    splits = rng.choice([None, 1, 2, 3, 4, 5, 6, 8])
     merge = int(rng.integers(0, 2))
     topk = int(rng.choice([1024, 512, 256]))
     need = max(q + 128 for q in queries) if slot_mode in ("draft", "shuffled") else 0
