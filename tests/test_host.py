@@ -119,6 +119,16 @@ def test_host_plan():
     assert c8_attention.choose_splits(1, 1, 0) == 1
 
 
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py measures one GPU; --gpus N > 1 exits with a message before it
+    touches a device."""
+    import subprocess
+    import sys
+    run = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                         timeout=120)
+    assert run.returncode == 2 and "measures one GPU" in run.stderr and not run.stdout
+
+
 def test_c8_switch():
     import os
     old = os.environ.get("SHAREDKV_C8_DECODE")
