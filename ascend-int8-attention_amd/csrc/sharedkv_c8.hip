@@ -444,16 +444,17 @@ c8_attention(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base
     const int batch = uni(s.misc[1]);
     uint16_t *out_row = reinterpret_cast<uint16_t *>(p.out) + ((int64_t)t * H + hbase) * D;
     float *lse_row = p.lse ? reinterpret_cast<float *>(p.lse) + (int64_t)t * H + hbase : nullptr;
+    // A row without keys is zero-filled by partition 0: output and LSE, and
+    // with a separate merge launch its partition count (0: nothing to fold).
+    auto zero_row = [&]() {
+        if (part != 0) return;
+        if (!ANYH || tid < hlive * (D / 8)) reinterpret_cast<v4i *>(out_row)[tid] = v4i{0, 0, 0, 0};
+        if (lse_row && tid < hlive) lse_row[tid] = 0.0f;
+        if (S > 1 && !fused && tid == 0)
+            reinterpret_cast<float *>(p.partial)[(int64_t)qrow * S * HEADS * PART_FLOATS + FOLD_SLOT] = 0.0f;
+    };
     if (t >= live_tokens || batch < 0) {
-        // Graph padding rows are zero-filled (attention_impl.h:443-460); with
-        // a separate merge launch, partition 0 also marks the row
-        // (denominator -1) so that launch leaves it alone.
-        if (part == 0) {
-            if (!ANYH || tid < hlive * (D / 8)) reinterpret_cast<v4i *>(out_row)[tid] = v4i{0, 0, 0, 0};
-            if (lse_row && tid < hlive) lse_row[tid] = 0.0f;
-            if (S > 1 && !fused && tid == 0)
-                reinterpret_cast<float *>(p.partial)[(int64_t)qrow * S * HEADS * PART_FLOATS + FOLD_SLOT] = 0.0f;
-        }
+        zero_row();   // graph padding rows (attention_impl.h:443-460)
         return;
     }
     // Sinks and the scales of both kinds (kind = tid / 256, 2 channels per
@@ -549,12 +550,20 @@ c8_attention(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base
     m.t0 = (m.ori_count + N - 1) / N;
     m.total = m.t0 + (m.list_len + N - 1) / N;
     const int my_tiles = m.total > part ? (m.total - part + S - 1) / S : 0;   // tiles part, part + S, ...
+    // A live row's window list holds at least its own position, so it has a
+    // tile, unless its request lists more query tokens than its sequence
+    // length (a negative position, which reference.py:104-105 rejects): that
+    // row is zero-filled, explicit original slots or not.
+    if (m.total == 0 || m.position < 0) {
+        zero_row();
+        return;
+    }
     // Partitions that own no tile (part >= total) hold the initial state
     // (max = sink <= every owning partition's max, numerator and denominator
     // 0), which folds to exactly nothing: they publish nothing, and a row
     // whose tiles all sit in partition 0 is finalized by it directly.  The
     // numbers equal the fold over all S partitions bit for bit.
-    const int folded = S < m.total ? S : m.total;    // partitions that own tiles (>= 1: the window is never empty)
+    const int folded = S < m.total ? S : m.total;    // partitions that own tiles (>= 1)
     if (part >= folded) return;
 
     // ---- per-lane softmax state for heads 2g and 2g+1 ----

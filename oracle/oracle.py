@@ -104,9 +104,11 @@ def cache_write(pool, page_stride, pages, page_size, updates_bf16, slots, invers
 
 
 def expf(x):
-    f = lib().sko_expf
-    return np.array([f(float(v)) for v in np.asarray(x, dtype=np.float32).ravel()],
-                    dtype=np.float32).reshape(np.shape(x))
+    """sko_expf elementwise (the checker's and the kernels' exponential)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty_like(x)
+    lib().sko_expf_array(_ptr(x), _ptr(y), ctypes.c_int64(x.size))
+    return y
 
 
 # ---------------------------------------------------------------- attention
@@ -155,13 +157,15 @@ class _Case(ctypes.Structure):
 
 class _Plan(ctypes.Structure):
     _fields_ = [(n, ctypes.c_int32) for n in
-                ("tile", "splits", "joint_dense", "joint_sparse", "joint_tile_limit", "dense_c4")]
+                ("tile", "splits", "joint_dense", "joint_sparse", "joint_tile_limit", "dense_c4",
+                 "query_group")]
 
 
 class _Debug(ctypes.Structure):
     _fields_ = [("qcodes", ctypes.c_void_p), ("alpha", ctypes.c_void_p), ("scores", ctypes.c_void_p),
                 ("probs", ctypes.c_void_p), ("values", ctypes.c_void_p),
-                ("cmp_capacity", ctypes.c_int32), ("tile_capacity", ctypes.c_int32)]
+                ("cmp_capacity", ctypes.c_int32), ("tile_capacity", ctypes.c_int32),
+                ("weight_args", ctypes.c_void_p)]
 
 
 def _c(a, dtype):
@@ -170,8 +174,10 @@ def _c(a, dtype):
 
 def tiled_attention(case, tile=128, splits=1, return_lse=True, joint_dense=False, joint_sparse=False,
                     joint_tile_limit=256, dense_c4=False, debug=False, threads=None,
-                    cmp_capacity=None, tile_capacity=None):
-    """reference.py:210-323.  Returns (out_bf16_bits [T,H,512], lse [T,H], debug dict or None)."""
+                    cmp_capacity=None, tile_capacity=None, query_group=1):
+    """reference.py:210-323.  Returns (out_bf16_bits [T,H,512], lse [T,H], debug dict or None).
+    debug (query_group 1, eight heads) adds the integer dumps and the
+    softmax-weight exponential arguments (weight_args)."""
     q = _c(case.q, np.uint16)
     T, H, _ = q.shape
     keep = dict(q=q, ori=_c(case.ori, np.int8), ot=_c(case.ori_table, np.int32),
@@ -190,7 +196,8 @@ def tiled_attention(case, tile=128, splits=1, return_lse=True, joint_dense=False
               _ptr(keep["cu"]), _ptr(keep["sl"]), len(keep["sl"]), _ptr(keep["sink"]),
               _ptr(keep["os"]), _ptr(keep["cs"]), T, H, case.block, case.ratio, case.window,
               case.softmax_scale, _ptr(keep["oi"]), ori_topk, case.ori_pages)
-    plan = _Plan(tile, splits, int(joint_dense), int(joint_sparse), joint_tile_limit, int(dense_c4))
+    plan = _Plan(tile, splits, int(joint_dense), int(joint_sparse), joint_tile_limit, int(dense_c4),
+                 int(query_group))
     out = np.zeros((T, H, DIM), dtype=np.uint16)
     lse = np.zeros((T, H), dtype=np.float32) if return_lse else None
     dbg = None
@@ -204,9 +211,10 @@ def tiled_attention(case, tile=128, splits=1, return_lse=True, joint_dense=False
         dbg_arrays = dict(
             qcodes=np.zeros((T, 2, 16, DIM), np.int8), alpha=np.zeros((T, 2, 8), np.float32),
             scores=np.zeros((T, positions, 16), np.int32), probs=np.zeros((T, positions, 16), np.int8),
-            values=np.zeros((T, tile_capacity, 16, DIM), np.int32))
+            values=np.zeros((T, tile_capacity, 16, DIM), np.int32),
+            weight_args=np.full((T, positions, 8), np.nan, np.float32))
         dbg = _Debug(*(_ptr(dbg_arrays[k]) for k in ("qcodes", "alpha", "scores", "probs", "values")),
-                     cmp_capacity, tile_capacity)
+                     cmp_capacity, tile_capacity, _ptr(dbg_arrays["weight_args"]))
     threads = threads or int(os.environ.get("SKO_THREADS", os.cpu_count() or 1))
     rc = lib().sko_tiled_attention(ctypes.byref(c), ctypes.byref(plan), _ptr(out), _ptr(lse),
                                    ctypes.byref(dbg) if dbg is not None else None, threads)

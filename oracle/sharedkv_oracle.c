@@ -56,6 +56,12 @@ float sko_expf(float x)
     return ldexpf(p, (int)n);
 }
 
+void sko_expf_array(const float *x, float *y, int64_t n)
+{
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; ++i) y[i] = sko_expf(x[i]);
+}
+
 uint16_t sko_f32_to_bf16(float x)
 {
     uint32_t u;
@@ -283,7 +289,10 @@ void sko_joint_row(const uint16_t *q, int heads, const int8_t *const *rows, cons
     free(lo);
 }
 
-/* One query row of reference.py:224-323 (query_group = 1). */
+/* One query row of reference.py:224-323.  Queries of one request form
+ * groups of pl->query_group consecutive tokens (reference.py:229-231); a
+ * group shares one window list and one compressed list, each query masking
+ * what it may not see. */
 static void attend_token(const sko_case *c, const sko_plan *pl, int32_t b, int32_t t, int32_t last,
                          uint16_t *out, float *lse, sko_debug *dbg)
 {
@@ -291,15 +300,25 @@ static void attend_token(const sko_case *c, const sko_plan *pl, int32_t b, int32
     const int32_t length = c->seq_lens[b];
     const int64_t position = (int64_t)length - last + t;
     const int residual = H <= 8;   /* reference.py:221-222 */
+    const int32_t G = pl->query_group;
+    const int32_t first_q = c->cu_q[b];
+    const int32_t group_first = first_q + (t - first_q) / G * G;
+    const int32_t group_last = (last < group_first + G ? last : group_first + G) - 1;
+    const int64_t first_pos = (int64_t)length - last + group_first;
+    const int64_t last_pos = (int64_t)length - last + group_last;
     kind_list lists[2];
     int kinds = 1;
 
-    /* Kind 0: SWA window, reference.py:232-234, or the explicit physical
-     * slots of reference.py:236-239 (every entry keeps its place; entries
-     * outside [0, pages * block) are holes). */
-    int64_t first = position + 1 - c->window;
+    /* Kind 0: SWA window, reference.py:232-234 (the group's positions
+     * max(0, first_pos + 1 - window) .. last_pos, valid where they fall in
+     * this query's own window), or the explicit physical slots of
+     * reference.py:236-239 (every entry keeps its place; entries outside
+     * [0, pages * block) are holes). */
+    int64_t first = first_pos + 1 - c->window;
     if (first < 0) first = 0;
-    int32_t ori_count = c->ori_slots ? c->ori_topk : (int32_t)(position + 1 - first);
+    int64_t own_first = position + 1 - c->window;
+    if (own_first < 0) own_first = 0;
+    int32_t ori_count = c->ori_slots ? c->ori_topk : (int32_t)(last_pos + 1 - first);
     lists[0] = (kind_list){c->ori, c->ori_stride, c->ori_slots ? NULL : c->ori_table, c->ori_table_width,
                            c->ori_scale, ori_count, malloc(sizeof(int64_t) * (ori_count ? ori_count : 1)),
                            malloc(ori_count ? ori_count : 1), NULL};
@@ -310,15 +329,17 @@ static void attend_token(const sko_case *c, const sko_plan *pl, int32_t b, int32
             lists[0].valid[i] = slot >= 0 && slot < (int64_t)c->ori_pages * c->block;
         } else {
             lists[0].index[i] = first + i;
-            lists[0].valid[i] = 1;
+            lists[0].valid[i] = first + i >= own_first && first + i <= position;
         }
     }
 
-    /* Kind 1: compressed rows, reference.py:242-253. */
+    /* Kind 1: compressed rows, reference.py:242-253.  C128 lists the
+     * group's rows, valid below this query's own count. */
     if (c->ratio != 1) {
         kinds = 2;
         int64_t count = (position + 1) / c->ratio;
-        int32_t n = c->ratio == 4 ? c->topk : (int32_t)count;
+        int64_t group_count = (last_pos + 1) / c->ratio;
+        int32_t n = c->ratio == 4 ? c->topk : (int32_t)group_count;
         kind_list *k = &lists[1];
         *k = (kind_list){c->cmp, c->cmp_stride, c->cmp_table, c->cmp_table_width, c->cmp_scale,
                          n, malloc(sizeof(int64_t) * (n ? n : 1)), malloc(n ? n : 1), NULL};
@@ -327,17 +348,18 @@ static void attend_token(const sko_case *c, const sko_plan *pl, int32_t b, int32
             k->index[j] = idx;
             k->valid[j] = idx >= 0 && idx < count;
         }
-        if (c->ratio == 4 && (pl->dense_c4 || pl->joint_sparse)) {
-            /* reference.py:246-249: multiplicity over arange(count). */
-            float *mult = calloc(count ? count : 1, sizeof(float));
+        if (c->ratio == 4 && (G > 1 || pl->dense_c4 || pl->joint_sparse)) {
+            /* reference.py:246-249: multiplicity over arange of the group's
+             * compressed rows (every valid index lies below it). */
+            float *mult = calloc(group_count ? group_count : 1, sizeof(float));
             for (int32_t j = 0; j < n; ++j)
                 if (k->valid[j]) mult[k->index[j]] += 1.0f;
             free(k->index);
             free(k->valid);
-            k->length = (int32_t)count;
-            k->index = malloc(sizeof(int64_t) * (count ? count : 1));
-            k->valid = malloc(count ? count : 1);
-            for (int64_t j = 0; j < count; ++j) {
+            k->length = (int32_t)group_count;
+            k->index = malloc(sizeof(int64_t) * (group_count ? group_count : 1));
+            k->valid = malloc(group_count ? group_count : 1);
+            for (int64_t j = 0; j < group_count; ++j) {
                 k->index[j] = j;
                 k->valid[j] = mult[j] > 0.0f;
             }
@@ -358,7 +380,7 @@ static void attend_token(const sko_case *c, const sko_plan *pl, int32_t b, int32
 
     /* Joint row, reference.py:254-267. */
     if (((pl->joint_dense && c->ratio == 128) || (pl->joint_sparse && c->ratio == 4)) && S == 1
-        && N <= pl->joint_tile_limit && kinds == 2 && lists[1].length <= N && lists[0].length <= N
+        && (c->ratio == 128 || G == 1) && N <= pl->joint_tile_limit && kinds == 2 && lists[1].length <= N && lists[0].length <= N
         && (pl->joint_sparse || lists[1].length > 0)) {
         const int8_t *rows[2];
         int32_t counts[2];
@@ -481,7 +503,12 @@ static void attend_token(const sko_case *c, const sko_plan *pl, int32_t b, int32
                     float m_new = *m_old;
                     for (int32_t j = 0; j < n; ++j) m_new = logit[h * N + j] > m_new ? logit[h * N + j] : m_new;
                     float factor = sko_expf(*m_old - m_new);
-                    for (int32_t j = 0; j < n; ++j) w[j] = sko_expf(logit[h * N + j] - m_new);
+                    for (int32_t j = 0; j < n; ++j) {
+                        w[j] = sko_expf(logit[h * N + j] - m_new);
+                        if (dbg && dbg->weight_args && H == 8)
+                            dbg->weight_args[((int64_t)t * cap + (k ? 128 : 0) + start + j) * 8 + h] =
+                                logit[h * N + j] - m_new;
+                    }
                     den[part * H + h] = den[part * H + h] * factor + sko_tree_sum(w, n, padded);
                     for (int32_t j = 0; j < n; ++j) {
                         float x = w[j] * 127.0f;
@@ -554,7 +581,8 @@ int sko_tiled_attention(const sko_case *c, const sko_plan *pl, uint16_t *out, fl
     if (!c || !pl || !out || c->heads <= 0 || c->heads > 128 || c->block <= 0 || c->window <= 0)
         return -1;
     if (c->ratio != 1 && c->ratio != 4 && c->ratio != 128) return -2;
-    if (pl->tile <= 0 || (pl->tile & (pl->tile - 1)) || pl->splits <= 0) return -3;
+    if (pl->tile <= 0 || (pl->tile & (pl->tile - 1)) || pl->splits <= 0 || pl->query_group <= 0) return -3;
+    if (pl->query_group > 1 && (c->ori_slots || dbg)) return -10;   /* reference.py:236-237 */
     if (c->ratio != 1 && (!c->cmp || !c->cmp_table || !c->cmp_scale)) return -4;
     if (c->ratio == 4 && (!c->cmp_indices || c->topk <= 0)) return -5;
     if (dbg && (c->window > 128 || (c->ori_slots && c->ori_topk > 128))) return -6;

@@ -21,6 +21,7 @@ extern "C" {
  * degree-8 Taylor polynomial in Horner form with explicit fma).  Inputs below
  * -87 return 0 (no subnormal results on either side). */
 float sko_expf(float x);
+void sko_expf_array(const float *x, float *y, int64_t n);
 
 /* reference.py:47-50  inverse_scale = fp32(1 / fp64(scale)). */
 void sko_inverse_scale(const float *scale, float *inverse, int64_t count);
@@ -79,6 +80,7 @@ typedef struct {
     int32_t joint_sparse;      /* reference.py:246,254 joint C4 row with log multiplicity */
     int32_t joint_tile_limit;  /* reference.py:212 default 256 */
     int32_t dense_c4;          /* reference.py:246 C4 as multiplicity-weighted dense list */
+    int32_t query_group;       /* reference.py:229-231: queries sharing one window/list (>= 1) */
 } sko_plan;
 
 /* Optional per-token dumps (heads must be 8).  Any pointer may be NULL.
@@ -89,6 +91,9 @@ typedef struct {
  *   probs  [tokens][128 + cmp_capacity][16] int8: p8 heads 0-7, p_low 8-15
  *   values [tokens][tile_capacity][16][512] int32: V_hi rows 0-7, V_lo 8-15,
  *          tiles numbered continuously across kinds
+ *   weight_args [tokens][128 + cmp_capacity][8] f32: the argument of each
+ *          softmax-weight exponential, logit - running max (reference.py:305),
+ *          per list position and head; masked positions included
  * Joint rows (reference.py:175-207) fill qcodes/alpha/scores/probs only. */
 typedef struct {
     int8_t *qcodes;
@@ -98,10 +103,12 @@ typedef struct {
     int32_t *values;
     int32_t cmp_capacity;
     int32_t tile_capacity;
+    float *weight_args;
 } sko_debug;
 
-/* reference.py:210-323 tiled_quantized_reference (query_group = 1, no
- * explicit original slots, no row factors).  out: BF16 bits [tokens][heads][512]
+/* reference.py:210-323 tiled_quantized_reference (any query_group; explicit
+ * original slots need query_group 1; no row factors; debug dumps need
+ * query_group 1).  out: BF16 bits [tokens][heads][512]
  * for tokens < cu_q[batch]; lse: FP32 [tokens][heads] or NULL.  Returns 0 on
  * success, a negative code on invalid arguments. */
 int sko_tiled_attention(const sko_case *c, const sko_plan *plan, uint16_t *out, float *lse,
