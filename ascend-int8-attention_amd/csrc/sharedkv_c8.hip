@@ -40,6 +40,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #include "sharedkv_hip.h"
 
 #pragma clang fp contract(off)
@@ -1156,6 +1158,44 @@ int launch_attention(hipStream_t stream, const SharedKVArgs *a, const SharedKVDe
     return (int)hipGetLastError();
 }
 
+// ---- scratch of the allocation-free entry point ----
+// One array per GPU, holding the launch's merge tickets (one uint32 per row,
+// 256-byte aligned block) followed by its partition states.  The loader
+// zero-fills it, and every launch leaves the tickets zero again.  Host code
+// never passes the array's name to a kernel: its device address is taken
+// once per device with hipGetSymbolAddress and kept in g_scratch.
+constexpr uint64_t NOALLOC_SCRATCH_BYTES = 16ull << 20;
+static __device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH_BYTES];
+
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mutex;
+void *g_scratch[MAX_DEVICES];
+
+// Device address of the current device's scratch array (looked up on the
+// first call on that device).
+int scratch_address(void **out)
+{
+    int device = 0;
+    hipError_t e = hipGetDevice(&device);
+    if (e != hipSuccess) return (int)e;
+    if (device < 0 || device >= MAX_DEVICES) return (int)hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_scratch_mutex);
+    if (!g_scratch[device]) {
+        void *ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return (int)e;
+        g_scratch[device] = ptr;
+    }
+    *out = g_scratch[device];
+    return (int)hipSuccess;
+}
+
+uint64_t workspace_bytes(uint32_t rows) { return ((uint64_t)rows * 4 + 255) / 256 * 256; }
+uint64_t partial_bytes(uint32_t rows, uint32_t splits)
+{
+    return splits > 1 ? (uint64_t)rows * splits * HEADS * PART_FLOATS * 4 : 0;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1207,13 +1247,32 @@ int launch_cache_write(uint32_t blocks, void *stream, const CacheWriteArgs *a)
 uint64_t sharedkv_c8_workspace_bytes(uint32_t rows, uint32_t splits)
 {
     (void)splits;
-    return ((uint64_t)rows * 4 + 255) / 256 * 256;
+    return workspace_bytes(rows);
 }
 
-uint64_t sharedkv_c8_partial_bytes(uint32_t rows, uint32_t splits)
+uint64_t sharedkv_c8_partial_bytes(uint32_t rows, uint32_t splits) { return partial_bytes(rows, splits); }
+
+int launch_sharedkv_c8_noalloc(uint32_t blocks, void *stream, const SharedKVArgs *args)
 {
-    return splits > 1 ? (uint64_t)rows * splits * HEADS * PART_FLOATS * 4 : 0;
+    if (!blocks) return (int)hipSuccess;
+    if (!args) return (int)hipErrorInvalidValue;
+    if (args->heads == 0 || args->heads > MAX_HEADS || args->splits == 0 || args->splits > MAX_SPLITS)
+        return (int)hipErrorInvalidValue;
+    const uint64_t rows = (uint64_t)args->tokens * head_groups(args->heads);
+    if (rows > UINT32_MAX) return (int)hipErrorInvalidValue;
+    const uint64_t tickets = workspace_bytes((uint32_t)rows);
+    if (tickets + partial_bytes((uint32_t)rows, args->splits) > NOALLOC_SCRATCH_BYTES)
+        return (int)hipErrorInvalidValue;
+    void *base = nullptr;
+    const int e = scratch_address(&base);
+    if (e) return e;
+    SharedKVArgs a = *args;
+    a.workspace = (uint64_t)(uintptr_t)base;
+    a.partial = (uint64_t)(uintptr_t)base + tickets;
+    return launch_attention<false>(static_cast<hipStream_t>(stream), &a, nullptr);
 }
+
+uint64_t sharedkv_c8_noalloc_scratch_bytes(void) { return NOALLOC_SCRATCH_BYTES; }
 
 int sharedkv_c8_set_merge_mode(int mode)
 {

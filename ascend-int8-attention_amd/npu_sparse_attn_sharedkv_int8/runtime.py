@@ -43,9 +43,10 @@ class SharedKVDebug(ctypes.Structure):
 
 
 EXPORTS = ("launch_sharedkv_c8_sparse", "launch_sharedkv_c8_dense", "launch_sharedkv_c8_sparse_small",
-           "sharedkv_c8_attention_debug", "launch_cache_write", "sharedkv_c8_workspace_bytes",
-           "sharedkv_c8_partial_bytes", "sharedkv_c8_set_merge_mode", "sharedkv_attention_args_size",
-           "sharedkv_cache_args_size", "sharedkv_abi_version")
+           "launch_sharedkv_c8_noalloc", "sharedkv_c8_attention_debug", "launch_cache_write",
+           "sharedkv_c8_workspace_bytes", "sharedkv_c8_partial_bytes", "sharedkv_c8_noalloc_scratch_bytes",
+           "sharedkv_c8_set_merge_mode", "sharedkv_attention_args_size", "sharedkv_cache_args_size",
+           "sharedkv_abi_version")
 
 
 @lru_cache(maxsize=1)
@@ -60,7 +61,8 @@ def library():
     """
     import torch  # noqa: F401  (binds the library to torch's HIP runtime)
     lib = ctypes.CDLL(str(native_path()))
-    for name in ("launch_sharedkv_c8_sparse", "launch_sharedkv_c8_dense", "launch_sharedkv_c8_sparse_small"):
+    for name in ("launch_sharedkv_c8_sparse", "launch_sharedkv_c8_dense", "launch_sharedkv_c8_sparse_small",
+                 "launch_sharedkv_c8_noalloc"):
         fn = getattr(lib, name)
         fn.argtypes = [ctypes.c_uint32, ctypes.c_void_p, ctypes.c_void_p]
         fn.restype = ctypes.c_int
@@ -71,6 +73,8 @@ def library():
     for name in ("sharedkv_c8_workspace_bytes", "sharedkv_c8_partial_bytes"):
         getattr(lib, name).argtypes = [ctypes.c_uint32, ctypes.c_uint32]
         getattr(lib, name).restype = ctypes.c_uint64
+    lib.sharedkv_c8_noalloc_scratch_bytes.argtypes = []
+    lib.sharedkv_c8_noalloc_scratch_bytes.restype = ctypes.c_uint64
     lib.sharedkv_c8_set_merge_mode.argtypes = [ctypes.c_int]
     lib.sharedkv_c8_set_merge_mode.restype = ctypes.c_int
     for name in ("sharedkv_attention_args_size", "sharedkv_cache_args_size", "sharedkv_abi_version"):

@@ -107,6 +107,21 @@ int launch_cache_write(uint32_t blocks, void *stream, const CacheWriteArgs *args
 uint64_t sharedkv_c8_workspace_bytes(uint32_t rows, uint32_t splits);
 uint64_t sharedkv_c8_partial_bytes(uint32_t rows, uint32_t splits);
 
+/* Allocation-free attention launch.  No counterpart in the reference: it is
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * launch as launch_sharedkv_c8_sparse / _dense (ratio from args->ratio);
+ * args->workspace and args->partial are ignored: the merge tickets and
+ * partition states live in a library-owned array of
+ * sharedkv_c8_noalloc_scratch_bytes() (16 MiB) per GPU, located on the first
+ * call on each device (the stream's device must be current).  A launch
+ * whose workspace_bytes(rows) + partial_bytes(rows, splits) exceeds it is
+ * rejected with hipErrorInvalidValue.  The function calls no hipMalloc or
+ * hipFree.  Every call on one GPU uses that GPU's array: calls that may
+ * overlap on one GPU (other streams, other threads) race on it. */
+int launch_sharedkv_c8_noalloc(uint32_t blocks, void *stream, const SharedKVArgs *args);
+uint64_t sharedkv_c8_noalloc_scratch_bytes(void);
+
 /* Partition merge placement for launches with splits > 1 (process-wide).
  * Mode 0 (default): fused; the last partition of a query row to finish
  * (ticket in `workspace`) folds the row inside the attention launch.

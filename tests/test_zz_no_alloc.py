@@ -1,0 +1,81 @@
+"""The allocation-free attention entry point (launch_sharedkv_c8_noalloc)
+against the allocating one, through the C ABI.
+
+Two calls in a row on the library's per-GPU scratch array, the second with a
+smaller input, each bit-exact with launch_sharedkv_c8_sparse / _dense on the
+same arguments (output and LSE), in both merge placements; a launch whose
+tickets and partition states exceed the array is rejected before any work.
+"""
+import ctypes
+import sys
+
+import numpy as np
+import pytest
+
+from tests import workloads
+from tests.device_cases import bits_of, to_device
+
+pytestmark = pytest.mark.gpu
+
+
+def say(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def _launch_both(case, splits):
+    import torch
+    from npu_sparse_attn_sharedkv_int8 import PreparedAttention
+    from npu_sparse_attn_sharedkv_int8.runtime import library
+    lib = library()
+    dev, oscale, cscale, keep = to_device(case)
+    op = PreparedAttention(dev, oscale, cscale, splits=splits, return_lse=True)
+    op.run()
+    out2 = torch.full_like(op.out, float("nan"))
+    lse2 = torch.full_like(op.lse, float("nan"))
+    args = type(op.args).from_buffer_copy(op.args)
+    args.out, args.lse = out2.data_ptr(), lse2.data_ptr()
+    args.workspace = args.partial = 0          # ignored by the allocation-free entry
+    stream = torch.cuda.current_stream().cuda_stream
+    rc = lib.launch_sharedkv_c8_noalloc(max(1, op.blocks), ctypes.c_void_p(stream), ctypes.byref(args))
+    assert rc == 0, rc
+    torch.cuda.synchronize()
+    return (bits_of(op.out), op.lse.cpu().numpy()), (bits_of(out2), lse2.cpu().numpy()), keep
+
+
+@pytest.mark.parametrize("mode", [0, 1])
+def test_no_alloc_entry_equals_allocating_entry(mode):
+    from npu_sparse_attn_sharedkv_int8.runtime import library
+    lib = library()
+    big = workloads.make_case(71, 4, [2] * 20, list(range(3000, 3000 + 20 * 900, 900)), index_mode="mixed")
+    small = workloads.make_case(72, 128, [1, 2, 1], [900, 5000, 130])
+    try:
+        assert lib.sharedkv_c8_set_merge_mode(mode) == 0
+        for name, case, splits in (("40 C4 rows, 3 partitions", big, 3), ("4 C128 rows, 2 partitions", small, 2),
+                                   ("4 C128 rows, 1 partition", small, 1)):
+            say(f"[no-alloc] merge mode {mode}: {name}")
+            (ref, ref_lse), (got, got_lse), _ = _launch_both(case, splits)
+            assert np.array_equal(got, ref), name
+            assert np.array_equal(got_lse.view(np.uint32), ref_lse.view(np.uint32)), name
+    finally:
+        lib.sharedkv_c8_set_merge_mode(0)
+
+
+def test_no_alloc_entry_rejects_launches_past_its_scratch():
+    import torch
+    from npu_sparse_attn_sharedkv_int8 import PreparedAttention
+    from npu_sparse_attn_sharedkv_int8.runtime import library
+    lib = library()
+    limit = lib.sharedkv_c8_noalloc_scratch_bytes()
+    assert limit == 16 << 20
+    case = workloads.make_case(73, 4, [1, 1], [3000, 2000])
+    dev, oscale, cscale, keep = to_device(case)
+    op = PreparedAttention(dev, oscale, cscale, splits=2, return_lse=True)
+    args = type(op.args).from_buffer_copy(op.args)
+    per_row = 2 * 8 * 520 * 4
+    args.tokens = limit // per_row + 1          # partition states alone pass the limit
+    args.splits = 2
+    before = bits_of(op.out).copy()
+    stream = torch.cuda.current_stream().cuda_stream
+    assert lib.launch_sharedkv_c8_noalloc(1, ctypes.c_void_p(stream), ctypes.byref(args)) == 1
+    torch.cuda.synchronize()
+    assert np.array_equal(bits_of(op.out), before)
