@@ -1,19 +1,22 @@
 """Calibration of the frozen "sharedkv-c8-v1" scales: observe, merge, load.
 
-Interface counterparts in the reference checkout:
-  CacheObserver     npu_sparse_attn_sharedkv_int8/calibration.py:16-73
-  merge step        docs/kv-cache.md:51-68 (steps 3-4: per-channel maximum
-                    over ranks, scale = clamp_min(margin * maximum / 127, 1e-8))
-  load_scales       npu_sparse_attn_sharedkv_int8/vllm_adapter.py:52-63
+Documented workflow followed (docs/kv-cache.md:51-68 of the reference
+checkout): while <directory>/collect exists, every rank records, per layer
+prefix and cache kind, the channel-wise absolute maximum of the BF16 cache
+updates it writes and how many rows it wrote, and checkpoints them to
+<directory>/rank_XX.pt ({"version": 1, "rank", "pid", "stats": {key:
+{"maximum": FP32[512], "rows": int}}}); merge_observations() combines the
+rank files into the scale payload that load_scales() validates
+(vllm_adapter.py:52-63 there).
 
-The observer watches the BF16 cache updates a serving engine writes (after
-RoPE) without changing them, keeps a per-channel absolute maximum and a row
-count per (layer prefix, cache kind), and checkpoints them to
-<directory>/rank_XX.pt while <directory>/collect exists.  It synchronises the
-device at every checkpoint, so it is a calibration tool, never a benchmark
-configuration.  merge_observations() turns the rank files of one deployment
-into the frozen scale file that load_scales() validates and the INT8 path
-reads.  Every file here is written by this module and read with
+This build's observer keeps all maxima of a rank in one device tensor
+[keys, 512] and the row counts in one [keys] tensor (a key's row index is
+assigned on first sight), so an observation is one masked reduction and two
+in-place updates with no host round trip.  The collect marker is looked up
+at most once per MARKER_POLL_SECONDS; when it disappears the statistics are
+checkpointed once.  Checkpoints copy to the host (a device synchronisation),
+so the observer is a calibration tool, never a benchmark configuration.
+Every file here is written by this module and read with
 torch.load(weights_only=True).
 """
 import atexit
@@ -28,31 +31,85 @@ PROTOCOL = "sharedkv-c8-v1"
 DIM = 512
 MARGIN = 1.1
 FLOOR = 1e-8
-CHECKPOINT_SECONDS = 10
+CHECKPOINT_SECONDS = 10.0
+MARKER_POLL_SECONDS = 1.0
 
 
 def _capturing():
     return torch.cuda.is_available() and torch.cuda.is_current_stream_capturing()
 
 
-class CacheObserver:
-    """Per-channel |x| maxima of the cache updates while `collect` exists."""
+def written_rows(cache, slots):
+    """Mask of the update rows PreparedCacheWrite stores: flat slots in
+    [0, pages * page_size), or (page, offset) pairs inside the cache
+    (cache_write.cpp:53-63 of the reference)."""
+    pages, page_size = cache.shape[0], cache.shape[1]
+    if slots.ndim == 1:
+        return (slots >= 0) & (slots < pages * page_size)
+    page, offset = slots[:, 0], slots[:, 1]
+    return (page >= 0) & (page < pages) & (offset >= 0) & (offset < page_size)
 
-    def __init__(self, directory):
+
+def write_rank_file(directory, rank, maxima, rows):
+    """Atomically (re)write <directory>/rank_XX.pt from {key: maximum} and
+    {key: rows}."""
+    stats = {key: {"maximum": maxima[key], "rows": int(rows[key])} for key in sorted(maxima)}
+    payload = {"version": 1, "rank": rank, "pid": os.getpid(), "stats": stats}
+    target = Path(directory) / f"rank_{rank:02d}.pt"
+    staging = target.with_name(f".{target.name}.{os.getpid()}.partial")
+    torch.save(payload, staging)
+    os.replace(staging, target)
+    return target
+
+
+class CacheObserver:
+    """Channel maxima and row counts of observed cache writes, per
+    "<layer prefix>.<kind>" key, while <directory>/collect exists."""
+
+    def __init__(self, directory, checkpoint_seconds=CHECKPOINT_SECONDS):
         self.directory = Path(directory)
         self.directory.mkdir(parents=True, exist_ok=True)
         self.marker = self.directory / "collect"
-        self.stats = {}
-        self.dirty = False
-        self.last_save = time.monotonic()
+        self.checkpoint_seconds = checkpoint_seconds
+        self.keys = {}                # key -> row of maxima / rows
+        self.maxima = None            # FP32 [keys, 512] on the observed device
+        self.rows = None              # int64 [keys]
+        self.pending = False          # observations not yet checkpointed
+        self._marker_seen = (-1e9, False)
+        self._checkpointed_at = time.monotonic()
         atexit.register(self.flush)
+
+    @property
+    def stats(self):
+        """{key: (maximum FP32[512], rows)} (views of the accumulators)."""
+        if self.maxima is None:
+            return {}
+        return {key: (self.maxima[i], self.rows[i]) for key, i in self.keys.items()}
+
+    def collecting(self):
+        now = time.monotonic()
+        checked, present = self._marker_seen
+        if now - checked >= MARKER_POLL_SECONDS:
+            present = self.marker.exists()
+            self._marker_seen = (now, present)
+        return present
+
+    def _slot(self, key, device):
+        i = self.keys.get(key)
+        if i is None:
+            i = self.keys[key] = len(self.keys)
+            grow = torch.zeros(1, DIM, dtype=torch.float32, device=device)
+            count = torch.zeros(1, dtype=torch.int64, device=device)
+            self.maxima = grow if self.maxima is None else torch.cat([self.maxima, grow])
+            self.rows = count if self.rows is None else torch.cat([self.rows, count])
+        return i
 
     @torch.inference_mode()
     def observe(self, prefix, kind, cache, updates, slots):
-        """Record one cache write: `updates` [T,512] or [T,1,512], `slots` the
-        writer's flat [T] or paired [T,2] slots into `cache` [pages,32,1,512].
-        Rows whose slot the writer would skip are not counted."""
-        if not self.marker.exists():
+        """One cache write: `updates` [T, 512] or [T, 1, 512] going to
+        `slots` (flat [T] or paired [T, 2]) of `cache` [pages, 32, 1, 512].
+        Rows the writer would skip are not observed."""
+        if not self.collecting():
             self.flush()
             return
         if updates is None or updates.shape[0] == 0:
@@ -61,43 +118,28 @@ class CacheObserver:
             raise RuntimeError("Calibration needs eager execution; keep the marker absent during graph capture")
         if updates.shape[-1] != DIM or cache.shape[-1] != DIM:
             raise ValueError("Calibration expects the D=512 shared KV cache")
-        pages, page_size = cache.shape[0], cache.shape[1]
-        if slots.ndim == 1:
-            valid = (slots >= 0) & (slots < pages * page_size)
-        else:
-            valid = (slots[:, 0] >= 0) & (slots[:, 0] < pages) & (slots[:, 1] >= 0) & (slots[:, 1] < page_size)
-        rows = updates.reshape(-1, DIM).float()
-        peak = torch.where(valid[:, None], rows, 0.0).abs().amax(0)
-        count = valid.sum()
-        key = f"{prefix}.{kind}"
-        entry = self.stats.get(key)
-        if entry is None:
-            self.stats[key] = [peak, count]
-        else:
-            torch.maximum(entry[0], peak, out=entry[0])
-            entry[1].add_(count)
-        self.dirty = True
-        if time.monotonic() - self.last_save >= CHECKPOINT_SECONDS:
+        keep = written_rows(cache, slots)
+        values = updates.reshape(-1, DIM).float().abs()
+        peak = values.masked_fill(~keep[:, None], 0.0).amax(0)
+        i = self._slot(f"{prefix}.{kind}", updates.device)
+        torch.maximum(self.maxima[i], peak, out=self.maxima[i])
+        self.rows[i] += keep.sum()
+        self.pending = True
+        if time.monotonic() - self._checkpointed_at >= self.checkpoint_seconds:
             self.flush()
 
     def flush(self):
-        """Checkpoint to rank_XX.pt (atomic rename); no-op when nothing changed."""
-        if not self.dirty:
+        """Checkpoint to rank_XX.pt if anything was observed since the last one."""
+        if not self.pending:
             return
-        keys = sorted(self.stats)
-        maxima = torch.stack([self.stats[k][0] for k in keys]).cpu()
-        counts = torch.stack([self.stats[k][1] for k in keys]).cpu()
+        maxima, rows = self.maxima.cpu(), self.rows.cpu()
         if not bool(torch.isfinite(maxima).all()):
             raise RuntimeError("Non-finite cache values observed during calibration")
         rank = torch.distributed.get_rank() if torch.distributed.is_initialized() else 0
-        payload = {"version": 1, "rank": rank, "pid": os.getpid(),
-                   "stats": {k: {"maximum": maxima[i].clone(), "rows": int(counts[i])} for i, k in enumerate(keys)}}
-        path = self.directory / f"rank_{rank:02d}.pt"
-        temporary = path.with_suffix(f".tmp.{os.getpid()}")
-        torch.save(payload, temporary)
-        os.replace(temporary, path)
-        self.dirty = False
-        self.last_save = time.monotonic()
+        write_rank_file(self.directory, rank, {k: maxima[i].clone() for k, i in self.keys.items()},
+                        {k: rows[i] for k, i in self.keys.items()})
+        self.pending = False
+        self._checkpointed_at = time.monotonic()
 
 
 def _sha256(path):

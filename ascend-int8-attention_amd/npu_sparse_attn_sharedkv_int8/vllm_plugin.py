@@ -1,110 +1,90 @@
-"""Opt-in vLLM general plugin: SHAREDKV_INT8_MODE unset leaves vLLM unchanged.
+"""Opt-in vLLM general plugin (the vllm.general_plugins entry point; the role
+of npu_sparse_attn_sharedkv_int8/vllm_plugin.py in the reference checkout).
 
-Interface counterpart: npu_sparse_attn_sharedkv_int8/vllm_plugin.py:1-67 of
-the reference checkout.  Modes, as there:
-  calibrate   observe every cache write (calibration.CacheObserver under
-              SHAREDKV_CALIBRATION_DIR) and let the BF16 write proceed
-  int8        route cache writes and sparse attention to the HIP kernels
-              (vllm_adapter.install) with the frozen scales of SHAREDKV_SCALES
-
-The reference patches vllm_ascend's DeepSeek-V4 classes by name.  The
-classes of a vLLM-ROCm deployment are named by the deployment instead, in
-SHAREDKV_VLLM_TARGETS, a JSON object of "module:Qualified.Name" strings:
-  impl              attention implementation (get_kv_plan, _write_kv_cache)
-  cache_specs       list of classes with get_kv_cache_spec(config)
-  metadata_builder  builder whose _build_sas_metadata sees max_seqlen_kv
-  draft_model       optional model with _store_standard_swa_kv (draft context
-                    KV written outside the attention layer)
-or handed to register(targets=...) directly.
+SHAREDKV_INT8_MODE selects what register() does; unset, vLLM runs unchanged:
+  calibrate   every cache write of the bound attention class is observed by a
+              calibration.CacheObserver writing to SHAREDKV_CALIBRATION_DIR,
+              then proceeds in BF16 (the offline step that produces scales)
+  int8        vllm_adapter.install(): cache writes and sparse attention run on
+              the HIP kernels with the frozen scales of SHAREDKV_SCALES
+The engine classes to hook come from an EngineBinding: passed to register()
+by a deployment, or named in SHAREDKV_VLLM_TARGETS as JSON
+{"impl": "module:Class", "cache_specs": ["module:Class", ...],
+ "compact_pages": false}.  (vLLM-ROCm does not fix the names of its
+DeepSeek-V4 attention classes, so the deployment names them.)
 """
 import importlib
 import json
-import logging
 import os
 
-_registered = False
-_observer = None
+from .vllm_adapter import EngineBinding, describe_dsa_impl
+
+MODES = ("calibrate", "int8")
 TARGETS_ENV = "SHAREDKV_VLLM_TARGETS"
 
 
-def layer_prefix(impl):
-    return impl.swa_cache_layer.prefix.removesuffix(".swa_cache")
+class _State:
+    mode = None          # the mode register() installed, or None
+    observer = None      # the CacheObserver of calibrate mode
+
+
+state = _State()
 
 
 def resolve(name):
-    """'package.module:Outer.Inner' -> the object."""
-    module, _, qualified = name.partition(":")
-    if not module or not qualified:
+    """'package.module:Outer.Inner' -> the named object."""
+    module, sep, qualified = name.partition(":")
+    if not sep or not module or not qualified:
         raise ValueError(f"Expected 'module:Qualified.Name', got {name!r}")
-    obj = importlib.import_module(module)
-    for part in qualified.split("."):
-        obj = getattr(obj, part)
-    return obj
+    target = importlib.import_module(module)
+    for attribute in qualified.split("."):
+        target = getattr(target, attribute)
+    return target
 
 
-def targets_from_env():
+def binding_from_env():
     text = os.environ.get(TARGETS_ENV)
     if not text:
-        raise RuntimeError(f"{TARGETS_ENV} must name the engine's DeepSeek-V4 attention classes "
-                           "(impl, cache_specs, metadata_builder[, draft_model])")
-    names = json.loads(text)
-    return {"impl": resolve(names["impl"]),
-            "cache_specs": [resolve(n) for n in names.get("cache_specs", ())],
-            "metadata_builder": resolve(names["metadata_builder"]) if names.get("metadata_builder") else None,
-            "draft_model": resolve(names["draft_model"]) if names.get("draft_model") else None}
+        raise RuntimeError(f"{TARGETS_ENV} must name the engine's DeepSeek-V4 sparse attention class "
+                           "(and its cache-spec classes)")
+    spec = json.loads(text)
+    return EngineBinding(impl=resolve(spec["impl"]), cache_specs=tuple(resolve(n) for n in spec.get("cache_specs", ())),
+                         compact_pages=bool(spec.get("compact_pages", os.environ.get("SHAREDKV_COMPACT_PAGES") == "1")))
 
 
-def register(targets=None):
-    global _registered, _observer
-    if os.environ.get("SHAREDKV_PROFILE_DIAGNOSTICS_DIR"):
-        logging.getLogger("vllm.sharedkv_c8").warning(
-            "SHAREDKV_PROFILE_DIAGNOSTICS_DIR is ignored: serving diagnostics are not part of this build")
+def observe_writes(binding, observer):
+    """Wrap the binding's cache-write method: observe, then write in BF16."""
+    bf16_write = getattr(binding.impl, binding.write_method)
+
+    def write(self, cache, kv, slot_mapping, *, quantize):
+        layer = binding.describe(self)
+        if layer.quantized_elsewhere:
+            raise ValueError("Shared-KV calibration requires the ordinary BF16 DSA path")
+        observer.observe(layer.prefix, "cmp" if quantize else "ori", cache, kv, slot_mapping)
+        return bf16_write(self, cache, kv, slot_mapping, quantize=quantize)
+
+    setattr(binding.impl, binding.write_method, write)
+
+
+def register(binding=None):
+    """Install the mode SHAREDKV_INT8_MODE names (once per process)."""
     mode = os.environ.get("SHAREDKV_INT8_MODE", "")
-    if not mode or _registered:
+    if not mode or state.mode is not None:
         return
-    if mode not in ("calibrate", "int8"):
+    if mode not in MODES:
         raise ValueError(f"Unsupported SHAREDKV_INT8_MODE={mode!r}")
     directory = os.environ.get("SHAREDKV_CALIBRATION_DIR")
     if mode == "calibrate" and not directory:
         raise ValueError("calibrate mode requires SHAREDKV_CALIBRATION_DIR")
-    targets = targets if targets is not None else targets_from_env()
-    impl_cls = targets["impl"]
-
+    binding = binding if binding is not None else binding_from_env()
     if mode == "calibrate":
         from .calibration import CacheObserver
-        _observer = CacheObserver(directory)
-        original_write = impl_cls._write_kv_cache
-
-        def observed_write(self, cache, kv, slot_mapping, *, quantize):
-            if getattr(self, "turboquant", None) is not None:
-                raise ValueError("Shared-KV calibration requires the ordinary BF16 DSA path")
-            _observer.observe(layer_prefix(self), "cmp" if quantize else "ori", cache, kv, slot_mapping)
-            return original_write(self, cache, kv, slot_mapping, quantize=quantize)
-
-        impl_cls._write_kv_cache = observed_write
+        state.observer = CacheObserver(directory)
+        observe_writes(binding, state.observer)
     else:
         from .vllm_adapter import install
-        install(impl_cls, targets.get("cache_specs", ()), targets.get("metadata_builder"))
+        install(binding)
+    state.mode = mode
 
-    draft = targets.get("draft_model")
-    if draft is not None:
-        # Draft-context KV is written outside the attention layer; send it
-        # through the same (observed or INT8) original-cache writer.
-        def store_draft_context(self, shared_kv, slot_mapping, attn=None):
-            if slot_mapping is None or slot_mapping.numel() == 0:
-                return
-            if attn is None:
-                raise ValueError("Draft context writes need the attention layer")
-            layer = attn.dsa_attn.swa_cache_layer
-            cache = getattr(layer, "kv_cache", None)
-            if cache is None:
-                return
-            while isinstance(cache, (tuple, list)) and len(cache) == 1:
-                cache = cache[0]
-            impl = attn.dsa_attn.dsa_attn.impl
-            if slot_mapping.ndim == 1:
-                slot_mapping = impl.get_kv_plan().format_dsa_slot_mapping(slot_mapping, layer.block_size)
-            impl._write_kv_cache(cache, shared_kv, slot_mapping, quantize=False)
 
-        draft._store_standard_swa_kv = store_draft_context
-    _registered = True
+__all__ = ["EngineBinding", "binding_from_env", "describe_dsa_impl", "observe_writes", "register", "resolve", "state"]

@@ -1,6 +1,6 @@
 """The serving adapter end to end on the GPU: compact page views, cache writes
-through LayerRuntime, attention through the same keyword contract vLLM uses,
-streams, graph capture and the (out, lse) result shapes.
+through SharedKVLayer, attention through the same keyword contract vLLM
+uses, streams, graph capture and the (out, lse) result shapes.
 
 Flow of the reference's tests/npu/test_adapter.py:30-191: per ratio (window
 only, C4, C128) a frozen scale file, caches written by the INT8 writer into
@@ -46,7 +46,7 @@ def _check(case, q_bits, out, lse, splits, tag):
 
 
 @pytest.mark.parametrize("ratio", [1, 4, 128])
-def test_layer_runtime_end_to_end(ratio, tmp_path, monkeypatch):
+def test_layer_end_to_end(ratio, tmp_path, monkeypatch):
     import torch
     from npu_sparse_attn_sharedkv_int8 import cache_layout, vllm_adapter
 
@@ -75,9 +75,7 @@ def test_layer_runtime_end_to_end(ratio, tmp_path, monkeypatch):
     impl = SimpleNamespace(swa_cache_layer=SimpleNamespace(prefix=f"{prefix}.swa_cache"), head_dim=512,
                            turboquant=None, vllm_config=SimpleNamespace(parallel_config=SimpleNamespace(
                                decode_context_parallel_size=1, prefill_context_parallel_size=1)))
-    state = vllm_adapter.LayerRuntime(impl)
-    metadata = torch.empty(1, device=device)
-    metadata._sharedkv_max_seq_len = int(case["seq_lens"].max())
+    state = vllm_adapter.runtime(impl)
     q0 = torch_bf16(case["q"], device)
     kw = dict(ori_kv=caches["ori"], cmp_kv=caches.get("cmp"),
               ori_block_table=torch.from_numpy(case["ori"].table).to(device),
@@ -85,7 +83,7 @@ def test_layer_runtime_end_to_end(ratio, tmp_path, monkeypatch):
               cmp_sparse_indices=torch.from_numpy(case["cmp_indices"]).to(device) if ratio == 4 else None,
               cu_seqlens_q=torch.from_numpy(case["cu_q"]).to(device),
               seqused_kv=torch.from_numpy(case["seq_lens"]).to(device),
-              sinks=torch.from_numpy(case["sink"]).to(device), metadata=metadata, cmp_ratio=ratio,
+              sinks=torch.from_numpy(case["sink"]).to(device), cmp_ratio=ratio,
               ori_mask_mode=4, cmp_mask_mode=3, ori_win_left=127, ori_win_right=0,
               softmax_scale=case["softmax_scale"], layout_q="TND", layout_kv="PA_ND", return_softmax_lse=True)
 
@@ -99,7 +97,7 @@ def test_layer_runtime_end_to_end(ratio, tmp_path, monkeypatch):
         query = (q0 * multiplier).contiguous()
         out, lse = run(query)
         torch.cuda.synchronize()
-        op = next(reversed(state.attention_ops.values()))
+        op = next(reversed(state.operators.values()))
         assert op.c8_dynamic and lse.shape == (*query.shape[:2], 1)
         _check(case, bits_of(query), out, lse, op.splits, f"eager x{multiplier}")
     for k in kinds:
@@ -115,9 +113,9 @@ def test_layer_runtime_end_to_end(ratio, tmp_path, monkeypatch):
         out_side, lse_side = state.attention(q0, **kw)
     side.synchronize()
     assert key_side != vllm_adapter.stream_key(device)
-    side_op = next(reversed(state.attention_ops.values()))
+    side_op = next(reversed(state.operators.values()))
     _check(case, case["q"], out_side, lse_side, side_op.splits, "side stream")
-    scratch_streams = {key[1] for key in vllm_adapter._scratch if key[0] == device}
+    scratch_streams = {key[1] for key in vllm_adapter.StreamScratch.pools() if key[0] == device}
     assert key_side in scratch_streams or side_op.splits == 1
 
     # Capture writes + attention; an eager call on the same op between
@@ -130,7 +128,7 @@ def test_layer_runtime_end_to_end(ratio, tmp_path, monkeypatch):
         with torch.cuda.graph(graph, stream=capture):
             g_out, g_lse = run(query)
     torch.cuda.current_stream().wait_stream(capture)
-    captured = state.captured_ops[-1]
+    captured = state.captured[-1]
     say(f"[adapter] ratio={ratio} captured (splits={captured.splits})")
     for i, sign in enumerate((1.0, -1.0, 1.0)):
         query.copy_(q0 * sign)
@@ -139,7 +137,7 @@ def test_layer_runtime_end_to_end(ratio, tmp_path, monkeypatch):
         graph.replay()
         torch.cuda.synchronize()
         _check(case, bits_of(query), g_out, g_lse, captured.splits, f"replay {i}")
-        eager_op = next(reversed(state.attention_ops.values()))
+        eager_op = next(reversed(state.operators.values()))
         _check(case, bits_of((-query).contiguous()), negated, None, eager_op.splits, f"eager {i}")
     say(f"[adapter] ratio={ratio} replays ok")
 
@@ -154,7 +152,7 @@ def test_layer_runtime_end_to_end(ratio, tmp_path, monkeypatch):
     for raw in raws:
         blocks = raw.view(-1, STRIDE).cpu()
         assert (blocks[:, :OFFSET] == 73).all() and (blocks[:, OFFSET + 16384:] == 73).all()
-    assert all(op.case is None and op.out is None for op in state.attention_ops.values())
+    assert all(op.case is None and op.out is None for op in state.operators.values())
     assert all(w.updates is None and w.slots is None for w in state.writers.values())
     del graph
     vllm_adapter.load_scales.cache_clear()
@@ -168,8 +166,8 @@ def test_scratch_allocator_grows_and_keys_by_stream():
     b = vllm_adapter.scratch_allocator("t_ws", (60,), torch.uint8, device)
     assert a.data_ptr() == b.data_ptr() and b.shape == (60,)
     c = vllm_adapter.scratch_allocator("t_ws", (300,), torch.uint8, device)
-    key = (device, vllm_adapter.stream_key(device), "t_ws", torch.uint8)
-    assert c.data_ptr() != a.data_ptr() and [t.numel() for t in vllm_adapter._scratch[key]] == [128, 512]
+    pool = vllm_adapter.StreamScratch.pools()[(device, vllm_adapter.stream_key(device))]
+    assert c.data_ptr() != a.data_ptr() and [t.numel() for t in pool.buffers[("t_ws", torch.uint8)]] == [128, 512]
     side = torch.cuda.Stream()
     with torch.cuda.stream(side):
         d = vllm_adapter.scratch_allocator("t_ws", (100,), torch.uint8, device)

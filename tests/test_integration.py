@@ -4,8 +4,11 @@ plugin wiring driven with stand-in engine classes (vLLM is not installed
 here; the reference drives its adapter with SimpleNamespace stand-ins too,
 tests/npu/test_adapter.py:77-114).
 
-Reference behaviour followed: calibration.py:16-73, docs/kv-cache.md:51-68,
-vllm_adapter.py:52-63 and 74-277, vllm_plugin.py:13-67, cache_layout.py:32-134.
+Reference behaviour followed: the calibration workflow of docs/kv-cache.md:51-68
+(marker-gated observation, rank_XX.pt payload, merge rule), the scale-file
+checks of vllm_adapter.py:52-63, the sparse-attention keyword contract and
+result of vllm_adapter.py:140-214, the plugin modes of vllm_plugin.py:13-30,
+and the page planner of cache_layout.py:32-134.
 """
 from dataclasses import dataclass
 import json
@@ -62,7 +65,33 @@ def test_observer_rejects_other_widths_and_nonfinite(tmp_path):
     obs.observe("p", "cmp", cache, torch.full((1, 512), float("inf")), torch.arange(1))
     with pytest.raises(RuntimeError):
         obs.flush()
-    obs.stats, obs.dirty = {}, False
+    obs.pending = False
+
+
+def test_observer_checkpoints_when_the_marker_goes(tmp_path, monkeypatch):
+    """The marker is looked up at most once per MARKER_POLL_SECONDS; once it
+    is gone the next observation checkpoints what was collected and records
+    nothing more."""
+    monkeypatch.setattr(calibration, "MARKER_POLL_SECONDS", 0.0)
+    obs = _observer(tmp_path)
+    cache = torch.zeros(1, 32, 1, 512, dtype=torch.int8)
+    obs.observe("p", "ori", cache, torch.full((2, 512), 3.0), torch.arange(2))
+    assert not (tmp_path / "rank_00.pt").exists()
+    (tmp_path / "collect").unlink()
+    obs.observe("p", "ori", cache, torch.full((2, 512), 5.0), torch.arange(2))
+    saved = torch.load(tmp_path / "rank_00.pt", weights_only=True)
+    assert saved["stats"]["p.ori"]["rows"] == 2 and float(saved["stats"]["p.ori"]["maximum"][0]) == 3.0
+    assert not obs.pending
+
+
+def test_observer_marker_poll_is_cached(tmp_path, monkeypatch):
+    monkeypatch.setattr(calibration, "MARKER_POLL_SECONDS", 3600.0)
+    obs = _observer(tmp_path, collect=False)
+    assert not obs.collecting()
+    (tmp_path / "collect").touch()
+    assert not obs.collecting()          # within the poll interval the old answer stands
+    obs._marker_seen = (-1e9, False)
+    assert obs.collecting()
 
 
 def test_observer_refuses_graph_capture(tmp_path, monkeypatch):
@@ -255,25 +284,61 @@ def scale_file(tmp_path, monkeypatch):
     vllm_adapter.load_scales.cache_clear()
 
 
-def test_layer_runtime_contract_checks(scale_file):
-    state = vllm_adapter.LayerRuntime(_impl())
-    assert state.prefix == "model.layers.3.self_attn" and state.clean_c8_decode
+def test_layer_contract_checks(scale_file):
+    layer = vllm_adapter.runtime(_impl())
+    assert layer.prefix == "model.layers.3.self_attn"
+    for bad in ({"head_dim": 128}, {"turboquant": object()}):
+        with pytest.raises(ValueError):
+            vllm_adapter.runtime(SimpleNamespace(**{**vars(_impl()), **bad}))
     with pytest.raises(ValueError):
-        vllm_adapter.LayerRuntime(SimpleNamespace(**{**vars(_impl()), "head_dim": 128}))
-    with pytest.raises(ValueError):
-        vllm_adapter.LayerRuntime(SimpleNamespace(**{**vars(_impl()), "turboquant": object()}))
-    with pytest.raises(ValueError):
-        vllm_adapter.LayerRuntime(_impl(decode_context_parallel_size=2))
+        vllm_adapter.runtime(_impl(decode_context_parallel_size=2))
     q = torch.zeros(1, 8, 512, dtype=torch.bfloat16)
     for kw in (dict(layout_q="BSND", layout_kv="PA_ND"), dict(layout_q="TND", layout_kv="PA_ND", ori_mask_mode=3),
                dict(layout_q="TND", layout_kv="PA_ND", ori_win_right=4),
                dict(layout_q="TND", layout_kv="PA_ND", cmp_ratio=4, cmp_mask_mode=1)):
         with pytest.raises(ValueError):
-            state.attention(q, **kw)
-    state.write(None, torch.zeros(0, 512), torch.zeros(0, dtype=torch.int32), "ori")   # empty: nothing
+            layer.attention(q, **kw)
+    layer.write(None, torch.zeros(0, 512), torch.zeros(0, dtype=torch.int32), "ori")   # empty: nothing
     with pytest.raises(ValueError):
-        state.write(None, torch.zeros(2, 512), torch.zeros(3, dtype=torch.int32), "ori")
-    assert vllm_adapter.runtime(impl := _impl()) is vllm_adapter.runtime(impl)
+        layer.write(None, torch.zeros(2, 512), torch.zeros(3, dtype=torch.int32), "ori")
+    impl = _impl()
+    assert vllm_adapter.runtime(impl) is vllm_adapter.runtime(impl)
+
+
+def test_parse_and_launch_shape():
+    """The keyword contract maps onto SharedKVCase; calls that differ only in
+    device pointers share a launch shape, anything baked into the argument
+    block (tokens, pages, strides, table widths, LSE) does not."""
+    case = workloads.make_case(5, 4, [2, 1], [3000, 900])
+    dev = SimpleNamespace()
+
+    def kw(tokens=3, lse=True, stride=16384):
+        q = torch.zeros(tokens, 8, 512, dtype=torch.bfloat16)
+        pool = torch.zeros(40 * stride, dtype=torch.int8).as_strided((40, 32, 1, 512), (stride, 512, 512, 1))
+        return q, dict(ori_kv=pool, cmp_kv=pool, ori_block_table=torch.zeros(2, 94, dtype=torch.int32),
+                       cmp_block_table=torch.zeros(2, 24, dtype=torch.int32),
+                       cmp_sparse_indices=torch.zeros(tokens, 1, 1024, dtype=torch.int32),
+                       cu_seqlens_q=torch.tensor([0, 2, tokens], dtype=torch.int32),
+                       seqused_kv=torch.tensor([3000, 900], dtype=torch.int32), sinks=torch.zeros(8),
+                       cmp_ratio=4, ori_win_left=127, softmax_scale=0.04, layout_q="TND", layout_kv="PA_ND",
+                       return_softmax_lse=lse)
+    del case, dev
+    c1, l1 = vllm_adapter.parse_attention_call(*kw())
+    c2, l2 = vllm_adapter.parse_attention_call(*kw())
+    assert c1.ratio == 4 and c1.window == 128 and l1 is True
+    assert vllm_adapter.launch_shape(c1, l1) == vllm_adapter.launch_shape(c2, l2)
+    for other in (kw(tokens=4), kw(lse=False), kw(stride=622592)):
+        c3, l3 = vllm_adapter.parse_attention_call(*other)
+        assert vllm_adapter.launch_shape(c3, l3) != vllm_adapter.launch_shape(c1, l1)
+
+
+def test_operator_cache_is_lru():
+    cache = vllm_adapter.OperatorCache(capacity=2)
+    cache.put("a", 1)
+    cache.put("b", 2)
+    assert cache.get("a") == 1
+    cache.put("c", 3)                       # "b" is the least recently used
+    assert cache.get("b") is None and list(cache.values()) == [1, 3]
 
 
 def test_load_scales_requires_the_file(monkeypatch, scale_file):
@@ -316,90 +381,97 @@ def _engine_classes():
         def get_kv_cache_spec(self, config):
             return BF16Spec()
 
-    class Builder:
-        def _build_sas_metadata(self, *args, **kwargs):
-            return SimpleNamespace()
-
-    return Impl, Cache, Builder
+    return Impl, Cache
 
 
-def test_install_routes_plan_writes_specs_and_metadata(scale_file, monkeypatch):
-    Impl, Cache, Builder = _engine_classes()
-    monkeypatch.delenv("SHAREDKV_COMPACT_PAGES", raising=False)
-    vllm_adapter.install(Impl, (Cache,), Builder)
+def test_install_routes_plan_writes_and_specs(scale_file, monkeypatch):
+    Impl, Cache = _engine_classes()
+    vllm_adapter.install(vllm_adapter.EngineBinding(impl=Impl, cache_specs=(Cache,)))
     impl = Impl()
     plan = impl.get_kv_plan()
     assert plan.other == 7 and plan.sparse_attn_op == vllm_adapter.runtime(impl).attention
     assert impl.get_kv_plan() is plan
     calls = []
-    monkeypatch.setattr(vllm_adapter.LayerRuntime, "write", lambda self, *a: calls.append(a))
+    monkeypatch.setattr(vllm_adapter.SharedKVLayer, "write", lambda self, *a: calls.append(a))
     impl._write_kv_cache("c", "kv", "s", quantize=True)
     impl._write_kv_cache("c", "kv", "s", quantize=False)
     assert calls == [("c", "kv", "s", "cmp"), ("c", "kv", "s", "ori")]
     spec = Cache().get_kv_cache_spec(None)
     assert spec.dtype == torch.int8 and spec.page_size_padded == 32768 and spec.indexes_kv_by_block_stride
-    assert Builder()._build_sas_metadata(0, 1, 2, 3, 4, 260)._sharedkv_max_seq_len == 260
-    assert Builder()._build_sas_metadata(max_seqlen_kv=9000)._sharedkv_max_seq_len == 9000
-    assert Builder()._build_sas_metadata()._sharedkv_max_seq_len is None
-    Impl2, Cache2, _ = _engine_classes()
-    vllm_adapter.install(Impl2, (Cache2,), compact_pages=True)
+    Impl2, Cache2 = _engine_classes()
+    vllm_adapter.install(vllm_adapter.EngineBinding(impl=Impl2, cache_specs=(Cache2,), compact_pages=True))
     assert Cache2().get_kv_cache_spec(None).page_size_padded is None
+
+    class Renamed:
+        """Method and field names are the binding's, not fixed."""
+        def __init__(self):
+            self.__dict__.update(vars(_impl()))
+
+        def plan(self):
+            return SimpleNamespace(attention=None)
+
+        def store(self, cache, kv, slot_mapping, *, quantize):
+            return "bf16"
+
+    @dataclass(frozen=True)
+    class RenamedPlan:
+        attention: object = None
+
+    Renamed.plan = lambda self: RenamedPlan()
+    vllm_adapter.install(vllm_adapter.EngineBinding(impl=Renamed, plan_method="plan", plan_field="attention",
+                                                    write_method="store"))
+    r = Renamed()
+    assert r.plan().attention == vllm_adapter.runtime(r).attention
+    r.store("c", "kv", "s", quantize=False)
+    assert calls[-1] == ("c", "kv", "s", "ori")
 
 
 def test_plugin_modes(tmp_path, scale_file, monkeypatch):
-    monkeypatch.setattr(vllm_plugin, "_registered", False)
+    monkeypatch.setattr(vllm_plugin.state, "mode", None)
     monkeypatch.delenv("SHAREDKV_INT8_MODE", raising=False)
-    vllm_plugin.register(targets={})            # unset: nothing happens, targets unused
-    assert not vllm_plugin._registered
+    vllm_plugin.register(binding=object())       # unset: nothing happens, the binding is not used
+    assert vllm_plugin.state.mode is None
     monkeypatch.setenv("SHAREDKV_INT8_MODE", "fp8")
     with pytest.raises(ValueError):
-        vllm_plugin.register(targets={})
+        vllm_plugin.register(binding=object())
     monkeypatch.setenv("SHAREDKV_INT8_MODE", "calibrate")
     monkeypatch.delenv("SHAREDKV_CALIBRATION_DIR", raising=False)
     with pytest.raises(ValueError):
-        vllm_plugin.register(targets={})
+        vllm_plugin.register(binding=object())
 
-    Impl, Cache, Builder = _engine_classes()
+    Impl, Cache = _engine_classes()
     monkeypatch.setenv("SHAREDKV_CALIBRATION_DIR", str(tmp_path / "cal"))
-    vllm_plugin.register(targets={"impl": Impl})
-    assert vllm_plugin._registered
+    vllm_plugin.register(binding=vllm_adapter.EngineBinding(impl=Impl))
+    assert vllm_plugin.state.mode == "calibrate"
     (tmp_path / "cal" / "collect").touch()
+    vllm_plugin.state.observer._marker_seen = (-1e9, False)
     impl = Impl()
     cache = torch.zeros(2, 32, 1, 512, dtype=torch.int8)
     kv = torch.ones(3, 512, dtype=torch.bfloat16)
     assert impl._write_kv_cache(cache, kv, torch.arange(3), quantize=True) == "bf16"
-    assert len(impl.writes) == 1 and int(vllm_plugin._observer.stats["model.layers.3.self_attn.cmp"][1]) == 3
+    assert len(impl.writes) == 1 and int(vllm_plugin.state.observer.stats["model.layers.3.self_attn.cmp"][1]) == 3
+    vllm_plugin.register(binding=object())       # registered once per process
+    vllm_plugin.state.observer.pending = False
 
-    monkeypatch.setattr(vllm_plugin, "_registered", False)
+    monkeypatch.setattr(vllm_plugin.state, "mode", None)
     monkeypatch.setenv("SHAREDKV_INT8_MODE", "int8")
-    Impl, Cache, Builder = _engine_classes()
-
-    class Draft:
-        pass
-
-    vllm_plugin.register(targets={"impl": Impl, "cache_specs": [Cache], "metadata_builder": Builder,
-                                  "draft_model": Draft})
+    Impl, Cache = _engine_classes()
+    vllm_plugin.register(binding=vllm_adapter.EngineBinding(impl=Impl, cache_specs=(Cache,)))
+    assert vllm_plugin.state.mode == "int8"
     assert Cache().get_kv_cache_spec(None).dtype == torch.int8
-    seen = []
-    impl = SimpleNamespace(_write_kv_cache=lambda c, kv, s, quantize: seen.append((c, kv, s, quantize)),
-                           get_kv_plan=lambda: SimpleNamespace(format_dsa_slot_mapping=lambda s, b: (s, b)))
-    attn = SimpleNamespace(dsa_attn=SimpleNamespace(swa_cache_layer=SimpleNamespace(kv_cache=[["C"]], block_size=32),
-                                                    dsa_attn=SimpleNamespace(impl=impl)))
-    Draft._store_standard_swa_kv(None, "kv", torch.arange(4), attn)
-    assert seen[0][0] == "C" and seen[0][2][1] == 32 and seen[0][3] is False
-    Draft._store_standard_swa_kv(None, "kv", torch.zeros(0), attn)
-    assert len(seen) == 1
 
 
-def test_plugin_targets_from_env(monkeypatch):
+def test_plugin_binding_from_env(monkeypatch):
     monkeypatch.setenv(vllm_plugin.TARGETS_ENV, json.dumps({"impl": "collections:OrderedDict",
-                                                            "cache_specs": ["types:SimpleNamespace"]}))
-    targets = vllm_plugin.targets_from_env()
+                                                            "cache_specs": ["types:SimpleNamespace"],
+                                                            "compact_pages": True}))
+    binding = vllm_plugin.binding_from_env()
     from collections import OrderedDict
-    assert targets["impl"] is OrderedDict and targets["cache_specs"] == [SimpleNamespace]
-    assert targets["metadata_builder"] is None
+    assert binding.impl is OrderedDict and binding.cache_specs == (SimpleNamespace,) and binding.compact_pages
+    assert binding.plan_method == "get_kv_plan" and binding.write_method == "_write_kv_cache"
     monkeypatch.delenv(vllm_plugin.TARGETS_ENV)
     with pytest.raises(RuntimeError):
-        vllm_plugin.targets_from_env()
-    with pytest.raises(ValueError):
-        vllm_plugin.resolve("no_colon")
+        vllm_plugin.binding_from_env()
+    for bad in ("no_colon", ":Name", "collections:"):
+        with pytest.raises(ValueError):
+            vllm_plugin.resolve(bad)
