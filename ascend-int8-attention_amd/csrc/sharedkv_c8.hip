@@ -52,6 +52,10 @@ constexpr int D = 512;
 constexpr int HEADS = 8;               // heads per work-group (one MFMA row block with residual rows)
 constexpr int MAX_HEADS = 128;
 constexpr int N = SHAREDKV_C8_TILE;    // keys per tile
+// Partition plan of a launch's live rows (the host's choose_splits rule):
+// PLAN_FEW partitions while rows x PLAN_FEW work-groups fit the PLAN_CUS
+// compute units, else PLAN_MANY.
+constexpr int32_t PLAN_CUS = 256, PLAN_FEW = 5, PLAN_MANY = 3;
 constexpr int THREADS = 512;           // 8 waves: two per SIMD
 constexpr int WAVES = THREADS / 64;
 constexpr int PROW = N + 16;           // LDS row stride of the P codes
@@ -368,7 +372,7 @@ template <int RATIO, bool DEBUG, bool SLOTS, bool ANYH>
 __global__ void __launch_bounds__(THREADS, 1)   // one work-group per CU: the 128 KiB tile ring fills the LDS
 c8_attention(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, const uint64_t cmp_indices,
              const uint32_t batch_arg, const uint32_t topk_arg, const uint32_t heads_arg, const uint32_t splits,
-             const uint32_t items, const uint32_t grid, const SharedKVArgs p, const SharedKVDebug dbg,
+             const uint32_t rows_arg, const uint32_t grid, const SharedKVArgs p, const SharedKVDebug dbg,
              const uint32_t fused)
 {
     __shared__ Shared s;
@@ -378,20 +382,24 @@ c8_attention(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base
     // then the next row) stay on one XCD and share its L2.
     const uint32_t G = grid;
     const uint32_t item = (blockIdx.x & 7u) * (G >> 3) + (blockIdx.x >> 3);
+    const uint32_t items = rows_arg * splits;
     if (item >= items) return;
     const int H = ANYH ? (int)heads_arg : HEADS;                 // heads of a query token
     const int HG = ANYH ? (H + HEADS - 1) / HEADS : 1;           // groups of eight
     const bool resid = !ANYH || H <= HEADS;
-    const int32_t qrow = (int32_t)(item / splits);               // (token, head group)
-    const int32_t t = ANYH ? qrow / HG : qrow;
-    const int32_t hbase = ANYH ? HEADS * (qrow % HG) : 0;
-    const int hlive = ANYH ? (H - hbase < HEADS ? H - hbase : HEADS) : HEADS;
-    const int32_t part = (int32_t)(item % splits);
-    const int32_t S = (int32_t)splits;
+    // The launch's plan: `splits` partitions per row over rows_arg rows.
+    // rows.  The work item's row under that plan is loaded at once; with
+    // graph padding the device re-plans (below) and may move it.
+    int32_t S = (int32_t)splits;
+    int32_t qrow = (int32_t)(item / splits);                     // (token, head group)
+    int32_t t = ANYH ? qrow / HG : qrow;
+    int32_t hbase = ANYH ? HEADS * (qrow % HG) : 0;
+    int hlive = ANYH ? (H - hbase < HEADS ? H - hbase : HEADS) : HEADS;
+    int32_t part = (int32_t)(item % splits);
 
     // ---- prologue: the loads the selection needs, issued together ----
     // cu_q, seq_lens, q_base, cmp_indices, batch_arg, topk_arg, heads_arg,
-    // splits, items and grid are the leading kernel arguments (copies of
+    // splits, rows_arg and grid are the leading kernel arguments (copies of
     // argument-block fields) that arrive preloaded in SGPRs.
     const __attribute__((address_space(1))) int32_t *cu = gptr<int32_t>(cu_q);
     const __attribute__((address_space(1))) int32_t *lens = gptr<int32_t>(seq_lens);
@@ -415,8 +423,10 @@ c8_attention(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base
             if (tid * 2 + i < topk) ix[i] = row_ix[tid * 2 + i];
     }
 
-    // ---- live shape (attention_impl.h:121-137) and the row's request ----
-    if (tid == 0) { s.misc[0] = 0; s.misc[1] = -1; s.misc[2] = 0; }
+    // ---- live shape (attention_impl.h:121-137) ----
+    // The last request with seq_len > 0 and cu_q >= 0 ends the live batch;
+    // its cu_q end bounds the live tokens.
+    if (tid == 0) { s.misc[0] = 0; s.misc[1] = -1; s.misc[2] = 0; s.misc[6] = 0; }
     __syncthreads();
     for (int b = tid; b < batch_n; b += THREADS) {
         const int len = b == tid ? my_len : lens[b];
@@ -425,24 +435,91 @@ c8_attention(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base
     }
     __syncthreads();
     const int live_batch = uni(s.misc[0]);
-    for (int b = tid; b < batch_n; b += THREADS) {
-        const int c0 = b == tid ? my_cu0 : cu[b];
-        const int c1 = b == tid ? my_cu1 : cu[b + 1];
-        const int len = b == tid ? my_len : lens[b];
-        if (b == live_batch - 1) s.misc[2] = c1;
-        if (b < live_batch && c0 <= t && t < c1) {
-            s.misc[1] = b;
-            s.misc[3] = len;
-            s.misc[4] = c1;
+    // The live end and the request holding token t of the launch plan's row.
+    auto find_request = [&](int token, bool first) {
+        for (int b = tid; b < live_batch; b += THREADS) {
+            const int c0 = b == tid ? my_cu0 : cu[b];
+            const int c1 = b == tid ? my_cu1 : cu[b + 1];
+            const int len = b == tid ? my_len : lens[b];
+            if (c0 <= token && token < c1) {
+                s.misc[1] = b;
+                s.misc[3] = len;
+                s.misc[4] = c1;
+            }
+            if (first && b == live_batch - 1) s.misc[2] = c1;
+        }
+        __syncthreads();
+    };
+    find_request(t, true);
+    const int end = live_batch ? uni(s.misc[2]) : 0;
+    const int live_tokens = end <= 0 ? 0 : (end < (int)p.tokens ? end : (int)p.tokens);
+
+    // ---- device plan (c4_wide.h:16-41 of the reference chooses from the
+    // live shape too) ----  When graph padding leaves live rows below the
+    // launch's capacity, the idle work items become more partitions of the
+    // live rows: the host's rule for an eager launch of that many rows (5
+    // partitions while rows x 5 fit the CUs, else 3, at most CUs / rows and
+    // the longest live row's tile count), capped by items / live rows and
+    // never below the launch's own plan.  Each work item also zero-fills one
+    // padding row.  The rule is c8_attention.device_splits on the host; the
+    // separate merge launch (not fused) keeps the launch plan.
+    const int32_t rows_cap = (int32_t)rows_arg;
+    const int32_t live_rows = live_tokens * HG;
+    if (fused && live_rows < rows_cap) {
+        const int32_t pad = live_rows + (int32_t)item;
+        if (pad < rows_cap) {   // zero-fill padding row `pad` (attention_impl.h:443-460)
+            const int32_t pt = ANYH ? pad / HG : pad, ph = ANYH ? HEADS * (pad % HG) : 0;
+            const int pl = ANYH ? (H - ph < HEADS ? H - ph : HEADS) : HEADS;
+            uint16_t *o = reinterpret_cast<uint16_t *>(p.out) + ((int64_t)pt * H + ph) * D;
+            if (!ANYH || tid < pl * (D / 8)) reinterpret_cast<v4i *>(o)[tid] = v4i{0, 0, 0, 0};
+            if (p.lse && tid < pl) reinterpret_cast<float *>(p.lse)[(int64_t)pt * H + ph + tid] = 0.0f;
+        }
+        if (live_rows == 0) return;
+        // The longest live sequence bounds the rows' tile counts.
+        for (int b = tid; b < live_batch; b += THREADS) atomicMax(&s.misc[6], b == tid ? my_len : lens[b]);
+        __syncthreads();
+        const int longest = uni(s.misc[6]);
+        int tiles = SLOTS ? ((int)p.oriTopk + N - 1) / N : 1;
+        if (RATIO == 4) {
+            const int cnt = longest / 4 < (int)topk_arg ? longest / 4 : (int)topk_arg;
+            tiles += (cnt + N - 1) / N;
+        } else if (RATIO == 128) {
+            tiles += (longest / 128 + N - 1) / N;
+        }
+        int32_t plan = live_rows * PLAN_FEW <= PLAN_CUS ? PLAN_FEW : PLAN_MANY;
+        const int32_t fit = PLAN_CUS / live_rows > 1 ? PLAN_CUS / live_rows : 1;
+        const int32_t room = (int32_t)(items / (uint32_t)live_rows);
+        plan = plan < fit ? plan : fit;
+        plan = plan < tiles ? plan : tiles;
+        plan = plan < room ? plan : room;
+        plan = plan > S ? plan : S;
+        if (item >= (uint32_t)(live_rows * plan)) return;
+        const int32_t row = (int32_t)(item / (uint32_t)plan);
+        S = plan;
+        part = (int32_t)(item % (uint32_t)plan);
+        if (row != qrow) {
+            // The work item moved to another row: load that row's Q and indices.
+            qrow = row;
+            t = ANYH ? qrow / HG : qrow;
+            hbase = ANYH ? HEADS * (qrow % HG) : 0;
+            hlive = ANYH ? (H - hbase < HEADS ? H - hbase : HEADS) : HEADS;
+            qv = v4i{0, 0, 0, 0};
+            if (!ANYH || wave < hlive) qv = *gptr<v4i>(q_base + (((uint64_t)t * H + hbase + wave) * D + qd0) * 2);
+            if (RATIO == 4) {
+                const int topk = (int)topk_arg;
+                const __attribute__((address_space(1))) int32_t *row_ix = gptr<int32_t>(cmp_indices) + (int64_t)t * topk;
+#pragma unroll
+                for (int i = 0; i < 2; ++i) ix[i] = tid * 2 + i < topk ? row_ix[tid * 2 + i] : -1;
+            }
+            if (tid == 0) s.misc[1] = -1;
+            __syncthreads();
+            find_request(t, false);
         }
     }
-    __syncthreads();
     // Every metadata load has landed: said explicitly (vmcnt(0)) so that the
     // compiler's own wait tracking does not hold back the block-table reads
     // issued next for these registers.
     __builtin_amdgcn_s_waitcnt(0x0F70);
-    const int end = live_batch ? uni(s.misc[2]) : 0;
-    const int live_tokens = end <= 0 ? 0 : (end < (int)p.tokens ? end : (int)p.tokens);
     const int batch = uni(s.misc[1]);
     uint16_t *out_row = reinterpret_cast<uint16_t *>(p.out) + ((int64_t)t * H + hbase) * D;
     float *lse_row = p.lse ? reinterpret_cast<float *>(p.lse) + (int64_t)t * H + hbase : nullptr;
@@ -1118,7 +1195,7 @@ int g_merge_mode = 0;   // 0: fused (last partition folds), 1: separate merge la
 
 template <bool DEBUG, bool ANYH>
 void launch_variant(hipStream_t stream, const SharedKVArgs *a, const SharedKVDebug &dbg, bool slots, uint32_t grid,
-                    uint32_t splits, uint32_t items, uint32_t fused)
+                    uint32_t splits, uint32_t rows, uint32_t fused)
 {
     auto kernel = &c8_attention<1, DEBUG, false, ANYH>;
     if (slots)
@@ -1132,7 +1209,7 @@ void launch_variant(hipStream_t stream, const SharedKVArgs *a, const SharedKVDeb
     // build preloads them into SGPRs (-amdgpu-kernarg-preload-count), so
     // those loads do not wait for a read of the argument block.
     hipLaunchKernelGGL(kernel, dim3(grid), dim3(THREADS), 0, stream, a->cuQ, a->seqLens, a->q, a->indices, a->batch,
-                       a->topk, a->heads, splits, items, grid, *a, dbg, fused);
+                       a->topk, a->heads, splits, rows, grid, *a, dbg, fused);
 }
 
 template <bool DEBUG>
@@ -1150,9 +1227,9 @@ int launch_attention(hipStream_t stream, const SharedKVArgs *a, const SharedKVDe
     if (DEBUG && (a->heads != HEADS || (a->oriIndices && a->oriTopk > N))) return (int)hipErrorInvalidValue;
     const bool slots = a->oriIndices != 0;
     if (!DEBUG && a->heads != HEADS)
-        launch_variant<false, true>(stream, a, dbg, slots, grid, splits, items, fused);
+        launch_variant<false, true>(stream, a, dbg, slots, grid, splits, rows, fused);
     else
-        launch_variant<DEBUG, false>(stream, a, dbg, slots, grid, splits, items, fused);
+        launch_variant<DEBUG, false>(stream, a, dbg, slots, grid, splits, rows, fused);
     if (splits > 1 && !fused)
         hipLaunchKernelGGL(c8_merge, dim3(rows), dim3(THREADS), 0, stream, *a, splits);
     return (int)hipGetLastError();

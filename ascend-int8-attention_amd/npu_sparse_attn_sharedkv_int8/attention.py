@@ -176,6 +176,20 @@ class PreparedAttention:
                              ("seqLens", case.seq_lens), ("sinks", case.sink), ("oriIndices", case.ori_indices)):
             setattr(self.args, name, tensor.data_ptr() if tensor is not None else 0)
 
+    def device_splits(self, cu_q=None, seq_lens=None, merge_mode=0):
+        """KV partitions the kernel uses for this launch under live metadata
+        (default: the case's, read back to the host); equals .splits unless
+        graph padding leaves rows idle.  merge_mode is the library's
+        (sharedkv_c8_set_merge_mode): 1 keeps the launch plan."""
+        if not self.blocks:
+            return self.splits
+        c = self.case
+        cu_q = c.cu_q.cpu().tolist() if cu_q is None else cu_q
+        seq_lens = c.seq_lens.cpu().tolist() if seq_lens is None else seq_lens
+        return c8_attention.device_splits(self.splits, self.args.tokens, self.args.heads, self.args.ratio,
+                                          self.args.topk, cu_q, seq_lens, self.args.oriTopk,
+                                          fused=merge_mode == 0)
+
     def run(self):
         """Launch on the current stream of the case's device; returns .out."""
         if self.blocks == 0:

@@ -76,16 +76,87 @@ def max_tiles(ratio, topk, max_seq_len=None, ori_topk=0):
     return window_tiles
 
 
+def plan_splits(rows, tiles):
+    """Partitions for `rows` query rows of at most `tiles` tiles each.
+
+    Five partitions while rows x 5 work-groups fit one wave on the CUs (a
+    row's nine tiles then take at most two per partition), else three; on
+    MI355X this is the fastest of 2..6 at 1, 32 and 64 rows.  The kernel
+    applies the same rule to the live rows of a padded launch."""
+    wanted = SPLITS_FEW_ROWS if rows * SPLITS_FEW_ROWS <= CORES else SPLITS_MANY_ROWS
+    wanted = min(wanted, max(1, CORES // rows))
+    return max(1, min(wanted, tiles, MAX_SPLITS))
+
+
 def choose_splits(tokens, ratio, topk, max_seq_len=None, ori_topk=0):
     """KV partitions for a launch of `tokens` query rows (host-side plan)."""
     if tokens <= 0:
         return 1
-    # Five partitions while rows x 5 work-groups fit one wave on the CUs (a
-    # row's nine tiles then take at most two per partition), else three; on
-    # MI355X this is the fastest of 2..6 at 1, 32 and 64 rows.
-    wanted = SPLITS_FEW_ROWS if tokens * SPLITS_FEW_ROWS <= CORES else SPLITS_MANY_ROWS
-    wanted = min(wanted, max(1, CORES // tokens))
-    return max(1, min(wanted, max_tiles(ratio, topk, max_seq_len, ori_topk), MAX_SPLITS))
+    return plan_splits(tokens, max_tiles(ratio, topk, max_seq_len, ori_topk))
+
+
+def live_shape(cu_q, seq_lens, tokens):
+    """(live tokens, longest live sequence) of a launch's metadata, as the
+    kernel reads them (attention_impl.h:121-137): the last request with
+    seq_len > 0 and cu_q[b + 1] >= 0 ends the live batch, its cu_q end
+    (clamped to the launch's tokens) bounds the live tokens."""
+    cu_q = [int(x) for x in cu_q]
+    seq_lens = [int(x) for x in seq_lens]
+    live_batch = 0
+    for b, length in enumerate(seq_lens):
+        if length > 0 and cu_q[b + 1] >= 0:
+            live_batch = b + 1
+    if not live_batch:
+        return 0, 0
+    end = cu_q[live_batch]
+    return max(0, min(end, tokens)), max([0] + seq_lens[:live_batch])
+
+
+def keyless_tokens(cu_q, seq_lens, tokens):
+    """Query tokens whose output and LSE rows the kernel zero-fills: past the
+    live tokens (graph padding, attention_impl.h:443-460), in no live
+    request, or at a negative position (a request listing more query tokens
+    than its sequence length; reference.py:104-105 rejects such metadata on
+    the host, the device cannot read it back)."""
+    cu = [int(x) for x in cu_q]
+    lens = [int(x) for x in seq_lens]
+    live_tokens, _ = live_shape(cu, lens, tokens)
+    live_batch = max([b + 1 for b, n in enumerate(lens) if n > 0 and cu[b + 1] >= 0] + [0])
+    keyless = [True] * tokens
+    for t in range(live_tokens):
+        for b in range(live_batch):
+            if cu[b] <= t < cu[b + 1]:
+                keyless[t] = lens[b] - cu[b + 1] + t < 0
+    return keyless
+
+
+def device_splits(splits, tokens, heads, ratio, topk, cu_q, seq_lens, ori_topk=0, fused=True):
+    """The KV partitions the kernel runs a launch with, from its live metadata.
+
+    A launch planned for `tokens` query tokens (graph capacity) at `splits`
+    partitions has tokens x head groups x splits work-groups.  When fewer
+    rows are live (graph padding), the kernel hands idle work-groups to the
+    live rows as more partitions: plan_splits(live rows, tile count of the
+    longest live row), at most work-groups // live rows and never below
+    `splits`.  Only fused launches (splits > 1, merge in the same launch)
+    re-plan: the partition states need the partial buffer, which a
+    one-partition launch does not carry.  The kernel's numerics follow this
+    count (tile k folds into partition k % count), so checkers use it in
+    place of `splits`.
+    """
+    if not fused or splits <= 1:
+        return splits
+    live_tokens, longest = live_shape(cu_q, seq_lens, tokens)
+    groups = head_groups(heads)
+    live_rows, rows = live_tokens * groups, tokens * groups
+    if live_rows == 0 or live_rows >= rows:
+        return splits
+    tiles = (ori_topk + TILE - 1) // TILE if ori_topk else 1
+    if ratio == 4:
+        tiles += (min(longest // 4, topk) + TILE - 1) // TILE
+    elif ratio == 128:
+        tiles += (longest // 128 + TILE - 1) // TILE
+    return max(splits, min(plan_splits(live_rows, tiles), rows * splits // live_rows))
 
 
 def supported(entry):

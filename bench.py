@@ -113,7 +113,8 @@ def bench_writer(args, torch):
     ms_per_step = start.elapsed_time(end) / args.steps
     algorithmic = rows * (512 * 2 + 512 + 4) + 512 * 4
     achieved = algorithmic / (ms_per_step * 1e-3) / 1e9
-    return {
+    traffic, traffic_source = recorded_traffic("cfg4_writer")
+    record = {
         "metric": "INT8 KV cache write rows/s + HBM GB/s, config 4 writer", "value": rows / (ms_per_step * 1e-3),
         "unit": "rows/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_per_step,
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "i8",
@@ -122,30 +123,110 @@ def bench_writer(args, torch):
                    "rows": rows, "pages": pages, "page_stride": stride, "layers_rotated": layers},
         "latency_us_per_launch": ms_per_step * 1e3,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": achieved / PEAK_HBM_GBS, "traffic": None, "algorithmic_bytes_per_launch": algorithmic},
+                     "frac": achieved / PEAK_HBM_GBS, "traffic": traffic, "traffic_source": traffic_source,
+                     "algorithmic_bytes_per_launch": algorithmic},
     }
+    if not args.no_cpu:
+        log(f"[bench] writer CPU baseline ({args.cpu_seconds:.0f} s sample)")
+        record["cpu_baseline"] = writer_cpu_baseline(rows, pages, stride, args.cpu_seconds)
+    return record
+
+
+def host_cores():
+    """Threads the CPU baseline may use: the job's CPU share (OMP_NUM_THREADS
+    where the launcher sets it, else the process's CPU affinity)."""
+    affinity = len(os.sched_getaffinity(0))
+    share = int(os.environ.get("OMP_NUM_THREADS") or affinity)
+    return max(1, min(share, affinity))
 
 
 def cpu_baseline(dc, layers, splits, seconds):
     """Time the C restatement on whole launches of the same workload until
-    about `seconds` of wall time have passed (bounded sample)."""
+    about `seconds` of wall time have passed (bounded sample), on every host
+    core of the job's share and then on one thread (half the time)."""
     import oracle.oracle as ora
     from tests import workloads
-    threads = max(1, min(16, os.cpu_count() or 1))
     hosts = [workloads.oracle_case(dc.host(layer)) for layer in range(min(layers, 2))]
-    queries = 0
-    launches = 0
+
+    def timed(threads, budget):
+        queries = launches = 0
+        start = time.perf_counter()
+        while time.perf_counter() - start < budget:
+            ora.tiled_attention(hosts[launches % len(hosts)], tile=128, splits=splits, return_lse=False,
+                                threads=threads)
+            queries += int(dc.meta["cu_q"][-1])
+            launches += 1
+        elapsed = time.perf_counter() - start
+        return queries / elapsed, (f"{launches} whole launches of the bench workload ({queries} queries, "
+                                   f"{min(layers, 2)} layers' data) through oracle/libsharedkv_oracle.so, "
+                                   f"{threads} OpenMP thread(s), {elapsed:.1f} s")
+
+    cores = host_cores()
+    value, sample = timed(cores, seconds)
+    single, single_sample = timed(1, seconds / 2)
+    return dict(value=value, unit="queries/s", cores=cores, kind="port", sample=sample,
+                host={"nproc": os.cpu_count(), "affinity": len(os.sched_getaffinity(0)),
+                      "omp_num_threads": os.environ.get("OMP_NUM_THREADS")},
+                single_thread={"value": single, "unit": "queries/s", "cores": 1, "sample": single_sample})
+
+
+def writer_cpu_baseline(rows, pages, stride, seconds):
+    """The writer's C restatement (oracle/, scalar, one thread) on the same
+    shape: `rows` BF16 rows through a random unique slot mapping into a
+    `pages`-page pool at `stride` bytes a page, repeated for ~`seconds`."""
+    import numpy as np
+    import oracle.oracle as ora
+    from tests import workloads
+    rng = np.random.default_rng(4)
+    pool = np.zeros(pages * stride, np.int8)
+    updates = workloads.bf16_bits(rng.standard_normal((rows, 512), dtype=np.float32))
+    slots = rng.choice(pages * 32, rows, replace=False).astype(np.int32)
+    inverse = ora.inverse_scale(workloads.frozen_scale(workloads.bf16_value(updates)))
+    ora.cache_write(pool, stride, pages, 32, updates, slots, inverse)     # untimed: first touch of the pool
+    calls = 0
     start = time.perf_counter()
     while time.perf_counter() - start < seconds:
-        ora.tiled_attention(hosts[launches % len(hosts)], tile=128, splits=splits, return_lse=False,
-                            threads=threads)
-        queries += int(dc.meta["cu_q"][-1])
-        launches += 1
+        ora.cache_write(pool, stride, pages, 32, updates, slots, inverse)
+        calls += 1
     elapsed = time.perf_counter() - start
-    return dict(value=queries / elapsed, unit="queries/s", cores=threads, kind="port",
-                sample=f"{launches} whole launches of the bench workload ({queries} queries, "
-                       f"{min(layers, 2)} layers' data) through oracle/libsharedkv_oracle.so, "
-                       f"{threads} OpenMP threads, {elapsed:.1f} s")
+    return dict(value=calls * rows / elapsed, unit="rows/s", cores=1, kind="port",
+                sample=f"{calls} whole launches ({rows} rows each) through oracle/libsharedkv_oracle.so "
+                       f"sko_cache_write, one thread, {elapsed:.1f} s")
+
+
+def recorded_traffic(workload):
+    """HBM bytes per launch from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE summary of this workload (scaled by a plain copy's reading),
+    or None.  A recorded figure: bench.py itself does not run counters."""
+    path = ROOT / "profiles" / f"traffic_{workload}.md"
+    if path.exists():
+        for line in path.read_text().splitlines():
+            if line.startswith("bytes_per_launch:"):
+                return int(line.split(":", 1)[1]), f"profiles/{path.name}"
+    return None, None
+
+
+def eager_latency(op, stream, torch, calls=50):
+    """Per-call latency of single eager launches: HIP events around each
+    launch on its stream (kernel time alone) and host wall time of run()
+    plus synchronize (what a caller without graphs waits); medians."""
+    import statistics
+    kernel, wall = [], []
+    with torch.cuda.stream(stream):
+        for _ in range(calls):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            a.record(stream)
+            op.run()
+            b.record(stream)
+            torch.cuda.synchronize()
+            wall.append((time.perf_counter() - t0) * 1e6)
+            kernel.append(a.elapsed_time(b) * 1e3)
+    return {"calls": calls, "kernel_us_median": statistics.median(kernel),
+            "call_us_median": statistics.median(wall),
+            "note": "each launch alone: events on its stream around one run(); call = host wall of run() + "
+                    "synchronize, launch overhead included"}
 
 
 def main():
@@ -161,6 +242,9 @@ def main():
     ap.add_argument("--heads", type=int, default=8, help="query heads per token (the metric is quoted at 8)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--live", type=int, default=None, metavar="SEQS",
+                    help="also replay the captured graph with only SEQS sequences live (graph padding; the "
+                         "kernel re-plans partitions on the device); default 8 for the headline, 0 = skip")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="also run a plain device copy of MIB MiB four times (the reference kernel "
                          "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
@@ -226,12 +310,46 @@ def main():
 
     # HBM bytes per launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE
     # (scaled by a plain copy's reading); the summary states the commands.
-    traffic = None
-    traffic_file = ROOT / "profiles" / f"traffic_{args.workload}.md"
-    if traffic_file.exists():
-        for line in traffic_file.read_text().splitlines():
-            if line.startswith("bytes_per_launch:"):
-                traffic = int(line.split(":", 1)[1])
+    traffic, traffic_source = recorded_traffic(args.workload) if args.heads == 8 else (None, None)
+
+    # The same graph replayed with only `live` sequences live: the rest get
+    # seq_len 0 (graph padding) and the kernel hands their work-groups to the
+    # live rows as extra partitions (c8_attention.device_splits).
+    live_seqs = args.live if args.live is not None else (8 if args.workload == "headline" else 0)
+    padded = None
+    if 0 < live_seqs < len(queries) and args.merge == 0:
+        from npu_sparse_attn_sharedkv_int8 import c8_attention
+        cu_full, lens_full = dc.meta["cu_q"].copy(), dc.meta["seq_lens"].copy()
+        cu = cu_full.copy()
+        cu[live_seqs + 1:] = cu_full[live_seqs]
+        lens = lens_full.copy()
+        lens[live_seqs:] = 0
+        device_plan = c8_attention.device_splits(splits, int(cu_full[-1]), args.heads, ratio, 1024, cu, lens)
+        dc.dev.cu_q.copy_(torch.from_numpy(cu))
+        dc.dev.seq_lens.copy_(torch.from_numpy(lens))
+        torch.cuda.synchronize()
+        with torch.cuda.stream(stream):
+            graph.replay()
+            torch.cuda.synchronize()
+            p0, p1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            p0.record(stream)
+            graph.replay()
+            p1.record(stream)
+            torch.cuda.synchronize()
+        dc.dev.cu_q.copy_(torch.from_numpy(cu_full))
+        dc.dev.seq_lens.copy_(torch.from_numpy(lens_full))
+        torch.cuda.synchronize()
+        us = p0.elapsed_time(p1) / args.steps * 1e3
+        live_rows = int(cu[live_seqs])
+        padded = {"capacity_sequences": len(queries), "live_sequences": live_seqs, "live_queries": live_rows,
+                  "launch_splits": splits, "device_splits": device_plan, "us_per_launch": us,
+                  "queries_per_s": live_rows / (us * 1e-6),
+                  "note": "the timed graph replayed with the sequences past the live ones at seq_len 0"}
+        log(f"[bench] padded graph: {live_seqs} of {len(queries)} sequences live, {device_plan} partitions, "
+            f"{us:.2f} us per launch")
+
+    eager = eager_latency(ops[0], stream, torch)
+    log(f"[bench] eager: kernel {eager['kernel_us_median']:.2f} us, call {eager['call_us_median']:.2f} us")
 
     # int8 MFMA work the launch performs: per selected key, QK and PV over
     # 16 rows (8 heads x {code, residual}) x 512 channels, 2 ops per MAC.
@@ -250,11 +368,14 @@ def main():
                    "timing": "one HIP graph replay of K launches, HIP events on its stream"},
         "latency_us_per_layer": ms_per_step * 1e3,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
-                     "frac": achieved / PEAK_HBM_GBS, "traffic": traffic,
+                     "frac": achieved / PEAK_HBM_GBS, "traffic": traffic, "traffic_source": traffic_source,
                      "algorithmic_bytes_per_launch": mean_bytes},
         "mfma": {"int8_ops_per_launch": int8_ops, "achieved_tops": int8_ops / (ms_per_step * 1e-3) / 1e12,
                  "peak_tops": 5000.0, "frac": int8_ops / (ms_per_step * 1e-3) / 1e12 / 5000.0},
+        "eager_latency": eager,
     }
+    if padded:
+        record["padded_graph"] = padded
     if args.copy_calibration:
         n = args.copy_calibration << 20
         src = torch.ones(n, dtype=torch.int8, device="cuda")

@@ -331,12 +331,12 @@ def test_padded_graph_rows_are_zero_and_guards_hold(mode, heads):
     from npu_sparse_attn_sharedkv_int8.runtime import library
     assert library().sharedkv_c8_set_merge_mode(mode) == 0
     try:
-        _padded_rows_case(heads)
+        _padded_rows_case(heads, mode)
     finally:
         library().sharedkv_c8_set_merge_mode(0)
 
 
-def _padded_rows_case(heads=8):
+def _padded_rows_case(heads=8, mode=0):
     import torch
     from npu_sparse_attn_sharedkv_int8 import PreparedAttention
     case = workloads.make_case(21, 4, [2, 1, 0, 0], [3000, 700, 0, 0], index_mode="mixed", heads=heads)
@@ -356,7 +356,12 @@ def _padded_rows_case(heads=8):
     torch.cuda.synchronize()
     assert (guard_out[[0, -1]].float().cpu() == 123).all() and (guard_lse[[0, -1]].cpu() == 123).all()
     assert (op.out[live:].float().cpu() == 0).all() and (op.lse[live:].cpu() == 0).all()
-    compare(case, bits_of(op.out)[:live], op.lse.cpu().numpy()[:live], op.splits, tag="padding")
+    # Fused launches hand the padding rows' work-groups to the live rows.
+    splits = op.device_splits(merge_mode=mode)
+    # 3 (or 6) live rows of at most 1 + ceil(750 / 128) = 7 tiles: 5
+    # partitions, as an eager launch of those rows would choose.
+    assert splits == (4 if mode else 5), splits
+    compare(case, bits_of(op.out)[:live], op.lse.cpu().numpy()[:live], splits, tag="padding")
 
 
 def test_metadata_views_and_scratch_guards():
@@ -442,6 +447,58 @@ def test_graph_replay_with_changing_live_metadata():
         say(f"[graph] replay {i}")
         assert torch.equal(op.out, eager.out), i
         assert torch.equal(op.lse, eager.lse), i
+
+
+def test_graph_at_capacity_replayed_at_fewer_live_sequences():
+    """One launch captured at a capacity of 64 one-token C4 requests (3
+    partitions: 192 work-groups), replayed with 64, 8, 16, 32, 64 and 8 live
+    requests (graph padding: the rest seq_len 0).  The kernel re-plans from
+    the live metadata (the idle work-groups become partitions of the live
+    rows); every replay is bit-exact with the checker on that plan, padding
+    rows are zero, and eager work runs between replays."""
+    import torch
+    from npu_sparse_attn_sharedkv_int8 import PreparedAttention, c8_attention
+    cap = 64
+    rng = np.random.default_rng(5)
+    lengths = [int(n) for n in rng.integers(2100, 3000, cap)]      # 6-7 tiles a row
+    case = workloads.make_case(26, 4, [1] * cap, lengths, index_mode="uniform")
+    dev, oscale, cscale, keep = to_device(case)
+    op = PreparedAttention(dev, oscale, cscale, return_lse=True)
+    assert op.splits == 3
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        op.run()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            op.run()
+    torch.cuda.current_stream().wait_stream(stream)
+    other = PreparedAttention(dev, oscale, cscale, return_lse=True, splits=2)
+    expected = {}
+    for i, live in enumerate((64, 8, 16, 32, 64, 8)):
+        cu = np.array(list(range(live + 1)) + [live] * (cap - live), np.int32)
+        lens = np.array(lengths[:live] + [0] * (cap - live), np.int32)
+        plan = c8_attention.device_splits(op.splits, cap, 8, 4, 1024, cu, lens)
+        assert plan == (3 if live == cap else 5)
+        dev.cu_q.copy_(torch.from_numpy(cu))
+        dev.seq_lens.copy_(torch.from_numpy(lens))
+        op.out.fill_(float("nan"))
+        op.lse.fill_(float("nan"))
+        other.run()                                     # eager work between replays
+        torch.cuda.synchronize()
+        say(f"[capacity graph] replay {i}: {live} live, {plan} partitions")
+        graph.replay()
+        torch.cuda.synchronize()
+        out, lse = bits_of(op.out), op.lse.cpu().numpy()
+        assert not out[live:].any() and not lse[live:].any(), "padding rows are not zero"
+        if live not in expected:
+            expected[live] = run_oracle(query_subcase(case, np.arange(live)), plan)[:2]
+        ref, ref_lse = expected[live]
+        diff = out[:live] != ref
+        assert not diff.any(), f"{live} live: {int(diff.sum())} BF16 mismatches"
+        np.testing.assert_allclose(lse[:live], ref_lse, rtol=0, atol=2e-6)
+    del graph
 
 
 def test_rebind_same_geometry():

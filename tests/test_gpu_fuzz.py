@@ -68,11 +68,12 @@ def test_random_launch_matches_checker(seed):
         out, lse, op = run_hip(case, splits=splits)
     finally:
         lib.sharedkv_c8_set_merge_mode(0)
+    plan = op.device_splits(merge_mode=merge)     # the kernel's re-plan under padding
     live = int(case["cu_q"][-1]) - desc["pad"]
     if desc["pad"]:
         assert not out[live:].any() and not lse[live:].any(), "padding rows are not zero"
         case = dict(case, q=case["q"][:live], cu_q=case["cu_q"][:-1], seq_lens=case["seq_lens"][:-1])
-    ref, ref_lse, _ = run_oracle(case, op.splits)
+    ref, ref_lse, _ = run_oracle(case, plan)
     diff = out[:live] != ref[:live]
     assert not diff.any(), f"seed {seed}: {int(diff.sum())} BF16 mismatches of {diff.size}"
     np.testing.assert_allclose(lse[:live], ref_lse[:live], rtol=0, atol=2e-6)

@@ -119,6 +119,59 @@ def test_host_plan():
     assert c8_attention.choose_splits(1, 1, 0) == 1
 
 
+def test_device_plan_of_padded_launches():
+    """The kernel's re-plan of a graph-padded launch (its host mirror):
+    capacity 64 C4 rows at 3 partitions (192 work-groups) replayed with
+    8/16/32/64 live requests of 9-tile rows runs what an eager launch of the
+    live rows would choose; one-partition and separate-merge launches keep
+    their plan."""
+    plan = c8_attention.device_splits
+    cap = 64
+    assert c8_attention.choose_splits(cap, 4, 1024) == 3
+    for live, want in ((8, 5), (16, 5), (32, 5), (51, 3), (64, 3)):
+        cu = list(range(live + 1)) + [cap] * (cap - live)
+        lens = [20000] * live + [0] * (cap - live)
+        assert plan(3, cap, 8, 4, 1024, cu, lens) == want, live
+        assert plan(3, cap, 8, 4, 1024, cu, lens, fused=False) == 3
+        assert plan(1, cap, 8, 4, 1024, cu, lens) == 1
+        # Eager's choice where the work-groups allow it (51 x 5 > 192).
+        assert want == c8_attention.choose_splits(live, 4, 1024) or live == 51
+    # Work-groups cap the plan: capacity 6 at 2 partitions, 5 live rows -> 2.
+    assert plan(2, 6, 8, 4, 1024, [0, 5, 6], [9000, 0]) == 2
+    # The longest live row bounds the plan by its tile count: C4 top-k rows
+    # of a 600-key sequence have 1 + ceil(150 / 128) = 3 tiles, C128 rows of
+    # 4096 keys 1 + 1, window-only rows 1 (explicit slots: ceil(K / 128)).
+    assert plan(2, 64, 8, 4, 1024, [0, 1, 64], [600, 0]) == 3
+    assert plan(2, 64, 8, 128, 0, [0, 1, 64], [4096, 0]) == 2
+    assert plan(2, 64, 8, 1, 0, [0, 1, 64], [4096, 0]) == 2
+    assert plan(2, 64, 8, 1, 0, [0, 1, 64], [4096, 0], ori_topk=384) == 3
+    # Head groups count as rows: 16 heads, 4 live tokens of 32 -> 8 rows.
+    assert plan(3, 32, 16, 4, 1024, [0, 4, 32], [30000, 0]) == 5
+    # The live shape: a cu_q sentinel (-1) or seq_len 0 ends the live batch.
+    assert c8_attention.live_shape([0, 2, 4, -1], [5000, 2600, 9000], 6) == (4, 5000)
+    assert c8_attention.live_shape([0, 2, 4, 6], [5000, 0, 0], 6) == (2, 5000)
+    assert c8_attention.live_shape([0, 2, 9], [1, 8], 6) == (6, 8)
+    assert c8_attention.live_shape([0, 0], [0], 4) == (0, 0)
+    assert plan(3, 6, 8, 4, 1024, [0, 0, 0], [0, 0]) == 3     # nothing live
+
+
+def test_keyless_tokens_rule():
+    """Tokens the kernel zero-fills: past the live end, outside every live
+    request, or at a negative position; the checker (like the reference,
+    reference.py:104-105) rejects negative positions instead."""
+    keyless = c8_attention.keyless_tokens
+    # Request 0 lists 3 tokens over 1 key (positions -2, -1, 0).
+    assert keyless([0, 3, 5, 6], [1, 900, 40], 6) == [True, True, False, False, False, False]
+    assert keyless([0, 2, 3, 6, 6], [3000, 700, 0, 0], 6) == [False] * 3 + [True] * 3
+    assert keyless([0, 2, 4, -1], [5000, 2600, 9000], 6) == [False] * 4 + [True] * 2
+    assert keyless([1, 2], [10], 3) == [True, False, True]
+    import oracle.oracle as ora
+    from tests import workloads
+    case = workloads.make_case(31, 4, [3, 2, 1], [1, 900, 40])
+    with pytest.raises(ValueError, match="code -8"):
+        ora.tiled_attention(workloads.oracle_case(case), tile=128, splits=1, return_lse=True)
+
+
 def test_bench_refuses_more_than_one_gpu():
     """bench.py measures one GPU; --gpus N > 1 exits with a message before it
     touches a device."""
