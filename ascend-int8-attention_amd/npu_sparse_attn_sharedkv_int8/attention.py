@@ -105,7 +105,9 @@ class PreparedAttention:
 
         # Tuning knobs of the Ascend planner.  Only the ones that change this
         # build's numerics (tile_size, splits) are honoured; the rest are
-        # validated for type and recorded.
+        # validated for type and recorded.  adaptive_splits has nothing left
+        # to switch: the kernel always adapts the partition count to the live
+        # rows of a padded launch (c8_attention.device_splits).
         if tile_size is not None and tile_size != c8_attention.TILE:
             raise ValueError(f"This build tiles keys in groups of {c8_attention.TILE}; tile_size must be None or "
                              f"{c8_attention.TILE}")

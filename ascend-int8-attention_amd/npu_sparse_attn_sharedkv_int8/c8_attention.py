@@ -3,9 +3,11 @@
 Interface counterpart: npu_sparse_attn_sharedkv_int8/c8_attention.py:18-138 of
 the reference checkout (CORES, HEADS, MAX_SPLITS, enabled(), supported(),
 prepare()).  The Ascend build plans tiles on the device from live metadata
-for 24 cores; this build fixes the plan on the host instead, from the graph
-capacity alone, so the plan (and hence the numerics) is a pure function of
-(tokens, ratio, top-k, max_seq_len) that tests and the CPU checker recompute:
+for 24 cores.  This build plans a launch on the host from its capacity
+(choose_splits: a pure function of tokens, ratio, top-k and max_seq_len),
+and the kernel re-plans on the device only when graph padding leaves rows
+idle (device_splits, the host mirror of that rule), so tests and the CPU
+checker can recompute the plan, and hence the numerics, of every launch:
 
   tile   128 keys; a query's list is the window rows, then its compressed rows,
          cut into 128-key tiles numbered continuously across the two kinds

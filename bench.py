@@ -76,6 +76,20 @@ WORKLOADS = ["headline", "cfg0", "cfg1", "cfg2_c4", "cfg2_c128", "cfg3_prefill",
              "cfg4_writer"]
 
 
+def copy_calibration(mib, torch):
+    """A plain device copy of `mib` MiB, four times: the reference dispatches
+    for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes."""
+    if not mib:
+        return
+    n = mib << 20
+    src = torch.ones(n, dtype=torch.int8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(4):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"[bench] copy calibration: 4 copies of {n} bytes (read {n // 1024} KiB, write {n // 1024} KiB each)")
+
+
 def bench_writer(args, torch):
     """Config 4's writer: 4096 BF16 rows quantised and scattered through a
     random unique slot mapping into a stride-viewed block32 pool (page stride
@@ -261,7 +275,9 @@ def main():
 
     torch.cuda.set_device(0)
     if args.workload == "cfg4_writer":
-        print(json.dumps(bench_writer(args, torch)), flush=True)
+        record = bench_writer(args, torch)
+        copy_calibration(args.copy_calibration, torch)
+        print(json.dumps(record), flush=True)
         return
     from npu_sparse_attn_sharedkv_int8.runtime import library
     if library().sharedkv_c8_set_merge_mode(args.merge):
@@ -376,15 +392,7 @@ def main():
     }
     if padded:
         record["padded_graph"] = padded
-    if args.copy_calibration:
-        n = args.copy_calibration << 20
-        src = torch.ones(n, dtype=torch.int8, device="cuda")
-        dst = torch.empty_like(src)
-        for _ in range(4):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        log(f"[bench] copy calibration: 4 copies of {n} bytes (read {n // 1024} KiB, write {n // 1024} KiB each)")
-        del src, dst
+    copy_calibration(args.copy_calibration, torch)
     if not args.no_cpu:
         log(f"[bench] CPU baseline ({args.cpu_seconds:.0f} s sample)")
         record["cpu_baseline"] = cpu_baseline(dc, layers, splits, args.cpu_seconds)
