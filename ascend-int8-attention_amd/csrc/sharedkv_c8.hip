@@ -246,6 +246,7 @@ static_assert(DMA_PER_TILE == 8, "vm_wait<8> covers one tile in flight");
 struct alignas(16) Shared {
     int32_t redmax[HEADS][WAVES];   // per-wave tile maxima (fkey)
     float redsum[HEADS][WAVES];     // per-wave weight sums
+    float redsum1[HEADS][WAVES];    // joint rows: per-wave weight sums of the compressed tile
     float asc[2][HEADS];            // alpha * softmax_scale per kind
     int32_t scan[WAVES];
     int32_t misc[8];
@@ -465,7 +466,29 @@ c8_attention(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base
     // separate merge launch (not fused) keeps the launch plan.
     const int32_t rows_cap = (int32_t)rows_arg;
     const int32_t live_rows = live_tokens * HG;
-    if (fused && live_rows < rows_cap) {
+    // The longest live sequence bounds the rows' tile counts (one scan, only
+    // where a plan needs it).
+    int longest = -1;
+    auto longest_live = [&]() {
+        if (longest < 0) {
+            for (int b = tid; b < live_batch; b += THREADS) atomicMax(&s.misc[6], b == tid ? my_len : lens[b]);
+            __syncthreads();
+            longest = uni(s.misc[6]);
+        }
+        return longest;
+    };
+    // Joint plan (C128): when every live row's window and compressed lists
+    // fit one tile each, the launch runs as one partition per row and those
+    // rows take one softmax over both kinds, as the reference device's
+    // one-split C128 plans do (c128.cpp:79-105, attention_impl.h:94-100).
+    // Work items of the other partitions have nothing to do.  A launch with
+    // a separate merge keeps its plan; c8_attention.device_splits mirrors
+    // the rule.
+    if (RATIO == 128 && !DEBUG && !SLOTS && resid && (fused || S == 1) && live_rows > 0 &&
+        longest_live() / RATIO <= N) {
+        if (part != 0) return;
+        S = 1;
+    } else if (fused && live_rows < rows_cap) {
         const int32_t pad = live_rows + (int32_t)item;
         if (pad < rows_cap) {   // zero-fill padding row `pad` (attention_impl.h:443-460)
             const int32_t pt = ANYH ? pad / HG : pad, ph = ANYH ? HEADS * (pad % HG) : 0;
@@ -475,10 +498,7 @@ c8_attention(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base
             if (p.lse && tid < pl) reinterpret_cast<float *>(p.lse)[(int64_t)pt * H + ph + tid] = 0.0f;
         }
         if (live_rows == 0) return;
-        // The longest live sequence bounds the rows' tile counts.
-        for (int b = tid; b < live_batch; b += THREADS) atomicMax(&s.misc[6], b == tid ? my_len : lens[b]);
-        __syncthreads();
-        const int longest = uni(s.misc[6]);
+        longest_live();
         int tiles = SLOTS ? ((int)p.oriTopk + N - 1) / N : 1;
         if (RATIO == 4) {
             const int cnt = longest / 4 < (int)topk_arg ? longest / 4 : (int)topk_arg;
@@ -644,6 +664,17 @@ c8_attention(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base
     // numbers equal the fold over all S partitions bit for bit.
     const int folded = S < m.total ? S : m.total;    // partitions that own tiles (>= 1)
     if (part >= folded) return;
+    // Joint row (reference.py:254-267 with joint_dense; the reference
+    // device's two-kind pipeline, attention_impl.h:94-100): a C128 row run as
+    // one partition whose window and compressed lists each fit one tile
+    // takes one softmax over both kinds (joint_quantized_row,
+    // reference.py:175-207) instead of two online tiles.  The window of such
+    // a row is full (its position is at least 127), so its valid keys fill
+    // tile 0 and the first list_len keys of tile 1, the order in which the
+    // reference concatenates them.  Explicit original slots, more than eight
+    // heads (no residual codes) and the debug entry keep the tiled plan.
+    const bool joint = RATIO == 128 && !DEBUG && !SLOTS && resid && S == 1 && m.t0 == 1 && m.list_len >= 1 &&
+                       m.list_len <= N;
 
     // ---- per-lane softmax state for heads 2g and 2g+1 ----
     float mx[2] = {sink0, sink1}, den[2], num[2][4];
@@ -884,6 +915,140 @@ c8_attention(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base
         asm volatile("" : "+v"(lane_x));
         const int gx = lane_x >> 4, nx = lane_x & 15;
 
+        if (joint) {
+            // ---- joint row: both tiles resident (tile 0 = window in buffer
+            // 0, tile 1 = compressed rows in buffer 1) ----
+            vm_wait<0>();
+            lds_barrier();
+            const int key = 16 * wave + nx;
+            const int sl = slot_of(key);
+            // QK of both kinds, each with its own Q encoding (reference.py:181-188).
+            v4i sacc[2] = {v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}};
+#pragma unroll
+            for (int kind = 0; kind < 2; ++kind) {
+                v4i b[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) b[j] = *reinterpret_cast<const v4i *>(s.tile[kind] + tile_offset(sl, 4 * j + gx));
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    sacc[kind] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kind ? qa1[j] : qa0[j], b[j], sacc[kind], 0, 0, 0);
+            }
+            float lg[2][2];   // [kind][head 2g + hh]
+#pragma unroll
+            for (int kind = 0; kind < 2; ++kind) {
+                const bool valid = s.code[kind * N + key] >= 0;
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    float dots = (float)sacc[kind][2 * hh];
+                    dots = dots + (float)sacc[kind][2 * hh + 1] * (float)(1.0 / 127.0);
+                    const float l = dots * s.asc[kind][2 * gx + hh];
+                    lg[kind][hh] = valid ? l : -1e30f;
+                }
+            }
+            // maximum = max(sink, every score of both kinds) (reference.py:193)
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                const int kmax = row16_max_key(max(fkey(lg[0][hh]), fkey(lg[1][hh])));
+                if (nx == 0) s.redmax[2 * gx + hh][wave] = kmax;
+            }
+            lds_barrier();
+            float mnew[2], factor[2];
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                const int h = 2 * gx + hh;
+                const v4i a = *reinterpret_cast<const v4i *>(&s.redmax[h][0]);
+                const v4i b = *reinterpret_cast<const v4i *>(&s.redmax[h][4]);
+                const int k = max(max(max(fkey(mx[hh]), a.x), max(a.y, a.z)), max(max(a.w, b.x), max(max(b.y, b.z), b.w)));
+                mnew[hh] = fkey_value(k);
+            }
+            {
+                const bool odd = nx & 1;   // exp(sink - maximum), one exponential per lane pair
+                const float mine = sk_expf_nonpos(odd ? mx[1] - mnew[1] : mx[0] - mnew[0]);
+                const float other = dpp<DPP_XOR1>(mine);
+                factor[0] = odd ? other : mine;
+                factor[1] = odd ? mine : other;
+            }
+            // Weights and P codes (reference.py:194-198); the compressed
+            // tile's P codes go to the free address table.
+            int8_t *p1 = reinterpret_cast<int8_t *>(s.addr);
+            static_assert(16 * PROW <= (int)sizeof(s.addr), "P codes of the second tile fit the address table");
+#pragma unroll
+            for (int kind = 0; kind < 2; ++kind) {
+                int8_t *pk = kind ? p1 : s.p;
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    const float w = sk_expf_nonpos(lg[kind][hh] - mnew[hh]);
+                    const float x = w * 127.0f;
+                    const float ph = __builtin_rintf(x);
+                    const float pl = __builtin_rintf((x - ph) * 127.0f);
+                    pk[row_of(2 * gx + hh, 0) * PROW + key] = (int8_t)(int32_t)ph;
+                    pk[row_of(2 * gx + hh, 1) * PROW + key] = (int8_t)(int32_t)pl;
+                    const float wsum = row16_tree_sum(w);
+                    if (nx == 0) (kind ? s.redsum1 : s.redsum)[2 * gx + hh][wave] = wsum;
+                }
+            }
+            lds_barrier();
+            // denominator = exp(sink - maximum) + the pairwise sum of the
+            // concatenated weights: the 256-leaf tree is the window tile's
+            // 128-leaf tree plus the compressed tile's (zero leaves past the
+            // list change nothing).
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                const int h = 2 * gx + hh;
+                const f32x4 a0 = *reinterpret_cast<const f32x4 *>(&s.redsum[h][0]);
+                const f32x4 b0 = *reinterpret_cast<const f32x4 *>(&s.redsum[h][4]);
+                const f32x4 a1 = *reinterpret_cast<const f32x4 *>(&s.redsum1[h][0]);
+                const f32x4 b1 = *reinterpret_cast<const f32x4 *>(&s.redsum1[h][4]);
+                const float t0 = ((a0.x + a0.y) + (a0.z + a0.w)) + ((b0.x + b0.y) + (b0.z + b0.w));
+                const float t1 = ((a1.x + a1.y) + (a1.z + a1.w)) + ((b1.x + b1.y) + (b1.z + b1.w));
+                den[hh] = factor[hh] + (t0 + t1);
+            }
+            // PV per kind, then output = sum over kinds of dot * (scale / 127)
+            // in kind order (reference.py:199-206).
+            v4i vacc[2][4];
+#pragma unroll
+            for (int kind = 0; kind < 2; ++kind) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) vacc[kind][j] = v4i{0, 0, 0, 0};
+                const lds_i8 *vbase = (const lds_i8 *)(s.tile[kind]);
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb) {
+                    const v4i pa = kind ? *reinterpret_cast<const v4i *>(p1 + nx * PROW + 64 * kb + 16 * gx)
+                                        : *reinterpret_cast<const v4i *>(s.p + nx * PROW + 64 * kb + 16 * gx);
+                    const int sl_lo = slot_of(64 * kb + 16 * gx + (nx >> 1));
+                    const int sl_hi = slot_of(64 * kb + 16 * gx + 8 + (nx >> 1));
+                    v2i b0[4], b1[4];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const int chunk = 4 * wave + j;
+                        b0[j] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i *)(vbase + tile_offset(sl_lo, chunk) + 8 * (nx & 1)));
+                        b1[j] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i *)(vbase + tile_offset(sl_hi, chunk) + 8 * (nx & 1)));
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const v4i vb = {b0[j].x, b0[j].y, b1[j].x, b1[j].y};
+                        vacc[kind][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(pa, vb, vacc[kind][j], 0, 0, 0);
+                    }
+                }
+            }
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    float acc = 0.0f;
+#pragma unroll
+                    for (int kind = 0; kind < 2; ++kind) {
+                        float dots = (float)vacc[kind][j][2 * hh];
+                        dots = dots + (float)vacc[kind][j][2 * hh + 1] * (float)(1.0 / 127.0);
+                        const float sc = s.scale[kind][c0 + 16 * j + nx] * (float)(1.0 / 127.0);
+                        acc = acc + dots * sc;
+                    }
+                    num[hh][j] = acc;
+                }
+                mx[hh] = mnew[hh];
+            }
+        } else
         for (int i = 0; i < ntiles; ++i) {
             const int k = part + S * (first + i);
             const int kind = k >= m.t0 ? 1 : 0;

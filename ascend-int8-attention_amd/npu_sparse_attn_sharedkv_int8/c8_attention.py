@@ -145,12 +145,20 @@ def device_splits(splits, tokens, heads, ratio, topk, cu_q, seq_lens, ori_topk=0
     one-partition launch does not carry.  The kernel's numerics follow this
     count (tile k folds into partition k % count), so checkers use it in
     place of `splits`.
+
+    C128 launches of the joint plan (joint_dense_plan) whose live rows all
+    fit one window tile and one compressed tile (longest live sequence //
+    128 <= 128) run as one partition per row instead, fused or not when
+    `splits` is 1, and only fused otherwise.
     """
-    if not fused or splits <= 1:
-        return splits
     live_tokens, longest = live_shape(cu_q, seq_lens, tokens)
     groups = head_groups(heads)
     live_rows, rows = live_tokens * groups, tokens * groups
+    if (joint_dense_plan(ratio, heads, ori_topk > 0) and (fused or splits == 1) and live_rows > 0
+            and longest // 128 <= TILE):
+        return 1
+    if not fused or splits <= 1:
+        return splits
     if live_rows == 0 or live_rows >= rows:
         return splits
     tiles = (ori_topk + TILE - 1) // TILE if ori_topk else 1
@@ -159,6 +167,17 @@ def device_splits(splits, tokens, heads, ratio, topk, cu_q, seq_lens, ori_topk=0
     elif ratio == 128:
         tiles += (longest // 128 + TILE - 1) // TILE
     return max(splits, min(plan_splits(live_rows, tiles), rows * splits // live_rows))
+
+
+def joint_dense_plan(ratio, heads, explicit_slots):
+    """Whether a launch's plan takes joint C128 rows (reference.py:254-267,
+    joint_dense; the reference device's two-kind pipeline for C128 at one
+    partition, attention_impl.h:94-100).  When it does, every row of a
+    one-partition launch whose window and compressed lists each fit one
+    128-key tile runs one softmax over both kinds; other rows, and launches
+    of more partitions, are tiled as usual.  Residual codes are required
+    (at most eight heads), and explicit original slots keep the tiled plan."""
+    return ratio == 128 and heads <= HEADS and not explicit_slots
 
 
 def supported(entry):

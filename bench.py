@@ -159,15 +159,17 @@ def cpu_baseline(dc, layers, splits, seconds):
     about `seconds` of wall time have passed (bounded sample), on every host
     core of the job's share and then on one thread (half the time)."""
     import oracle.oracle as ora
+    from npu_sparse_attn_sharedkv_int8 import c8_attention
     from tests import workloads
     hosts = [workloads.oracle_case(dc.host(layer)) for layer in range(min(layers, 2))]
+    joint = c8_attention.joint_dense_plan(dc.meta["ratio"], dc.heads, False)
 
     def timed(threads, budget):
         queries = launches = 0
         start = time.perf_counter()
         while time.perf_counter() - start < budget:
             ora.tiled_attention(hosts[launches % len(hosts)], tile=128, splits=splits, return_lse=False,
-                                threads=threads)
+                                joint_dense=joint, threads=threads)
             queries += int(dc.meta["cu_q"][-1])
             launches += 1
         elapsed = time.perf_counter() - start
@@ -295,6 +297,11 @@ def main():
     ops = [PreparedAttention(dc.cases[l], dc.ori_scales[l], dc.cmp_scales[l], splits=args.splits)
            for l in range(layers)]
     splits = ops[0].splits
+    from npu_sparse_attn_sharedkv_int8 import c8_attention
+    # The partitions the kernel runs: the device re-plans joint C128 launches
+    # (and padded ones, below) from the live metadata.
+    device_plan = c8_attention.device_splits(splits, int(dc.meta["cu_q"][-1]), args.heads, ratio, 1024,
+                                             dc.meta["cu_q"], dc.meta["seq_lens"], fused=args.merge == 0)
     live_queries = int(sum(queries))
     bytes_per_launch = [dc.algorithmic_bytes(l) for l in range(layers)]
 
@@ -334,13 +341,12 @@ def main():
     live_seqs = args.live if args.live is not None else (8 if args.workload == "headline" else 0)
     padded = None
     if 0 < live_seqs < len(queries) and args.merge == 0:
-        from npu_sparse_attn_sharedkv_int8 import c8_attention
         cu_full, lens_full = dc.meta["cu_q"].copy(), dc.meta["seq_lens"].copy()
         cu = cu_full.copy()
         cu[live_seqs + 1:] = cu_full[live_seqs]
         lens = lens_full.copy()
         lens[live_seqs:] = 0
-        device_plan = c8_attention.device_splits(splits, int(cu_full[-1]), args.heads, ratio, 1024, cu, lens)
+        padded_plan = c8_attention.device_splits(splits, int(cu_full[-1]), args.heads, ratio, 1024, cu, lens)
         dc.dev.cu_q.copy_(torch.from_numpy(cu))
         dc.dev.seq_lens.copy_(torch.from_numpy(lens))
         torch.cuda.synchronize()
@@ -358,10 +364,10 @@ def main():
         us = p0.elapsed_time(p1) / args.steps * 1e3
         live_rows = int(cu[live_seqs])
         padded = {"capacity_sequences": len(queries), "live_sequences": live_seqs, "live_queries": live_rows,
-                  "launch_splits": splits, "device_splits": device_plan, "us_per_launch": us,
+                  "launch_splits": splits, "device_splits": padded_plan, "us_per_launch": us,
                   "queries_per_s": live_rows / (us * 1e-6),
                   "note": "the timed graph replayed with the sequences past the live ones at seq_len 0"}
-        log(f"[bench] padded graph: {live_seqs} of {len(queries)} sequences live, {device_plan} partitions, "
+        log(f"[bench] padded graph: {live_seqs} of {len(queries)} sequences live, {padded_plan} partitions, "
             f"{us:.2f} us per launch")
 
     eager = eager_latency(ops[0], stream, torch)
@@ -380,6 +386,8 @@ def main():
         "config": {"workload": description, "batch": len(queries), "query_tokens": live_queries, "heads": args.heads,
                    "dim": 512, "ratio": ratio, "topk": 1024 if ratio == 4 else 0, "window": 128,
                    "page_stride": stride, "layers_rotated": layers, "tile": 128, "splits": splits,
+                   "device_splits": device_plan,
+                   "joint_c128_rows": bool(device_plan == 1 and c8_attention.joint_dense_plan(ratio, args.heads, False)),
                    "lse": False, "merge": "fused" if args.merge == 0 else "separate launch",
                    "timing": "one HIP graph replay of K launches, HIP events on its stream"},
         "latency_us_per_layer": ms_per_step * 1e3,
@@ -395,7 +403,7 @@ def main():
     copy_calibration(args.copy_calibration, torch)
     if not args.no_cpu:
         log(f"[bench] CPU baseline ({args.cpu_seconds:.0f} s sample)")
-        record["cpu_baseline"] = cpu_baseline(dc, layers, splits, args.cpu_seconds)
+        record["cpu_baseline"] = cpu_baseline(dc, layers, device_plan, args.cpu_seconds)
     print(json.dumps(record), flush=True)
 
 

@@ -583,6 +583,9 @@ int sko_tiled_attention(const sko_case *c, const sko_plan *pl, uint16_t *out, fl
     if (c->ratio != 1 && c->ratio != 4 && c->ratio != 128) return -2;
     if (pl->tile <= 0 || (pl->tile & (pl->tile - 1)) || pl->splits <= 0 || pl->query_group <= 0) return -3;
     if (pl->query_group > 1 && (c->ori_slots || dbg)) return -10;   /* reference.py:236-237 */
+    /* reference.py:258 asserts residual codes (at most eight heads) for
+     * joint rows; refused here for the whole plan. */
+    if ((pl->joint_dense || pl->joint_sparse) && c->heads > 8) return -11;
     if (c->ratio != 1 && (!c->cmp || !c->cmp_table || !c->cmp_scale)) return -4;
     if (c->ratio == 4 && (!c->cmp_indices || c->topk <= 0)) return -5;
     if (dbg && (c->window > 128 || (c->ori_slots && c->ori_topk > 128))) return -6;

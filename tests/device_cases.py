@@ -111,12 +111,30 @@ def default_cmp_capacity(case):
     return 0
 
 
+def effective_splits(case, splits, merge_mode=0):
+    """KV partitions the kernel runs for a launch of `case` (host numpy
+    metadata) planned at `splits`, with the library in `merge_mode`
+    (c8_attention.device_splits: the device's re-plan of padded launches and
+    joint C128 launches)."""
+    from npu_sparse_attn_sharedkv_int8 import c8_attention
+    slots = case.get("ori_indices")
+    return c8_attention.device_splits(
+        splits, case["q"].shape[0], case["q"].shape[1], case["ratio"],
+        case["cmp_indices"].shape[-1] if case["ratio"] == 4 else 0, case["cu_q"], case["seq_lens"],
+        slots.shape[-1] if slots is not None else 0, fused=merge_mode == 0)
+
+
 def run_oracle(case, splits, debug=False, cmp_capacity=None, tile_capacity=None, threads=None):
-    """The CPU checker with this build's plan (128-key tiles, `splits` partitions)."""
+    """The CPU checker with this build's plan: 128-key tiles, `splits`
+    partitions, and joint C128 rows where the kernel takes them
+    (c8_attention.joint_dense_plan; the debug entry runs the tiled plan)."""
     import oracle.oracle as ora
+    from npu_sparse_attn_sharedkv_int8 import c8_attention
+    joint = not debug and c8_attention.joint_dense_plan(case["ratio"], case["q"].shape[1],
+                                                        case.get("ori_indices") is not None)
     return ora.tiled_attention(workloads.oracle_case(case), tile=128, splits=splits, return_lse=True,
-                               debug=debug, cmp_capacity=cmp_capacity, tile_capacity=tile_capacity,
-                               threads=threads)
+                               joint_dense=joint, debug=debug, cmp_capacity=cmp_capacity,
+                               tile_capacity=tile_capacity, threads=threads)
 
 
 def query_subcase(case, rows):

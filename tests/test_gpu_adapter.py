@@ -18,7 +18,7 @@ import numpy as np
 import pytest
 
 from tests import workloads
-from tests.device_cases import bits_of, run_oracle, torch_bf16
+from tests.device_cases import bits_of, effective_splits, run_oracle, torch_bf16
 
 pytestmark = pytest.mark.gpu
 
@@ -37,7 +37,7 @@ def _expected(case, q_bits, splits):
 
 
 def _check(case, q_bits, out, lse, splits, tag):
-    ref, ref_lse = _expected(case, q_bits, splits)
+    ref, ref_lse = _expected(case, q_bits, effective_splits(case, splits))
     got = bits_of(out)
     mism = int((got != ref).sum())
     assert mism == 0, f"{tag}: {mism} BF16 mismatches"

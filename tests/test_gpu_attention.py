@@ -13,7 +13,7 @@ import numpy as np
 import pytest
 
 from tests import workloads
-from tests.device_cases import (query_subcase, run_hip, run_hip_debug, run_oracle, to_device, bits_of,
+from tests.device_cases import (effective_splits, query_subcase, run_hip, run_hip_debug, run_oracle, to_device, bits_of,
                                 default_cmp_capacity)
 
 pytestmark = pytest.mark.gpu
@@ -42,7 +42,11 @@ def kinds_with_rows(case):
     return used
 
 
-def compare(case, out, lse, splits, rows=None, tag=""):
+def compare(case, out, lse, splits, rows=None, tag="", merge_mode=0):
+    """HIP output of a launch of `case` planned at `splits` (run with the
+    library in `merge_mode`) against the checker on the partitions the
+    kernel actually ran (effective_splits)."""
+    splits = effective_splits(case, splits, merge_mode)
     ref, ref_lse, _ = run_oracle(case if rows is None else query_subcase(case, rows), splits)
     got = out if rows is None else out[rows]
     got_lse = lse if rows is None else lse[rows]
@@ -162,7 +166,7 @@ def test_head_groups_with_both_merge_placements(mode):
         for splits in (2, 5):
             say(f"[heads merge mode {mode}] splits={splits}")
             out, lse, op = run_hip(case, splits=splits)
-            compare(case, out, lse, splits, tag=f"heads 20 mode {mode} splits {splits}")
+            compare(case, out, lse, splits, tag=f"heads 20 mode {mode} splits {splits}", merge_mode=mode)
     finally:
         lib.sharedkv_c8_set_merge_mode(0)
 
@@ -201,6 +205,35 @@ def _golden_plans(z):
     return [tuple(int(v) for v in p) + (0, 1)[len(p) - 5:] for p in z["plans"]]
 
 
+@pytest.mark.parametrize("heads", [8, 4, 16])
+def test_joint_c128_rows(heads):
+    """One-partition C128 launches take joint rows (reference.py:254-267,
+    joint_dense) for rows whose window and compressed lists fit one tile
+    each: bit-exact with the checker's joint plan, and different from the
+    tiled plan's numbers (so the joint path is the one that ran).  Longer
+    rows (more than 128 compressed rows) and rows without compressed rows
+    stay tiled in the same launch; above eight heads every row is tiled."""
+    import oracle.oracle as ora
+    case = workloads.make_case(61, 128, [1, 2, 1, 1], [4096, 2000, 100, 17000], heads=heads)
+    say(f"[joint] heads {heads}")
+    out, lse, op = run_hip(case, splits=1)
+    host = workloads.oracle_case(case)
+    tiled, tiled_lse, _ = ora.tiled_attention(host, tile=128, splits=1, return_lse=True)
+    want, want_lse = tiled, tiled_lse
+    if heads <= 8:
+        want, want_lse, _ = ora.tiled_attention(host, tile=128, splits=1, return_lse=True, joint_dense=True)
+        joint_rows = [0, 1, 2]                 # counts 32, 15, 15; row 3 has none, row 4 has 132
+        assert (want[joint_rows] != tiled[joint_rows]).any()
+        np.testing.assert_array_equal(want[3:], tiled[3:])
+    diff = out != want
+    assert not diff.any(), f"{int(diff.sum())} BF16 mismatches"
+    np.testing.assert_allclose(lse, want_lse, rtol=0, atol=2e-6)
+    # Three partitions: tiled, whatever the row.
+    out3, _, op3 = run_hip(case, splits=3)
+    ref3, _, _ = ora.tiled_attention(host, tile=128, splits=3, return_lse=True)
+    assert np.array_equal(out3, ref3)
+
+
 @pytest.mark.parametrize("name", GOLDEN_NAMES)
 def test_against_reference_vectors(name):
     """HIP output vs reference.py's own tiled_quantized_reference output on
@@ -215,7 +248,7 @@ def test_against_reference_vectors(name):
     for bit except rare one-ulp exp flips (at most 0.1 %), LSE within 1e-5.
     Above eight heads (no residual codes) only the same-plan check applies."""
     import torch
-    from npu_sparse_attn_sharedkv_int8 import PreparedAttention, SharedKVCase
+    from npu_sparse_attn_sharedkv_int8 import PreparedAttention, SharedKVCase, c8_attention
     z = _golden(name)
     dev = "cuda"
     pool = lambda key, stride: torch.from_numpy(z[key]).to(dev).as_strided(  # noqa: E731
@@ -263,7 +296,12 @@ def test_against_reference_vectors(name):
                 (name, i, float(err.max()), float(err.mean()))
             np.testing.assert_allclose(own_lse, z[f"lse_{i}"][:live], rtol=0, atol=2e-3,
                                        err_msg=f"{name} plan {i}")
-        if tile != 128 or jd or js or dense or group != 1:
+        # Same-plan check where the stored plan is the HIP launch's plan at
+        # `splits`: 128-key tiles, ungrouped, and joint C128 rows exactly
+        # when the HIP plan takes them (one partition, at most eight heads,
+        # no explicit slots).
+        joint_here = c8_attention.joint_dense_plan(ratio, z["q"].shape[1], "ori_indices" in z.files)
+        if tile != 128 or js or dense or group != 1 or (splits == 1 and ratio == 128 and bool(jd) != joint_here):
             continue
         say(f"[reference vectors] {name} plan {i}: splits={splits}")
         got, got_lse = launch(splits)
@@ -590,14 +628,15 @@ def test_merge_modes_match_checker(mode):
         for splits in (2, 3, 7, 16):
             say(f"[merge mode {mode}] splits={splits}")
             out, lse, op = run_hip(case, splits=splits)
-            compare(case, out, lse, splits, tag=f"mode {mode} splits {splits}")
+            compare(case, out, lse, splits, tag=f"mode {mode} splits {splits}", merge_mode=mode)
         # Rows whose tiles all sit in partition 0 (no compressed rows yet) are
         # finalized by it; the others fold fewer partitions than launched.
-        short = workloads.make_case(28, 128, [2, 1, 3], [60, 130, 900])
+        # (The 17000-key request keeps the launch off the joint C128 plan.)
+        short = workloads.make_case(28, 128, [2, 1, 3, 1], [60, 130, 900, 17000])
         for splits in (3, 16):
             say(f"[merge mode {mode}] short rows splits={splits}")
             out, lse, op = run_hip(short, splits=splits)
-            compare(short, out, lse, splits, tag=f"mode {mode} short splits {splits}")
+            compare(short, out, lse, splits, tag=f"mode {mode} short splits {splits}", merge_mode=mode)
     finally:
         lib.sharedkv_c8_set_merge_mode(0)
 
@@ -635,7 +674,8 @@ def test_rows_with_negative_position_are_zero(mode, ratio):
                 assert np.array_equal(out[good], ref)
                 np.testing.assert_allclose(lse[good], ref_lse, rtol=0, atol=2e-6)
             else:
-                compare(query_subcase(case, good), out[good], lse[good], splits, tag="negative positions")
+                compare(query_subcase(case, good), out[good], lse[good], splits, tag="negative positions",
+                        merge_mode=mode)
     finally:
         lib.sharedkv_c8_set_merge_mode(0)
 
@@ -646,7 +686,9 @@ def test_repeated_fused_merges_on_changing_inputs():
     partition state or a ticket left behind by an earlier launch would show."""
     import torch
     from npu_sparse_attn_sharedkv_int8 import PreparedAttention
-    cases = [workloads.make_case(40 + i, 128 if i % 2 else 4, [2, 1, 2], [2500 + 97 * i, 7000 - 55 * i, 4100])
+    # The 17000-key request keeps the C128 launches off the joint plan (more
+    # than 128 compressed rows), so they fold partitions too.
+    cases = [workloads.make_case(40 + i, 128 if i % 2 else 4, [2, 1, 2], [2500 + 97 * i, 7000 - 55 * i, 17000])
              for i in range(4)]
     # Same geometry within a ratio: shared scales, block tables of one width.
     for first in (0, 1):
@@ -678,7 +720,7 @@ def test_repeated_fused_merges_on_changing_inputs():
     refs = {}
     for c, out, lse in outs:
         if c not in refs:
-            refs[c] = run_oracle(cases[c], 5)[:2]
+            refs[c] = run_oracle(cases[c], effective_splits(cases[c], 5))[:2]
         ref, ref_lse = refs[c]
         assert (bits_of(out) == ref).all(), c
         np.testing.assert_allclose(lse.cpu().numpy(), ref_lse, rtol=0, atol=2e-6)

@@ -142,7 +142,7 @@ def test_device_plan_of_padded_launches():
     # of a 600-key sequence have 1 + ceil(150 / 128) = 3 tiles, C128 rows of
     # 4096 keys 1 + 1, window-only rows 1 (explicit slots: ceil(K / 128)).
     assert plan(2, 64, 8, 4, 1024, [0, 1, 64], [600, 0]) == 3
-    assert plan(2, 64, 8, 128, 0, [0, 1, 64], [4096, 0]) == 2
+    assert plan(2, 64, 8, 128, 0, [0, 1, 64], [20000, 0]) == 3      # 1 + ceil(156 / 128) tiles
     assert plan(2, 64, 8, 1, 0, [0, 1, 64], [4096, 0]) == 2
     assert plan(2, 64, 8, 1, 0, [0, 1, 64], [4096, 0], ori_topk=384) == 3
     # Head groups count as rows: 16 heads, 4 live tokens of 32 -> 8 rows.
@@ -153,6 +153,25 @@ def test_device_plan_of_padded_launches():
     assert c8_attention.live_shape([0, 2, 9], [1, 8], 6) == (6, 8)
     assert c8_attention.live_shape([0, 0], [0], 4) == (0, 0)
     assert plan(3, 6, 8, 4, 1024, [0, 0, 0], [0, 0]) == 3     # nothing live
+
+
+def test_device_plan_of_joint_c128_launches():
+    """C128 launches whose live rows all fit one window and one compressed
+    tile (longest live sequence // 128 <= 128) run one partition per row
+    with joint rows; not above eight heads, with explicit slots, or (for
+    more than one partition) with a separate merge launch."""
+    plan = c8_attention.device_splits
+    short = [0, 1, 2, 3, 4]
+    assert plan(5, 4, 8, 128, 0, short, [4096] * 4) == 1
+    assert plan(1, 4, 8, 128, 0, short, [4096] * 4, fused=False) == 1
+    assert plan(5, 4, 8, 128, 0, short, [4096] * 4, fused=False) == 5
+    assert plan(5, 4, 8, 128, 0, short, [16511] * 4) == 1 and plan(5, 4, 8, 128, 0, short, [16512] * 4) == 5
+    assert plan(5, 4, 16, 128, 0, short, [4096] * 4) == 5                      # no residual codes
+    assert plan(5, 4, 8, 128, 0, short, [4096] * 4, ori_topk=128) == 5         # explicit slots
+    assert plan(5, 4, 8, 4, 1024, short, [4096] * 4) == 5                      # C4 keeps its plan
+    assert plan(3, 64, 8, 128, 0, list(range(9)) + [8] * 56, [4096] * 8 + [0] * 56) == 1   # padded
+    assert c8_attention.joint_dense_plan(128, 8, False) and c8_attention.joint_dense_plan(128, 4, False)
+    assert not c8_attention.joint_dense_plan(128, 9, False) and not c8_attention.joint_dense_plan(4, 8, False)
 
 
 def test_keyless_tokens_rule():

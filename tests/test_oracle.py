@@ -90,6 +90,15 @@ def test_plan_families_are_covered():
     assert any(p[5] for p in golden_plans(dense_dups))
 
 
+def test_joint_plans_need_residual_codes():
+    """reference.py:258 asserts residual quantization (at most eight heads)
+    for joint rows; the checker refuses such a plan outright."""
+    case = workloads.oracle_case(workloads.make_case(4, 128, [1], [4096], heads=16))
+    with pytest.raises(ValueError, match="code -11"):
+        ora.tiled_attention(case, 128, 1, joint_dense=True)
+    ora.tiled_attention(case, 128, 1)
+
+
 def test_query_group_one_is_the_ungrouped_plan():
     """reference.py:229-231 with query_group = 1 reduces to each query's own
     window and list: the grouped code path at G = 1 equals the default."""
