@@ -174,3 +174,13 @@ def test_scratch_allocator_grows_and_keys_by_stream():
     assert d.data_ptr() not in (a.data_ptr(), c.data_ptr())
     vllm_adapter.check_device(device)
 
+
+
+def test_observer_on_device_reproduces_reference_calibrate(tmp_path):
+    """The calibration observer on GPU tensors (device accumulators, one
+    masked reduction per write), merged from two ranks' files: equal to the
+    reference's CacheQuantization.calibrate output (golden calibrate.npz)
+    bit for bit."""
+    from tests.test_integration import observe_calibrate_vector
+    got, want = observe_calibrate_vector(tmp_path, "cuda")
+    np.testing.assert_array_equal(got.numpy(), want)

@@ -129,6 +129,43 @@ def test_merge_takes_channel_maxima_over_ranks(tmp_path):
         calibration.merge_observations(paths, required=["missing"])
 
 
+def observe_calibrate_vector(tmp_path, device):
+    """The golden calibrate.npz samples (written by the reference's
+    CacheQuantization.calibrate, reference.py:32-37) observed as cache writes
+    by two ranks' observers on `device`, merged at margin 1: returns
+    (merged scale, golden scale)."""
+    from pathlib import Path
+    import shutil
+    z = np.load(Path(__file__).resolve().parent / "golden" / "vectors" / "calibrate.npz")
+    samples = [torch.from_numpy(z["sample0"]),
+               torch.from_numpy(z["sample1_bf16"].view(np.int16)).view(torch.bfloat16),
+               torch.from_numpy(z["sample2"])]
+    files = []
+    for rank, group in enumerate((samples[:1], samples[1:])):
+        directory = tmp_path / f"r{rank}"
+        obs = calibration.CacheObserver(directory)
+        (directory / "collect").touch()
+        for sample in group:
+            rows = sample.reshape(-1, 512).to(device)
+            cache = torch.zeros(max(1, (rows.shape[0] + 31) // 32), 32, 1, 512, dtype=torch.int8, device=device)
+            obs.observe("g.l0", "ori", cache, rows, torch.arange(rows.shape[0], device=device))
+        obs.flush()
+        files.append(shutil.copy(directory / "rank_00.pt", tmp_path / f"rank_{rank:02d}.pt"))
+    merged = calibration.merge_observations(files, margin=1.0, required=["g.l0.ori"])
+    return merged["scales"]["g.l0.ori"], z["scale"]
+
+
+def test_observer_and_merge_reproduce_reference_calibrate(tmp_path):
+    """Observer + merge at margin 1 equal CacheQuantization.calibrate on the
+    same rows bit for bit (golden calibrate.npz, including the 1e-8 floor of
+    an all-zero channel): the merge's FP32 sequence max -> fp32(margin *
+    max) / 127 -> floor is the reference's at margin 1, and margin 1.1
+    follows docs/kv-cache.md's formula left to right."""
+    got, want = observe_calibrate_vector(tmp_path, "cpu")
+    np.testing.assert_array_equal(got.numpy(), want)
+    assert got[7] == np.float32(1e-8)
+
+
 def test_scale_file_checks(tmp_path):
     good = {"protocol": "sharedkv-c8-v1", "scales": {"a.ori": torch.full((512,), 0.5)}}
     torch.save(good, tmp_path / "s.pt")
