@@ -539,6 +539,59 @@ def test_graph_at_capacity_replayed_at_fewer_live_sequences():
     del graph
 
 
+def test_graph_switches_between_joint_and_tiled_c128_plans():
+    """One C128 launch captured at a capacity of 16 one-token requests (5
+    partitions), replayed while the live metadata changes: all rows short
+    (the device runs one partition per row with joint rows), one row longer
+    than 128 compressed rows (the launch's own 5 partitions), and 4 live
+    requests (joint again, the rest padding).  Each replay is bit-exact with
+    the checker on the plan c8_attention.device_splits names."""
+    import torch
+    from npu_sparse_attn_sharedkv_int8 import PreparedAttention, c8_attention
+    cap = 16
+    lengths = [4096 + 311 * i for i in range(cap - 1)] + [20000]
+    case = workloads.make_case(27, 128, [1] * cap, lengths)
+    dev, oscale, cscale, keep = to_device(case)
+    op = PreparedAttention(dev, oscale, cscale, return_lse=True)
+    assert op.splits == 5
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        op.run()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            op.run()
+    torch.cuda.current_stream().wait_stream(stream)
+    short = lengths[:-1] + [3000]
+    variants = [("all short", list(range(cap + 1)), short, 1),
+                ("one long", list(range(cap + 1)), lengths, 5),
+                ("4 live", list(range(5)) + [4] * (cap - 4), short[:4] + [0] * (cap - 4), 1),
+                ("all short again", list(range(cap + 1)), short, 1)]
+    for tag, cu, lens, want in variants:
+        cu, lens = np.array(cu, np.int32), np.array(lens, np.int32)
+        plan = c8_attention.device_splits(op.splits, cap, 8, 128, 0, cu, lens)
+        assert plan == want, (tag, plan)
+        dev.cu_q.copy_(torch.from_numpy(cu))
+        dev.seq_lens.copy_(torch.from_numpy(lens))
+        op.out.fill_(float("nan"))
+        op.lse.fill_(float("nan"))
+        torch.cuda.synchronize()
+        say(f"[joint graph] {tag}: {plan} partition(s)")
+        graph.replay()
+        torch.cuda.synchronize()
+        live = int(cu[-1])
+        out, lse = bits_of(op.out), op.lse.cpu().numpy()
+        assert not out[live:].any() and not lse[live:].any()
+        sub = dict(case, cu_q=cu[:live + 1] if live < cap else cu, seq_lens=lens[:live] if live < cap else lens,
+                   q=case["q"][:live])
+        ref, ref_lse, _ = run_oracle(sub, plan)
+        diff = out[:live] != ref
+        assert not diff.any(), f"{tag}: {int(diff.sum())} BF16 mismatches"
+        np.testing.assert_allclose(lse[:live], ref_lse, rtol=0, atol=2e-6)
+    del graph
+
+
 def test_rebind_same_geometry():
     import torch
     from npu_sparse_attn_sharedkv_int8 import PreparedAttention
