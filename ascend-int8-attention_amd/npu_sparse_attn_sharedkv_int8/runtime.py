@@ -1,14 +1,19 @@
 """Native launcher for libsharedkv_hip.so (reference runtime.py:1-42 and the
 pybind host bridges csrc/host/launch.cpp:98-115, c8_launch.cpp:20-43).
 
-The reference binds its launchers through a torch_npu pybind module that
-reads the caller's current stream.  Here the C ABI is bound with ctypes and
-the caller's current HIP stream is read from torch; every launch returns a
+The reference launches through a torch_npu pybind module that reads the
+caller's current stream and releases the GIL.  Here launches go through
+_sharedkv_host, a CPython extension over the C ABI (csrc/host_bridge.cpp) that
+releases the GIL around each launch, with torch's current raw HIP stream
+passed in; SHAREDKV_USE_CTYPES=1 binds the same C ABI with ctypes instead
+(the reference's switch of the same name).  Every launch returns a
 hipError_t that is raised as RuntimeError.  There is no host-side fallback:
-a missing library raises at load time.
+a missing library or bridge raises at load time.
 """
 import ctypes
 from functools import lru_cache
+import importlib.machinery
+import importlib.util
 import os
 from types import SimpleNamespace
 
@@ -88,8 +93,23 @@ def library():
 
 
 def _stream(device):
+    """Raw handle of torch's current HIP stream on `device` (an index, or
+    None for the current device)."""
     import torch
-    return torch.cuda.current_stream(device).cuda_stream
+    return torch._C._cuda_getCurrentRawStream(torch.cuda.current_device() if device is None else device)
+
+
+@lru_cache(maxsize=1)
+def bridge():
+    """The compiled launch bridge (_sharedkv_host), loaded after library() so
+    that it binds the same libsharedkv_hip.so."""
+    library()
+    path = native_path("_sharedkv_host.so")
+    loader = importlib.machinery.ExtensionFileLoader("_sharedkv_host", str(path))
+    spec = importlib.util.spec_from_file_location("_sharedkv_host", str(path), loader=loader)
+    module = importlib.util.module_from_spec(spec)
+    loader.exec_module(module)
+    return module
 
 
 def _check(code, what):
@@ -98,19 +118,24 @@ def _check(code, what):
 
 
 class _Host:
-    """Counterpart of the reference's pybind host module (launch.cpp:105-115)."""
+    """Counterpart of the reference's pybind host module (launch.cpp:105-115):
+    the compiled bridge, or ctypes over the same C ABI."""
 
-    def __init__(self, lib):
+    def __init__(self, lib, use_ctypes=False):
         self.lib = lib
         self.attention_args_size = lib.sharedkv_attention_args_size()
         self.cache_args_size = lib.sharedkv_cache_args_size()
         self.attention_variant_count = ATTENTION_VARIANT_COUNT
+        self.bridge = None if use_ctypes else bridge()
         self._launchers = {VARIANT_SPARSE: lib.launch_sharedkv_c8_sparse,
                            VARIANT_DENSE: lib.launch_sharedkv_c8_dense,
                            VARIANT_SPARSE_SMALL: lib.launch_sharedkv_c8_sparse_small}
 
     def attention(self, address, blocks, variant, device):
         """Launch on the current stream of `device` (c8_launch.cpp:20-25)."""
+        if self.bridge is not None:
+            self.bridge.attention(address, blocks, variant, _stream(device))
+            return
         fn = self._launchers.get(variant)
         if fn is None:
             raise ValueError("Invalid C8 variant")   # c8_launch.cpp:17
@@ -123,6 +148,9 @@ class _Host:
         self.attention(address, blocks, variant, device)
 
     def cache_write(self, address, blocks, device):
+        if self.bridge is not None:
+            self.bridge.cache_write(address, blocks, _stream(device))
+            return
         _check(self.lib.launch_cache_write(blocks, _stream(device), address), "sharedkv cache write")
 
     def cache_write_queued(self, address, blocks, device):
@@ -135,12 +163,14 @@ class _Host:
 
 @lru_cache(maxsize=1)
 def native_launcher():
-    """reference runtime.py:12-31; SHAREDKV_USE_CTYPES / SHAREDKV_HOST_QUEUE
-    select among identical launch paths here, so both are accepted."""
+    """reference runtime.py:12-31.  SHAREDKV_USE_CTYPES=1 launches through
+    ctypes instead of the compiled bridge; SHAREDKV_HOST_QUEUE=1 selects the
+    queued entry points, which equal the direct ones here (a HIP launch
+    copies its arguments)."""
     for name in ("SHAREDKV_USE_CTYPES", "SHAREDKV_HOST_QUEUE"):
         if os.environ.get(name, "0") not in ("0", "1"):
             raise ValueError(f"{name} must be 0 or 1")
-    host = _Host(library())
+    host = _Host(library(), use_ctypes=os.environ.get("SHAREDKV_USE_CTYPES") == "1")
     if os.environ.get("SHAREDKV_HOST_QUEUE") == "1":
         return SimpleNamespace(attention=host.attention_queued, cache_write=host.cache_write_queued,
                                attention_args_size=host.attention_args_size,

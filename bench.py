@@ -239,10 +239,21 @@ def eager_latency(op, stream, torch, calls=50):
             torch.cuda.synchronize()
             wall.append((time.perf_counter() - t0) * 1e6)
             kernel.append(a.elapsed_time(b) * 1e3)
+    # The same wall-clock measure around a one-element torch add: the floor
+    # of one eager launch plus synchronisation on this runtime.
+    tiny = torch.zeros(1, device="cuda")
+    floor = []
+    with torch.cuda.stream(stream):
+        for _ in range(calls):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            tiny.add_(1)
+            torch.cuda.synchronize()
+            floor.append((time.perf_counter() - t0) * 1e6)
     return {"calls": calls, "kernel_us_median": statistics.median(kernel),
-            "call_us_median": statistics.median(wall),
+            "call_us_median": statistics.median(wall), "null_call_us_median": statistics.median(floor),
             "note": "each launch alone: events on its stream around one run(); call = host wall of run() + "
-                    "synchronize, launch overhead included"}
+                    "synchronize, launch overhead included; null call = the same around a one-element torch add"}
 
 
 def main():

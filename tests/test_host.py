@@ -104,6 +104,23 @@ def test_launch_rejects_grids_past_the_limit():
     assert lib.launch_cache_write(1, None, ctypes.byref(w)) == 1
 
 
+def test_compiled_bridge_loads_and_rejects_bad_calls_without_a_device():
+    """The CPython launch bridge (csrc/host_bridge.cpp) binds the same
+    library; malformed calls raise before any HIP call."""
+    bridge = runtime.bridge()
+    assert callable(bridge.attention) and callable(bridge.cache_write)
+    with pytest.raises(ValueError, match="variant"):
+        bridge.attention(0x1000, 1, 99, 0)
+    with pytest.raises(ValueError):
+        bridge.attention(0, 1, runtime.VARIANT_SPARSE, 0)           # no argument block
+    with pytest.raises(ValueError):
+        bridge.cache_write(0x1000, 1 << 33, 0)                       # more work-groups than a launch takes
+    with pytest.raises(TypeError):
+        bridge.attention(0x1000, 1, runtime.VARIANT_SPARSE)
+    with pytest.raises(OverflowError):
+        bridge.attention(-1, 1, runtime.VARIANT_SPARSE, 0)
+
+
 def test_host_plan():
     assert c8_attention.max_tiles(4, 1024) == 9
     assert c8_attention.max_tiles(128, 0, 4096) == 2
