@@ -14,6 +14,7 @@ import pytest
 
 from tests import workloads
 from tests.device_cases import (effective_splits, query_subcase, run_hip, run_hip_debug, run_oracle, to_device, bits_of,
+                                torch_bf16,
                                 default_cmp_capacity)
 
 pytestmark = pytest.mark.gpu
@@ -590,6 +591,105 @@ def test_graph_switches_between_joint_and_tiled_c128_plans():
         assert not diff.any(), f"{tag}: {int(diff.sum())} BF16 mismatches"
         np.testing.assert_allclose(lse[:live], ref_lse, rtol=0, atol=2e-6)
     del graph
+
+
+@pytest.mark.parametrize("ratio", [4, 128])
+def test_one_graph_across_live_batch_and_length_states(ratio):
+    """Flow of the reference's tests/npu/test_dynamic.py:18-80: one launch
+    captured at a capacity of 8 requests x 6 query tokens, replayed three
+    times per live state while the live batch and lengths change (8, 4, 1, 6
+    and 0 live requests; equal and mixed lengths).  Before each state the Q
+    rows, outputs, LSE and partition states are poisoned with NaN; padding
+    rows must come back zero and live rows bit-exact with the checker on the
+    plan the device picks.  (The merge tickets in the workspace are not
+    poisoned: this build's fused merge keeps them, zero between launches.)"""
+    import torch
+    from npu_sparse_attn_sharedkv_int8 import PreparedAttention
+    maximum = 8193 if ratio == 4 else 40000       # the reference runs C128 to 135000; 40000 keeps the case small
+    full = workloads.make_case(70 + ratio, ratio, [6] * 8, [maximum] * 8, index_mode="uniform")
+    dev, oscale, cscale, keep = to_device(full)
+    op = PreparedAttention(dev, oscale, cscale, return_lse=True)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        op.run()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            op.run()
+    torch.cuda.current_stream().wait_stream(stream)
+    short = [1024, 1027, 1028, 8192] if ratio == 4 else [16384, 20000, 24000, 32768]
+    mixed = [1024, 8192, 1028, 4097, 777] if ratio == 4 else [12289, 39999, 16000, 9001, 25129]
+    states = [(8, [short[0]] * 8), (4, [short[1]] * 4), (1, [short[2]]), (6, [short[3]] * 6), (0, []),
+              (8, [maximum] * 8), (5, mixed)]
+    for batch, lengths in states:
+        cu = np.array([min(6 * b, 6 * batch) for b in range(9)], np.int32)
+        lens = np.array(lengths + [0] * (8 - batch), np.int32)
+        # Q rows of this state: the case's own; rows past the live ones NaN.
+        q = full["q"].copy()
+        q[6 * batch:] = 0x7FC0
+        dev.q.copy_(torch_bf16(q, "cuda"))
+        dev.cu_q.copy_(torch.from_numpy(cu))
+        dev.seq_lens.copy_(torch.from_numpy(lens))
+        if op.partial is not None:
+            op.partial.fill_(float("nan"))
+        op.out.fill_(float("nan"))
+        op.lse.fill_(float("nan"))
+        torch.cuda.synchronize()
+        say(f"[dynamic c{ratio}] {batch} live, lengths {lengths[:3]}")
+        for _ in range(3):
+            graph.replay()
+        torch.cuda.synchronize()
+        out, lse = bits_of(op.out), op.lse.cpu().numpy()
+        live = 6 * batch
+        assert not out[live:].any() and not lse[live:].any(), "padding rows are not zero"
+        if not batch:
+            continue
+        sub = dict(full, q=q[:live], cu_q=cu[:batch + 1], seq_lens=lens[:batch])
+        plan = effective_splits(dict(full, q=q, cu_q=cu, seq_lens=lens), op.splits)
+        ref, ref_lse, _ = run_oracle(sub, plan)
+        diff = out[:live] != ref
+        assert not diff.any(), f"{batch} live: {int(diff.sum())} BF16 mismatches"
+        np.testing.assert_allclose(lse[:live], ref_lse, rtol=0, atol=2e-6)
+    del graph
+
+
+@pytest.mark.parametrize("ratio", [1, 4, 128])
+def test_queued_launches_with_rapid_rebinding(ratio):
+    """Flow of the reference's tests/npu/test_queue.py:17-60: per stream (the
+    current one, then an auxiliary one), 32 launches of one operator, each
+    rebound to a query its producer (a scaling kernel) has just written and
+    to a fresh output, with the case reference dropped right after the
+    launch; one synchronisation at the end.  Every output is bit-exact with
+    the checker on its own query (the reference asserts closeness to its
+    CPU model; this build's bar is bit equality)."""
+    import dataclasses
+    import torch
+    from npu_sparse_attn_sharedkv_int8 import PreparedAttention
+    case = workloads.make_case(2801, ratio, [6], [513])
+    dev, oscale, cscale, keep = to_device(case)
+    op = PreparedAttention(dev, oscale, cscale)
+    factors = (1.0, -0.75, 0.5, -1.25)
+    expected = []
+    for factor in factors:
+        q_bits = bits_of((dev.q * factor).contiguous())
+        expected.append(run_oracle(dict(case, q=q_bits), effective_splits(case, op.splits))[0])
+    for auxiliary in (False, True):
+        stream = torch.cuda.Stream() if auxiliary else torch.cuda.current_stream()
+        stream.wait_stream(torch.cuda.current_stream())
+        outputs = []
+        with torch.cuda.stream(stream):
+            for index in range(32):
+                query = dev.q * factors[index % 4]
+                output = torch.empty_like(query)
+                op._rebind_same_geometry(dataclasses.replace(dev, q=query), output=output)
+                op.run()
+                outputs.append(output)
+                op.case = None
+        stream.synchronize()
+        say(f"[queue] ratio {ratio} auxiliary {auxiliary}: 32 launches")
+        for index, output in enumerate(outputs):
+            assert np.array_equal(bits_of(output), expected[index % 4]), (auxiliary, index)
 
 
 def test_rebind_same_geometry():
