@@ -40,6 +40,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
 #include <mutex>
 
 #include "sharedkv_hip.h"
@@ -1356,7 +1357,9 @@ int check_attention(const SharedKVArgs *a)
     return 0;
 }
 
-int g_merge_mode = 0;   // 0: fused (last partition folds), 1: separate merge launch
+// 0: fused (last partition folds), 1: separate merge launch.  A process-wide
+// setting (tests and bench.py use it); read once per launch.
+std::atomic<int> g_merge_mode{0};
 
 template <bool DEBUG, bool ANYH>
 void launch_variant(hipStream_t stream, const SharedKVArgs *a, const SharedKVDebug &dbg, bool slots, uint32_t grid,
@@ -1387,7 +1390,7 @@ int launch_attention(hipStream_t stream, const SharedKVArgs *a, const SharedKVDe
     const uint32_t rows = a->tokens * head_groups(a->heads);
     const uint32_t items = rows * splits;
     const uint32_t grid = (items + 7u) & ~7u;
-    const uint32_t fused = splits > 1 && g_merge_mode == 0;
+    const uint32_t fused = splits > 1 && g_merge_mode.load(std::memory_order_relaxed) == 0;
     // Debug dumps hold eight heads and one original tile (list places 0..127) per row.
     if (DEBUG && (a->heads != HEADS || (a->oriIndices && a->oriTopk > N))) return (int)hipErrorInvalidValue;
     const bool slots = a->oriIndices != 0;
@@ -1519,7 +1522,7 @@ uint64_t sharedkv_c8_noalloc_scratch_bytes(void) { return NOALLOC_SCRATCH_BYTES;
 int sharedkv_c8_set_merge_mode(int mode)
 {
     if (mode != 0 && mode != 1) return (int)hipErrorInvalidValue;
-    g_merge_mode = mode;
+    g_merge_mode.store(mode, std::memory_order_relaxed);
     return (int)hipSuccess;
 }
 

@@ -94,9 +94,12 @@ def library():
 
 def _stream(device):
     """Raw handle of torch's current HIP stream on `device` (an index, or
-    None for the current device)."""
+    None for the current device).  torch._C._cuda_getCurrentRawStream skips
+    building a Stream object; builds without it use the public call."""
     import torch
-    return torch._C._cuda_getCurrentRawStream(torch.cuda.current_device() if device is None else device)
+    index = torch.cuda.current_device() if device is None else device
+    raw = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+    return raw(index) if raw is not None else torch.cuda.current_stream(index).cuda_stream
 
 
 @lru_cache(maxsize=1)
