@@ -346,6 +346,43 @@ __device__ __forceinline__ void fold_states(const __amdgpu_buffer_rsrc_t states,
     if (lse_row && (tid & 63) == 0) lse_row[h] = top + logf(dsum);
 }
 
+// The same fold for more than eight partitions, in the same order, with the
+// loads of each partition issued inside the loop: holding sixteen
+// partitions' values at once would spill registers in the attention kernel.
+template <int POLICY>
+__device__ __forceinline__ void fold_states_wide(const __amdgpu_buffer_rsrc_t states, int S, int tid,
+                                                 uint16_t *out_row, float *lse_row, int heads)
+{
+    const int h = tid >> 6, col = (tid & 63) * 8;
+    const int head_base = h * PART_FLOATS * 4;
+    const int part_step = HEADS * PART_FLOATS * 4;
+    float top = state_load<POLICY>(states, head_base + 512 * 4);
+    for (int sp = 1; sp < S; ++sp) top = fmaxf(top, state_load<POLICY>(states, head_base + sp * part_step + 512 * 4));
+    float dsum = 0.0f;
+    float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    for (int sp = 0; sp < S; ++sp) {
+        const int at = head_base + sp * part_step;
+        const float f = sk_expf_nonpos(state_load<POLICY>(states, at + 512 * 4) - top);
+        dsum = dsum + state_load<POLICY>(states, at + 513 * 4) * f;
+        const f32x4 v0 = state_load4<POLICY>(states, at + col * 4);
+        const f32x4 v1 = state_load4<POLICY>(states, at + (col + 4) * 4);
+        acc[0] = acc[0] + v0.x * f;
+        acc[1] = acc[1] + v0.y * f;
+        acc[2] = acc[2] + v0.z * f;
+        acc[3] = acc[3] + v0.w * f;
+        acc[4] = acc[4] + v1.x * f;
+        acc[5] = acc[5] + v1.y * f;
+        acc[6] = acc[6] + v1.z * f;
+        acc[7] = acc[7] + v1.w * f;
+    }
+    uint32_t w[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) w[e] = pack_bf16(acc[2 * e] / dsum, acc[2 * e + 1] / dsum);
+    if (heads < HEADS && h >= heads) return;
+    *reinterpret_cast<v4i *>(out_row + h * D + col) = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+    if (lse_row && (tid & 63) == 0) lse_row[h] = top + logf(dsum);
+}
+
 template <int POLICY>
 __device__ __forceinline__ void fold_row(const __amdgpu_buffer_rsrc_t states, int S, int tid, uint16_t *out_row,
                                          float *lse_row, int heads = HEADS)
@@ -356,7 +393,7 @@ __device__ __forceinline__ void fold_row(const __amdgpu_buffer_rsrc_t states, in
     else if (S == 5) fold_states<5, POLICY>(states, S, tid, out_row, lse_row, heads);
     else if (S == 6) fold_states<6, POLICY>(states, S, tid, out_row, lse_row, heads);
     else if (S <= 8) fold_states<8, POLICY>(states, S, tid, out_row, lse_row, heads);
-    else fold_states<16, POLICY>(states, S, tid, out_row, lse_row, heads);
+    else fold_states_wide<POLICY>(states, S, tid, out_row, lse_row, heads);
 }
 
 // SLOTS: the original kind is the explicit physical slot list of the row
