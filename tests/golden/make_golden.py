@@ -17,8 +17,8 @@ expected outputs, stored as .npz under tests/golden/vectors/.
 Plans are (tile_size, splits, joint_dense, joint_sparse, joint_tile_limit,
 dense_c4, query_group), the keyword arguments of tiled_quantized_reference.
 Besides 128-key plans, every case family carries the plans the reference's
-own device picks for that shape (SURVEY of the reference's c4_wide.h:16-41,
-c128.cpp:79-105 and tests/support/attention_cases.py:56-111): config 0's
+own device picks for that shape (the planners in the reference's
+c4_wide.h:16-41, c128.cpp:79-105 and tests/support/attention_cases.py:56-111): config 0's
 joint C128 row, config 1's 512-key tiles over 3 partitions, 512-key single
 partition tiles for the batched, prefill and long-context C4/C128 slices,
 and query groups of 2 (paired C4/C128 plans) and 4.
