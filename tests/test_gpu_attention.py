@@ -755,6 +755,31 @@ def test_long_c128_rows_span_two_code_chunks():
         compare(case, out, lse, splits, tag=f"long c128 splits {splits}")
 
 
+def test_ctypes_and_bridge_launches_agree():
+    """The compiled launch bridge (the default) and the ctypes binding of the
+    same C ABI (SHAREDKV_USE_CTYPES=1) launch the same kernels: identical
+    outputs, and both raise on a rejected argument block."""
+    import ctypes
+    import torch
+    from npu_sparse_attn_sharedkv_int8 import PreparedAttention, runtime
+    case = workloads.make_case(33, 4, [2, 1], [5000, 900], index_mode="mixed")
+    dev, oscale, cscale, keep = to_device(case)
+    op = PreparedAttention(dev, oscale, cscale, return_lse=True)
+    outs = []
+    for use_ctypes in (False, True):
+        host = runtime._Host(runtime.library(), use_ctypes=use_ctypes)
+        op.out.fill_(0)
+        host.attention(op.argument_address, op.blocks, op.variant, op.device_index)
+        torch.cuda.synchronize()
+        outs.append(bits_of(op.out))
+        bad = type(op.args).from_buffer_copy(op.args)
+        bad.splits = 0                                   # rejected by the C ABI's checks
+        with pytest.raises(RuntimeError, match="hipError_t"):
+            host.attention(ctypes.addressof(bad), op.blocks, op.variant, op.device_index)
+    assert np.array_equal(outs[0], outs[1])
+    compare(case, outs[0], op.lse.cpu().numpy(), op.splits, tag="bridge")
+
+
 def test_empty_launch_is_a_no_op():
     import torch
     from npu_sparse_attn_sharedkv_int8 import PreparedAttention
