@@ -191,6 +191,17 @@ def test_device_plan_of_joint_c128_launches():
     assert not c8_attention.joint_dense_plan(128, 9, False) and not c8_attention.joint_dense_plan(4, 8, False)
 
 
+def test_device_plan_constants_match_the_host_rule():
+    """The kernel's re-plan uses the host's partition rule: its constants
+    (csrc/sharedkv_c8.hip) equal c8_attention's."""
+    src = (ROOT / "ascend-int8-attention_amd" / "csrc" / "sharedkv_c8.hip").read_text()
+    found = re.search(r"constexpr int32_t PLAN_CUS = (\d+), PLAN_FEW = (\d+), PLAN_MANY = (\d+);", src)
+    assert found, "plan constants not found in the kernel source"
+    assert tuple(int(x) for x in found.groups()) == (c8_attention.CORES, c8_attention.SPLITS_FEW_ROWS,
+                                                      c8_attention.SPLITS_MANY_ROWS)
+    assert re.search(r"constexpr uint32_t MAX_SPLITS = (\d+);", src).group(1) == str(c8_attention.MAX_SPLITS)
+
+
 def test_keyless_tokens_rule():
     """Tokens the kernel zero-fills: past the live end, outside every live
     request, or at a negative position; the checker (like the reference,
