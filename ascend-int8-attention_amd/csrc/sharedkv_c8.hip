@@ -230,15 +230,26 @@ __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(
 // not track it: its own tracking cannot tell the two ring buffers apart and
 // would wait for the next tile's DMA before every LDS read.  The callers
 // order these copies with vm_wait and lds_barrier instead.  M0 carries the
-// LDS address (the compiler keeps nothing live in M0 in this file).
+// LDS address (the compiler keeps nothing live in M0 in this file).  NT sets
+// the non-temporal cache policy, for launches whose KV rows are read about
+// once (decode: few query tokens per sequence).  Prefill launches, whose
+// query tokens re-read the same rows from L2, keep the default policy.
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
+template <bool NT>
 __device__ __forceinline__ void dma16(uint64_t src, uint32_t lds)
 {
-    asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" :: "v"(src), "s"(lds) : "memory", "m0");
+    if (NT)
+        asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off nt" :: "v"(src), "s"(lds) : "memory", "m0");
+    else
+        asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" :: "v"(src), "s"(lds) : "memory", "m0");
 }
 #pragma clang diagnostic pop
 
+// Query tokens per sequence slot up to which a launch's KV copies are
+// non-temporal: C4 rows of two tokens' top-k lists rarely coincide; the C128
+// tokens of one sequence all read the same compressed rows.
+constexpr uint32_t STREAM_TOKENS_C4 = 4, STREAM_TOKENS_C128 = 1;
 constexpr int QSTAGE = D + 16;   // row stride of the Q code staging area
 constexpr int DMA_PER_TILE = N * D / 1024 / WAVES;   // LDS DMA instructions per wave and tile
 static_assert(DMA_PER_TILE == 8, "vm_wait<8> covers one tile in flight");
@@ -407,7 +418,7 @@ __device__ __forceinline__ void fold_row(const __amdgpu_buffer_rsrc_t states, in
 // written.  Above eight heads the Q and P residual codes are zero
 // (reference.py:221-222: residual quantization only for <= 8 heads), which
 // leaves every other operation as it is.  Without ANYH, heads == 8.
-template <int RATIO, bool DEBUG, bool SLOTS, bool ANYH>
+template <int RATIO, bool DEBUG, bool SLOTS, bool ANYH, bool STREAM>
 __global__ void __launch_bounds__(THREADS, 1)   // one work-group per CU: the 128 KiB tile ring fills the LDS
 c8_attention(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, const uint64_t cmp_indices,
              const uint32_t batch_arg, const uint32_t topk_arg, const uint32_t heads_arg, const uint32_t splits,
@@ -828,7 +839,7 @@ c8_attention(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base
             if (k >= count) break;
             const int r = r0 + k;
             const int chunk = c ^ r ^ (hx << 3);   // swz(16 wave + 2 r + h)
-            dma16(ra[k >> 1][k & 1] + (uint32_t)(chunk << 4), (uint32_t)uni((int)(dst + 2 * r * D)));
+            dma16<STREAM>(ra[k >> 1][k & 1] + (uint32_t)(chunk << 4), (uint32_t)uni((int)(dst + 2 * r * D)));
         }
     };
     auto issue_tile = [&](int i, int buf) { issue_rows(i, buf, 0, DMA_PER_TILE); };
@@ -1402,14 +1413,17 @@ template <bool DEBUG, bool ANYH>
 void launch_variant(hipStream_t stream, const SharedKVArgs *a, const SharedKVDebug &dbg, bool slots, uint32_t grid,
                     uint32_t splits, uint32_t rows, uint32_t fused)
 {
-    auto kernel = &c8_attention<1, DEBUG, false, ANYH>;
-    if (slots)
-        kernel = a->ratio == 4 ? &c8_attention<4, DEBUG, true, ANYH>
-               : a->ratio == 128 ? &c8_attention<128, DEBUG, true, ANYH> : &c8_attention<1, DEBUG, true, ANYH>;
-    else if (a->ratio == 4)
-        kernel = &c8_attention<4, DEBUG, false, ANYH>;
+    // Decode-shaped launches stream their KV rows with the non-temporal
+    // policy; window-only (ratio 1) launches keep the default.
+    const uint32_t per_slot = a->ratio == 4 ? STREAM_TOKENS_C4 : a->ratio == 128 ? STREAM_TOKENS_C128 : 0;
+    const bool streamed = !DEBUG && (uint64_t)a->tokens <= (uint64_t)per_slot * a->batch;
+    auto kernel = slots ? &c8_attention<1, DEBUG, true, ANYH, false> : &c8_attention<1, DEBUG, false, ANYH, false>;
+    if (a->ratio == 4)
+        kernel = slots ? (streamed ? &c8_attention<4, DEBUG, true, ANYH, !DEBUG> : &c8_attention<4, DEBUG, true, ANYH, false>)
+                       : (streamed ? &c8_attention<4, DEBUG, false, ANYH, !DEBUG> : &c8_attention<4, DEBUG, false, ANYH, false>);
     else if (a->ratio == 128)
-        kernel = &c8_attention<128, DEBUG, false, ANYH>;
+        kernel = slots ? (streamed ? &c8_attention<128, DEBUG, true, ANYH, !DEBUG> : &c8_attention<128, DEBUG, true, ANYH, false>)
+                       : (streamed ? &c8_attention<128, DEBUG, false, ANYH, !DEBUG> : &c8_attention<128, DEBUG, false, ANYH, false>);
     // The leading scalar arguments are the ones the first loads need; the
     // build preloads them into SGPRs (-amdgpu-kernarg-preload-count), so
     // those loads do not wait for a read of the argument block.
