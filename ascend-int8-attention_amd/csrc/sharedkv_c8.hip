@@ -262,6 +262,9 @@ struct alignas(16) Shared {
     float asc[2][HEADS];            // alpha * softmax_scale per kind
     int32_t scan[WAVES];
     int32_t misc[8];
+    uint64_t listed[2];             // joint C4 rows: compressed rows 0-127 with multiplicity > 0
+    int32_t mult[N];                // joint C4 rows: multiplicity of compressed row r among the top-k entries
+    float bias[N];                  // joint C4 rows: log(multiplicity) of compressed list position j
     float scale[2][D];              // channel scales of the window / compressed cache
     int8_t p[16 * PROW];            // P codes [MFMA row][key]
     int32_t code[CODE_TILES * N];   // row codes of the resident tiles: page * 32 + row, -1 masked
@@ -418,7 +421,7 @@ __device__ __forceinline__ void fold_row(const __amdgpu_buffer_rsrc_t states, in
 // written.  Above eight heads the Q and P residual codes are zero
 // (reference.py:221-222: residual quantization only for <= 8 heads), which
 // leaves every other operation as it is.  Without ANYH, heads == 8.
-template <int RATIO, bool DEBUG, bool SLOTS, bool ANYH, bool STREAM>
+template <int RATIO, bool DEBUG, bool SLOTS, bool ANYH, bool STREAM, bool JOINT>
 __global__ void __launch_bounds__(THREADS, 1)   // one work-group per CU: the 128 KiB tile ring fills the LDS
 c8_attention(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, const uint64_t cmp_indices,
              const uint32_t batch_arg, const uint32_t topk_arg, const uint32_t heads_arg, const uint32_t splits,
@@ -526,17 +529,22 @@ c8_attention(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base
         }
         return longest;
     };
-    // Joint plan (C128): when every live row's window and compressed lists
-    // fit one tile each, the launch runs as one partition per row and those
-    // rows take one softmax over both kinds, as the reference device's
-    // one-split C128 plans do (c128.cpp:79-105, attention_impl.h:94-100).
-    // Work items of the other partitions have nothing to do.  A launch with
-    // a separate merge keeps its plan; c8_attention.device_splits mirrors
-    // the rule.
-    if (RATIO == 128 && !DEBUG && !SLOTS && resid && (fused || S == 1) && live_rows > 0 &&
+    // Joint plan (JOINT: every C128 kernel, and C4 kernels launched for
+    // block tables of at most one tile of compressed rows per sequence):
+    // when every live row's window and compressed lists fit one tile each
+    // (at most N compressed rows: longest sequence / RATIO <= N),
+    // the launch runs as one partition per row and those rows take one
+    // softmax over both kinds, as the reference device's one-split C128
+    // plans (c128.cpp:79-105, attention_impl.h:94-100) and its short C4 task
+    // batches (c4.cpp:35-58, task_batch.h) do.  Work items of the other
+    // partitions have nothing to do.  A launch with a separate merge keeps
+    // its plan; c8_attention.device_splits mirrors the rule.
+    bool joint_launch = false;
+    if (JOINT && !DEBUG && !SLOTS && resid && (fused || S == 1) && live_rows > 0 &&
         longest_live() / RATIO <= N) {
         if (part != 0) return;
         S = 1;
+        joint_launch = true;
     } else if (fused && live_rows < rows_cap) {
         const int32_t pad = live_rows + (int32_t)item;
         if (pad < rows_cap) {   // zero-fill padding row `pad` (attention_impl.h:443-460)
@@ -697,6 +705,21 @@ c8_attention(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base
     }
     m.t0 = (m.ori_count + N - 1) / N;
     m.total = m.t0 + (m.list_len + N - 1) / N;
+    // Joint sparse row (C4, reference.py:246-267 with joint_sparse; JOINT
+    // instantiations only): in a launch of the joint plan (every live row's
+    // compressed rows fit one tile: count <= N) a row's compressed list is
+    // dense: every row below
+    // count that some valid top-k entry names, once, in row order, with
+    // log(multiplicity) added to its logits (built with the row codes,
+    // below).  reference.py switches every C4 row of such a plan to the
+    // dense list, so a launch with a longer row has no joint C4 rows (the
+    // reference device decides per launch too, c4.cpp:35-58).  A joint C4
+    // row is two tiles even when it lists no compressed row (reference.py:257
+    // takes the joint route then too): its compressed tile is then all
+    // masked.  The joint route rounds the PV dequantization differently from
+    // the tiled one, so the row keeps it.
+    const bool joint4 = RATIO == 4 && joint_launch && m.count <= N;
+    if (joint4 && m.position >= 0) m.total = 2;
     const int my_tiles = m.total > part ? (m.total - part + S - 1) / S : 0;   // tiles part, part + S, ...
     // A live row's window list holds at least its own position, so it has a
     // tile, unless its request lists more query tokens than its sequence
@@ -713,17 +736,19 @@ c8_attention(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base
     // numbers equal the fold over all S partitions bit for bit.
     const int folded = S < m.total ? S : m.total;    // partitions that own tiles (>= 1)
     if (part >= folded) return;
-    // Joint row (reference.py:254-267 with joint_dense; the reference
-    // device's two-kind pipeline, attention_impl.h:94-100): a C128 row run as
-    // one partition whose window and compressed lists each fit one tile
-    // takes one softmax over both kinds (joint_quantized_row,
-    // reference.py:175-207) instead of two online tiles.  The window of such
-    // a row is full (its position is at least 127), so its valid keys fill
-    // tile 0 and the first list_len keys of tile 1, the order in which the
-    // reference concatenates them.  Explicit original slots, more than eight
-    // heads (no residual codes) and the debug entry keep the tiled plan.
-    const bool joint = RATIO == 128 && !DEBUG && !SLOTS && resid && S == 1 && m.t0 == 1 && m.list_len >= 1 &&
-                       m.list_len <= N;
+    // Joint row (reference.py:254-267 with joint_dense for C128, joint_sparse
+    // for C4; the reference device's two-kind pipeline, attention_impl.h:
+    // 94-100, and C4 task batches): a row run as one partition whose window
+    // and compressed lists each fit one tile takes one softmax over both
+    // kinds (joint_quantized_row, reference.py:175-207) instead of two
+    // online tiles.  Tile 0 holds the window's keys in order, tile 1 the
+    // compressed list's, the order in which the reference concatenates
+    // them; the weight sum is one pairwise tree per kind, added in kind
+    // order.  Explicit original slots, more than eight heads (no residual
+    // codes) and the debug entry keep the tiled plan.
+    const bool joint = RATIO == 128 ? !DEBUG && !SLOTS && resid && S == 1 && m.t0 == 1 && m.list_len >= 1 &&
+                                          m.list_len <= N
+                                    : joint4 && m.total == 2;
 
     // ---- per-lane softmax state for heads 2g and 2g+1 ----
     float mx[2] = {sink0, sink1}, den[2], num[2][4];
@@ -848,7 +873,10 @@ c8_attention(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base
     // tile's worth of queued copies.
     constexpr int DMA_STEP = DMA_PER_TILE / 4;
 
-    for (int first = 0; first < my_tiles; first += CODE_TILES) {
+    // A C4 row without explicit slots has one chunk of codes: saying so lets
+    // the compiler end the live ranges of its selection values there.
+    constexpr bool ONE_CHUNK = RATIO == 4 && !SLOTS;
+    for (int first = 0; first < my_tiles && (!ONE_CHUNK || first == 0); first += CODE_TILES) {
         const int ntiles = my_tiles - first < CODE_TILES ? my_tiles - first : CODE_TILES;
         // ---- row codes of partition tiles [first, first + ntiles) ----
         for (int i = tid; i < ntiles * N; i += THREADS) {
@@ -898,7 +926,7 @@ c8_attention(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base
             }
         }
         int cslot[2] = {-1, -1};
-        if (RATIO == 4) {
+        if (RATIO == 4 && !joint) {       // joint rows take the dense list (below)
 #pragma unroll
             for (int e = 0; e < 2; ++e) {
                 if (ipos[e] < 0 || ix[e] < 0) continue;
@@ -910,6 +938,7 @@ c8_attention(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base
             }
         }
         if (first == 0) *reinterpret_cast<f32x2 *>(&s.scale[tid >> 8][(tid & 255) * 2]) = scale_pair;
+        if (RATIO == 4 && joint && tid < N) s.mult[tid] = 0;
         lds_barrier();                    // the -1 fill is complete before the writes below
 #pragma unroll
         for (int e = 0; e < PER; ++e) {
@@ -938,6 +967,35 @@ c8_attention(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base
                     s.code[cslot[e]] = cpage_raw[e] * BLOCK_ROWS + ix[e] % BLOCK_ROWS;
                     s.addr[cslot[e]] = p.cmp + (uint64_t)cpage_raw[e] * p.cmpStride + (uint64_t)((ix[e] % BLOCK_ROWS) * D);
                 }
+            if (joint) {
+                // Tile 1 = the dense compressed list (reference.py:246-249):
+                // each row's multiplicity among the valid entries, then the
+                // listed rows (multiplicity > 0) in row order.  The owner of
+                // an entry writes its row's code at the row's list place
+                // (entries naming one row write the same code), from the
+                // table entry it read for the tiled plan; thread r writes
+                // row r's bias.
+#pragma unroll
+                for (int e = 0; e < 2; ++e)
+                    if (ix[e] >= 0 && ix[e] < m.count) atomicAdd(&s.mult[ix[e]], 1);
+                lds_barrier();
+                const int times = tid < N ? s.mult[tid] : 0;
+                const uint64_t listed = __ballot(times > 0);
+                if (lane == 0 && wave < 2) s.listed[wave] = listed;
+                lds_barrier();
+                const uint64_t lo = s.listed[0], hi = s.listed[1];
+                auto place = [&](int r) {   // listed rows below r
+                    return r < 64 ? __popcll(lo & ((1ull << r) - 1)) : __popcll(lo) + __popcll(hi & ((1ull << (r - 64)) - 1));
+                };
+                if (times > 0) s.bias[place(tid)] = (float)log((double)times);   // exact: see the oracle's log_count
+#pragma unroll
+                for (int e = 0; e < 2; ++e)
+                    if (ix[e] >= 0 && ix[e] < m.count && cpage_raw[e] >= 0) {
+                        const int j = N + place(ix[e]);
+                        s.code[j] = cpage_raw[e] * BLOCK_ROWS + ix[e] % BLOCK_ROWS;
+                        s.addr[j] = p.cmp + (uint64_t)cpage_raw[e] * p.cmpStride + (uint64_t)((ix[e] % BLOCK_ROWS) * D);
+                    }
+            }
         }
         lds_barrier();                    // codes visible
 
@@ -990,7 +1048,8 @@ c8_attention(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base
                 for (int hh = 0; hh < 2; ++hh) {
                     float dots = (float)sacc[kind][2 * hh];
                     dots = dots + (float)sacc[kind][2 * hh + 1] * (float)(1.0 / 127.0);
-                    const float l = dots * s.asc[kind][2 * gx + hh];
+                    float l = dots * s.asc[kind][2 * gx + hh];
+                    if (RATIO == 4 && kind == 1) l = l + s.bias[key];   // reference.py:189-190, 261
                     lg[kind][hh] = valid ? l : -1e30f;
                 }
             }
@@ -1037,10 +1096,9 @@ c8_attention(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base
                 }
             }
             lds_barrier();
-            // denominator = exp(sink - maximum) + the pairwise sum of the
-            // concatenated weights: the 256-leaf tree is the window tile's
-            // 128-leaf tree plus the compressed tile's (zero leaves past the
-            // list change nothing).
+            // denominator = exp(sink - maximum) + (window tile's pairwise
+            // tree + compressed tile's); zero leaves past a kind's keys
+            // change neither tree.
 #pragma unroll
             for (int hh = 0; hh < 2; ++hh) {
                 const int h = 2 * gx + hh;
@@ -1052,13 +1110,14 @@ c8_attention(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base
                 const float t1 = ((a1.x + a1.y) + (a1.z + a1.w)) + ((b1.x + b1.y) + (b1.z + b1.w));
                 den[hh] = factor[hh] + (t0 + t1);
             }
-            // PV per kind, then output = sum over kinds of dot * (scale / 127)
-            // in kind order (reference.py:199-206).
-            v4i vacc[2][4];
+            // PV per kind, each added to the output as it completes:
+            // output = sum over kinds of dot * (scale / 127) in kind order
+            // (reference.py:199-206).
 #pragma unroll
             for (int kind = 0; kind < 2; ++kind) {
+                v4i vacc[4];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) vacc[kind][j] = v4i{0, 0, 0, 0};
+                for (int j = 0; j < 4; ++j) vacc[j] = v4i{0, 0, 0, 0};
                 const lds_i8 *vbase = (const lds_i8 *)(s.tile[kind]);
 #pragma unroll
                 for (int kb = 0; kb < 2; ++kb) {
@@ -1077,26 +1136,22 @@ c8_attention(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
                         const v4i vb = {b0[j].x, b0[j].y, b1[j].x, b1[j].y};
-                        vacc[kind][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(pa, vb, vacc[kind][j], 0, 0, 0);
+                        vacc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(pa, vb, vacc[j], 0, 0, 0);
                     }
                 }
-            }
 #pragma unroll
-            for (int hh = 0; hh < 2; ++hh) {
+                for (int hh = 0; hh < 2; ++hh) {
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    float acc = 0.0f;
-#pragma unroll
-                    for (int kind = 0; kind < 2; ++kind) {
-                        float dots = (float)vacc[kind][j][2 * hh];
-                        dots = dots + (float)vacc[kind][j][2 * hh + 1] * (float)(1.0 / 127.0);
+                    for (int j = 0; j < 4; ++j) {
+                        float dots = (float)vacc[j][2 * hh];
+                        dots = dots + (float)vacc[j][2 * hh + 1] * (float)(1.0 / 127.0);
                         const float sc = s.scale[kind][c0 + 16 * j + nx] * (float)(1.0 / 127.0);
-                        acc = acc + dots * sc;
+                        num[hh][j] = (kind ? num[hh][j] : 0.0f) + dots * sc;   // acc starts at 0
                     }
-                    num[hh][j] = acc;
                 }
-                mx[hh] = mnew[hh];
             }
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) mx[hh] = mnew[hh];
         } else
         for (int i = 0; i < ntiles; ++i) {
             const int k = part + S * (first + i);
@@ -1417,13 +1472,25 @@ void launch_variant(hipStream_t stream, const SharedKVArgs *a, const SharedKVDeb
     // policy; window-only (ratio 1) launches keep the default.
     const uint32_t per_slot = a->ratio == 4 ? STREAM_TOKENS_C4 : a->ratio == 128 ? STREAM_TOKENS_C128 : 0;
     const bool streamed = !DEBUG && (uint64_t)a->tokens <= (uint64_t)per_slot * a->batch;
-    auto kernel = slots ? &c8_attention<1, DEBUG, true, ANYH, false> : &c8_attention<1, DEBUG, false, ANYH, false>;
-    if (a->ratio == 4)
-        kernel = slots ? (streamed ? &c8_attention<4, DEBUG, true, ANYH, !DEBUG> : &c8_attention<4, DEBUG, true, ANYH, false>)
-                       : (streamed ? &c8_attention<4, DEBUG, false, ANYH, !DEBUG> : &c8_attention<4, DEBUG, false, ANYH, false>);
+    // Joint rows: C128 kernels always carry them; C4 kernels only when the
+    // launch's compressed block table names at most one tile of rows per
+    // sequence (C4 joint rows cost the tiled C4 path about 3 % where they
+    // are compiled in, so only such launches get them).
+    const bool joint4 = !DEBUG && !slots && a->heads <= HEADS && (uint64_t)a->cmpTableWidth * BLOCK_ROWS <= (uint64_t)N;
+    auto kernel = slots ? &c8_attention<1, DEBUG, true, ANYH, false, false> : &c8_attention<1, DEBUG, false, ANYH, false, false>;
+    if (a->ratio == 4 && joint4)
+        kernel = streamed ? &c8_attention<4, DEBUG, false, ANYH, !DEBUG, !DEBUG>
+                          : &c8_attention<4, DEBUG, false, ANYH, false, !DEBUG>;
+    else if (a->ratio == 4)
+        kernel = slots ? (streamed ? &c8_attention<4, DEBUG, true, ANYH, !DEBUG, false>
+                                   : &c8_attention<4, DEBUG, true, ANYH, false, false>)
+                       : (streamed ? &c8_attention<4, DEBUG, false, ANYH, !DEBUG, false>
+                                   : &c8_attention<4, DEBUG, false, ANYH, false, false>);
     else if (a->ratio == 128)
-        kernel = slots ? (streamed ? &c8_attention<128, DEBUG, true, ANYH, !DEBUG> : &c8_attention<128, DEBUG, true, ANYH, false>)
-                       : (streamed ? &c8_attention<128, DEBUG, false, ANYH, !DEBUG> : &c8_attention<128, DEBUG, false, ANYH, false>);
+        kernel = slots ? (streamed ? &c8_attention<128, DEBUG, true, ANYH, !DEBUG, true>
+                                   : &c8_attention<128, DEBUG, true, ANYH, false, true>)
+                       : (streamed ? &c8_attention<128, DEBUG, false, ANYH, !DEBUG, true>
+                                   : &c8_attention<128, DEBUG, false, ANYH, false, true>);
     // The leading scalar arguments are the ones the first loads need; the
     // build preloads them into SGPRs (-amdgpu-kernarg-preload-count), so
     // those loads do not wait for a read of the argument block.

@@ -190,7 +190,8 @@ class PreparedAttention:
         seq_lens = c.seq_lens.cpu().tolist() if seq_lens is None else seq_lens
         return c8_attention.device_splits(self.splits, self.args.tokens, self.args.heads, self.args.ratio,
                                           self.args.topk, cu_q, seq_lens, self.args.oriTopk,
-                                          fused=merge_mode == 0)
+                                          fused=merge_mode == 0,
+                                          cmp_rows=self.args.cmpTableWidth * c8_attention.BLOCK)
 
     def run(self):
         """Launch on the current stream of the case's device; returns .out."""

@@ -132,7 +132,7 @@ def keyless_tokens(cu_q, seq_lens, tokens):
     return keyless
 
 
-def device_splits(splits, tokens, heads, ratio, topk, cu_q, seq_lens, ori_topk=0, fused=True):
+def device_splits(splits, tokens, heads, ratio, topk, cu_q, seq_lens, ori_topk=0, fused=True, cmp_rows=None):
     """The KV partitions the kernel runs a launch with, from its live metadata.
 
     A launch planned for `tokens` query tokens (graph capacity) at `splits`
@@ -146,16 +146,14 @@ def device_splits(splits, tokens, heads, ratio, topk, cu_q, seq_lens, ori_topk=0
     count (tile k folds into partition k % count), so checkers use it in
     place of `splits`.
 
-    C128 launches of the joint plan (joint_dense_plan) whose live rows all
-    fit one window tile and one compressed tile (longest live sequence //
-    128 <= 128) run as one partition per row instead, fused or not when
-    `splits` is 1, and only fused otherwise.
+    Joint-plan launches (joint_launch; `cmp_rows` = the compressed block
+    table's rows per sequence, width x 32) run as one partition per row
+    instead.
     """
     live_tokens, longest = live_shape(cu_q, seq_lens, tokens)
     groups = head_groups(heads)
     live_rows, rows = live_tokens * groups, tokens * groups
-    if (joint_dense_plan(ratio, heads, ori_topk > 0) and (fused or splits == 1) and live_rows > 0
-            and longest // 128 <= TILE):
+    if joint_launch(splits, tokens, heads, ratio, cu_q, seq_lens, ori_topk, fused, cmp_rows):
         return 1
     if not fused or splits <= 1:
         return splits
@@ -169,15 +167,38 @@ def device_splits(splits, tokens, heads, ratio, topk, cu_q, seq_lens, ori_topk=0
     return max(splits, min(plan_splits(live_rows, tiles), rows * splits // live_rows))
 
 
-def joint_dense_plan(ratio, heads, explicit_slots):
-    """Whether a launch's plan takes joint C128 rows (reference.py:254-267,
-    joint_dense; the reference device's two-kind pipeline for C128 at one
-    partition, attention_impl.h:94-100).  When it does, every row of a
+def joint_launch(splits, tokens, heads, ratio, cu_q, seq_lens, ori_topk=0, fused=True, cmp_rows=None):
+    """Whether the kernel runs a launch as a joint-plan launch: joint_plan
+    holds, every live row fits one window tile and one compressed tile
+    (longest live sequence // ratio <= 128), and the launch is fused or of
+    one partition; for C4 also the compressed block table names at most 128
+    rows per sequence (`cmp_rows` = table width x 32; the library compiles
+    C4 joint rows only into the kernels it launches for such tables, since
+    they slow the tiled C4 path elsewhere).  Such a launch runs one
+    partition per row.  Its C128 rows with compressed rows, and all its C4
+    rows, are joint rows; C4 launches that are not joint-plan launches have
+    none (reference.py:246 switches every C4 row of a joint_sparse plan to
+    the dense multiplicity list)."""
+    if ratio == 4 and (cmp_rows is None or cmp_rows > TILE):
+        return False
+    live_tokens, longest = live_shape(cu_q, seq_lens, tokens)
+    return (joint_plan(ratio, heads, ori_topk > 0) and (fused or splits == 1) and live_tokens > 0
+            and longest // ratio <= TILE)
+
+
+def joint_plan(ratio, heads, explicit_slots):
+    """Whether a launch's plan takes joint rows (reference.py:254-267):
+    joint_dense for C128 (the reference device's two-kind pipeline at one
+    partition, attention_impl.h:94-100) and joint_sparse for C4 (its short
+    C4 task batches, c4.cpp:35-58).  When it does, every row of a
     one-partition launch whose window and compressed lists each fit one
     128-key tile runs one softmax over both kinds; other rows, and launches
-    of more partitions, are tiled as usual.  Residual codes are required
-    (at most eight heads), and explicit original slots keep the tiled plan."""
-    return ratio == 128 and heads <= HEADS and not explicit_slots
+    of more partitions, are tiled as usual.  C4 rows are joint only in a
+    joint-plan launch (joint_launch), where each takes its compressed list
+    densely with log(multiplicity) biases.
+    Residual codes are required (at most eight heads), and explicit
+    original slots keep the tiled plan."""
+    return ratio in (4, 128) and heads <= HEADS and not explicit_slots
 
 
 def supported(entry):

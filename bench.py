@@ -154,7 +154,7 @@ def host_cores():
     return max(1, min(share, affinity))
 
 
-def cpu_baseline(dc, layers, splits, seconds):
+def cpu_baseline(dc, layers, splits, seconds, cmp_rows):
     """Time the C restatement on whole launches of the same workload until
     about `seconds` of wall time have passed (bounded sample), on every host
     core of the job's share and then on one thread (half the time)."""
@@ -162,14 +162,17 @@ def cpu_baseline(dc, layers, splits, seconds):
     from npu_sparse_attn_sharedkv_int8 import c8_attention
     from tests import workloads
     hosts = [workloads.oracle_case(dc.host(layer)) for layer in range(min(layers, 2))]
-    joint = c8_attention.joint_dense_plan(dc.meta["ratio"], dc.heads, False)
+    m = dc.meta
+    joint_dense = c8_attention.joint_plan(m["ratio"], dc.heads, False) and m["ratio"] == 128
+    joint_sparse = m["ratio"] == 4 and splits == 1 and c8_attention.joint_launch(
+        splits, int(m["cu_q"][-1]), dc.heads, 4, m["cu_q"], m["seq_lens"], cmp_rows=cmp_rows)
 
     def timed(threads, budget):
         queries = launches = 0
         start = time.perf_counter()
         while time.perf_counter() - start < budget:
             ora.tiled_attention(hosts[launches % len(hosts)], tile=128, splits=splits, return_lse=False,
-                                joint_dense=joint, threads=threads)
+                                joint_dense=joint_dense, joint_sparse=joint_sparse, threads=threads)
             queries += int(dc.meta["cu_q"][-1])
             launches += 1
         elapsed = time.perf_counter() - start
@@ -311,8 +314,10 @@ def main():
     from npu_sparse_attn_sharedkv_int8 import c8_attention
     # The partitions the kernel runs: the device re-plans joint C128 launches
     # (and padded ones, below) from the live metadata.
+    cmp_rows = ops[0].args.cmpTableWidth * c8_attention.BLOCK
     device_plan = c8_attention.device_splits(splits, int(dc.meta["cu_q"][-1]), args.heads, ratio, 1024,
-                                             dc.meta["cu_q"], dc.meta["seq_lens"], fused=args.merge == 0)
+                                             dc.meta["cu_q"], dc.meta["seq_lens"], fused=args.merge == 0,
+                                             cmp_rows=cmp_rows)
     live_queries = int(sum(queries))
     bytes_per_launch = [dc.algorithmic_bytes(l) for l in range(layers)]
 
@@ -357,7 +362,8 @@ def main():
         cu[live_seqs + 1:] = cu_full[live_seqs]
         lens = lens_full.copy()
         lens[live_seqs:] = 0
-        padded_plan = c8_attention.device_splits(splits, int(cu_full[-1]), args.heads, ratio, 1024, cu, lens)
+        padded_plan = c8_attention.device_splits(splits, int(cu_full[-1]), args.heads, ratio, 1024, cu, lens,
+                                                 cmp_rows=cmp_rows)
         dc.dev.cu_q.copy_(torch.from_numpy(cu))
         dc.dev.seq_lens.copy_(torch.from_numpy(lens))
         torch.cuda.synchronize()
@@ -398,7 +404,9 @@ def main():
                    "dim": 512, "ratio": ratio, "topk": 1024 if ratio == 4 else 0, "window": 128,
                    "page_stride": stride, "layers_rotated": layers, "tile": 128, "splits": splits,
                    "device_splits": device_plan,
-                   "joint_c128_rows": bool(device_plan == 1 and c8_attention.joint_dense_plan(ratio, args.heads, False)),
+                   "joint_rows": bool(device_plan == 1 and c8_attention.joint_launch(
+                       splits, int(dc.meta["cu_q"][-1]), args.heads, ratio, dc.meta["cu_q"], dc.meta["seq_lens"],
+                       cmp_rows=cmp_rows)),
                    "lse": False, "merge": "fused" if args.merge == 0 else "separate launch",
                    "timing": "one HIP graph replay of K launches, HIP events on its stream"},
         "latency_us_per_layer": ms_per_step * 1e3,
@@ -414,7 +422,7 @@ def main():
     copy_calibration(args.copy_calibration, torch)
     if not args.no_cpu:
         log(f"[bench] CPU baseline ({args.cpu_seconds:.0f} s sample)")
-        record["cpu_baseline"] = cpu_baseline(dc, layers, device_plan, args.cpu_seconds)
+        record["cpu_baseline"] = cpu_baseline(dc, layers, device_plan, args.cpu_seconds, cmp_rows)
     print(json.dumps(record), flush=True)
 
 

@@ -13,7 +13,9 @@
  *   - exp is sko_expf (Cody-Waite + Taylor), identical to the HIP kernels';
  *     torch.exp differs from it by at most an ulp on rare inputs;
  *   - the per-tile sum of softmax weights (reference.py:306 weights.sum(-1))
- *     is a pairwise tree over the tile's positions; torch's order is its own.
+ *     is a pairwise tree over the tile's positions, and a joint row's sum
+ *     (reference.py:196) one such tree per kind, added in kind order;
+ *     torch's order is its own.
  * Both are pinned against vectors generated from reference.py (tests/golden).
  */
 #include "sharedkv_oracle.h"
@@ -77,6 +79,17 @@ float sko_bf16_to_f32(uint16_t x)
     float f;
     memcpy(&f, &u, 4);
     return f;
+}
+
+/* log of a multiplicity count (reference.py:249, 261 cmp_multiplicity.log()),
+ * evaluated in double and rounded once to FP32.  For every count 1..1024
+ * the exact ln(k) lies at least 4e-4 FP32 ulp from an FP32 rounding midpoint,
+ * so this is the correctly rounded value, equal to glibc logf and torch.log
+ * at every count, and any double log accurate to a few ulps gives the same
+ * float (the HIP kernel uses the device library's). */
+static float log_count(float count)
+{
+    return (float)log((double)count);
 }
 
 /* Pairwise sum: level by level, element 2i plus element 2i+1; the input is
@@ -248,13 +261,21 @@ void sko_joint_row(const uint16_t *q, int heads, const int8_t *const *rows, cons
         }
         offset += counts[k];
     }
-    int32_t padded = pow2_at_least(total ? total : 1);
     float *w = (float *)malloc(sizeof(float) * (size_t)(total ? total : 1));
     for (int h = 0; h < heads; ++h) {
         float m = sink[h];
         for (int32_t j = 0; j < total; ++j) m = scores[h * total + j] > m ? scores[h * total + j] : m;
         for (int32_t j = 0; j < total; ++j) w[j] = sko_expf(scores[h * total + j] - m);
-        float den = sko_expf(sink[h] - m) + sko_tree_sum(w, total, padded);
+        /* weights.sum(-1) over the concatenated kinds (reference.py:196): a
+         * pairwise tree per kind, the kinds' sums added in order. */
+        float wsum = 0.0f;
+        offset = 0;
+        for (int k = 0; k < kinds; ++k) {
+            const float part = sko_tree_sum(w + offset, counts[k], pow2_at_least(counts[k] ? counts[k] : 1));
+            wsum = k ? wsum + part : part;
+            offset += counts[k];
+        }
+        float den = sko_expf(sink[h] - m) + wsum;
         float acc[D];
         for (int c = 0; c < D; ++c) acc[c] = 0.0f;
         offset = 0;
@@ -403,7 +424,7 @@ static void attend_token(const sko_case *c, const sko_plan *pl, int32_t b, int32
             bias = malloc(sizeof(float) * (counts[1] ? counts[1] : 1));
             int32_t m = 0;
             for (int32_t j = 0; j < lists[1].length; ++j)
-                if (lists[1].valid[j]) bias[m++] = logf(lists[1].multiplicity[j]);
+                if (lists[1].valid[j]) bias[m++] = log_count(lists[1].multiplicity[j]);
         }
         const float *scales[2] = {c->ori_scale, c->cmp_scale};
         sko_joint_row(c->q + (int64_t)t * H * D, H, rows, counts, scales, 2, bias, c->sink,
@@ -486,7 +507,7 @@ static void attend_token(const sko_case *c, const sko_plan *pl, int32_t b, int32
                         float lg = dots * asc[h];
                         if (k == 1 && L->multiplicity) {
                             float m = L->multiplicity[L->index[start + j]];
-                            lg = lg + logf(m < 1.0f ? 1.0f : m);
+                            lg = lg + log_count(m < 1.0f ? 1.0f : m);
                         }
                         if (!L->valid[start + j]) lg = MASKED;
                         logit[h * N + j] = lg;

@@ -115,26 +115,53 @@ def effective_splits(case, splits, merge_mode=0):
     """KV partitions the kernel runs for a launch of `case` (host numpy
     metadata) planned at `splits`, with the library in `merge_mode`
     (c8_attention.device_splits: the device's re-plan of padded launches and
-    joint C128 launches)."""
+    joint-row launches)."""
     from npu_sparse_attn_sharedkv_int8 import c8_attention
     slots = case.get("ori_indices")
     return c8_attention.device_splits(
         splits, case["q"].shape[0], case["q"].shape[1], case["ratio"],
         case["cmp_indices"].shape[-1] if case["ratio"] == 4 else 0, case["cu_q"], case["seq_lens"],
-        slots.shape[-1] if slots is not None else 0, fused=merge_mode == 0)
+        slots.shape[-1] if slots is not None else 0, fused=merge_mode == 0, cmp_rows=cmp_rows(case))
 
 
-def run_oracle(case, splits, debug=False, cmp_capacity=None, tile_capacity=None, threads=None):
-    """The CPU checker with this build's plan: 128-key tiles, `splits`
-    partitions, and joint C128 rows where the kernel takes them
-    (c8_attention.joint_dense_plan; the debug entry runs the tiled plan)."""
-    import oracle.oracle as ora
+def cmp_rows(case):
+    """Rows per sequence the case's compressed block table names (width x 32),
+    or None without a compressed cache."""
+    return case["cmp"].table.shape[1] * 32 if case.get("cmp") is not None else None
+
+
+def joint_flags(case, splits, merge_mode=0):
+    """(joint_dense, joint_sparse) of the checker for a launch of `case`
+    planned at `splits`: C128 rows are joint per row at one partition
+    (c8_attention.joint_plan), C4 rows only in a joint-plan launch
+    (c8_attention.joint_launch: short live rows and a compressed block
+    table of at most 128 rows per sequence), judged on the whole launch's
+    metadata."""
     from npu_sparse_attn_sharedkv_int8 import c8_attention
-    joint = not debug and c8_attention.joint_dense_plan(case["ratio"], case["q"].shape[1],
-                                                        case.get("ori_indices") is not None)
+    slots = case.get("ori_indices")
+    heads, ratio = case["q"].shape[1], case["ratio"]
+    dense = ratio == 128 and c8_attention.joint_plan(ratio, heads, slots is not None)
+    sparse = ratio == 4 and c8_attention.joint_launch(
+        splits, case["q"].shape[0], heads, ratio, case["cu_q"], case["seq_lens"],
+        slots.shape[-1] if slots is not None else 0, fused=merge_mode == 0, cmp_rows=cmp_rows(case))
+    return bool(dense), bool(sparse)
+
+
+def run_oracle(case, splits, debug=False, cmp_capacity=None, tile_capacity=None, threads=None, joint=None):
+    """The CPU checker with this build's plan: 128-key tiles, `splits`
+    partitions (the ones the kernel runs), and joint rows where the kernel
+    takes them: `joint` = joint_flags of the launch (default: those of
+    `case` as its own launch at `splits`); the debug entry runs the tiled
+    plan."""
+    import oracle.oracle as ora
+    if joint is None:   # a joint-plan launch runs one partition
+        dense, sparse = joint_flags(case, splits)
+        sparse = sparse and splits == 1
+    else:
+        dense, sparse = joint
     return ora.tiled_attention(workloads.oracle_case(case), tile=128, splits=splits, return_lse=True,
-                               joint_dense=joint, debug=debug, cmp_capacity=cmp_capacity,
-                               tile_capacity=tile_capacity, threads=threads)
+                               joint_dense=dense and not debug, joint_sparse=sparse and not debug, debug=debug,
+                               cmp_capacity=cmp_capacity, tile_capacity=tile_capacity, threads=threads)
 
 
 def query_subcase(case, rows):

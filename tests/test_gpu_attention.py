@@ -13,7 +13,8 @@ import numpy as np
 import pytest
 
 from tests import workloads
-from tests.device_cases import (effective_splits, query_subcase, run_hip, run_hip_debug, run_oracle, to_device, bits_of,
+from tests.device_cases import (effective_splits, joint_flags, query_subcase, run_hip, run_hip_debug, run_oracle,
+                                to_device, bits_of,
                                 torch_bf16,
                                 default_cmp_capacity)
 
@@ -47,8 +48,9 @@ def compare(case, out, lse, splits, rows=None, tag="", merge_mode=0):
     """HIP output of a launch of `case` planned at `splits` (run with the
     library in `merge_mode`) against the checker on the partitions the
     kernel actually ran (effective_splits)."""
+    joint = joint_flags(case, splits, merge_mode)
     splits = effective_splits(case, splits, merge_mode)
-    ref, ref_lse, _ = run_oracle(case if rows is None else query_subcase(case, rows), splits)
+    ref, ref_lse, _ = run_oracle(case if rows is None else query_subcase(case, rows), splits, joint=joint)
     got = out if rows is None else out[rows]
     got_lse = lse if rows is None else lse[rows]
     live = ref.shape[0] if rows is not None else int(case["cu_q"][-1])
@@ -235,6 +237,41 @@ def test_joint_c128_rows(heads):
     assert np.array_equal(out3, ref3)
 
 
+@pytest.mark.parametrize("mode,heads", [("dups", 8), ("mixed", 8), ("uniform", 8), ("one_key_duplicates", 8),
+                                        ("extended_duplicates", 4), ("holes", 8), ("mixed", 16)])
+def test_joint_c4_rows(mode, heads):
+    """Short C4 rows (at most 128 compressed rows below the position) take
+    joint rows at one partition (reference.py:246-267, joint_sparse): the
+    compressed list is every row some valid top-k entry names, once, in row
+    order, with log(multiplicity) added to its logits, and one softmax spans
+    both kinds.  Bit-exact with the checker's joint plan and different from
+    the tiled plan (so the joint path is the one that ran).  The launch
+    mixes partial windows (positions below 127), rows with no compressed
+    row, and a request of three tokens.  Three planned partitions re-plan to
+    one (every live row fits).  One long row makes the launch tiled
+    throughout, its short rows on their top-k lists (reference.py:246
+    switches every C4 row of a joint_sparse plan to the dense list, so the
+    joint plan is per launch).  Above eight heads every row is tiled."""
+    import oracle.oracle as ora
+    queries, lengths = [1, 2, 1, 1, 3, 1], [300, 515, 100, 40, 200, 2]
+    case = workloads.make_case(71, 4, queries, lengths, heads=heads, index_mode=mode)
+    host = workloads.oracle_case(case)
+    say(f"[joint c4] {mode} heads {heads}")
+    tiled, _, _ = ora.tiled_attention(host, tile=128, splits=1, return_lse=True)
+    for splits in (1, 3):
+        out, lse, op = run_hip(case, splits=splits)
+        assert op.device_splits() == (1 if heads <= 8 else splits)
+        compare(case, out, lse, splits, tag=f"{mode} splits {splits}")
+        if heads <= 8 and mode != "uniform":
+            assert (out != tiled).any()
+    # A long row in the same launch: tiled rows at the launch's plan.
+    long_case = workloads.make_case(72, 4, queries + [1], lengths + [4096], heads=heads, index_mode=mode)
+    for splits in (1, 3):
+        out, lse, op = run_hip(long_case, splits=splits)
+        assert op.device_splits() == splits
+        compare(long_case, out, lse, splits, tag=f"{mode} with a long row, splits {splits}")
+
+
 @pytest.mark.parametrize("name", GOLDEN_NAMES)
 def test_against_reference_vectors(name):
     """HIP output vs reference.py's own tiled_quantized_reference output on
@@ -298,11 +335,12 @@ def test_against_reference_vectors(name):
             np.testing.assert_allclose(own_lse, z[f"lse_{i}"][:live], rtol=0, atol=2e-3,
                                        err_msg=f"{name} plan {i}")
         # Same-plan check where the stored plan is the HIP launch's plan at
-        # `splits`: 128-key tiles, ungrouped, and joint C128 rows exactly
-        # when the HIP plan takes them (one partition, at most eight heads,
-        # no explicit slots).
-        joint_here = c8_attention.joint_dense_plan(ratio, z["q"].shape[1], "ori_indices" in z.files)
-        if tile != 128 or js or dense or group != 1 or (splits == 1 and ratio == 128 and bool(jd) != joint_here):
+        # `splits`: 128-key tiles, ungrouped, and joint rows (C128
+        # joint_dense, C4 joint_sparse) exactly when the HIP plan takes them
+        # (one partition, at most eight heads, no explicit slots).
+        joint_here = splits == 1 and c8_attention.joint_plan(ratio, z["q"].shape[1], "ori_indices" in z.files)
+        stored_joint = bool(jd) if ratio == 128 else bool(js) if ratio == 4 else False
+        if tile != 128 or dense or group != 1 or stored_joint != joint_here:
             continue
         say(f"[reference vectors] {name} plan {i}: splits={splits}")
         got, got_lse = launch(splits)

@@ -172,11 +172,13 @@ def test_device_plan_of_padded_launches():
     assert plan(3, 6, 8, 4, 1024, [0, 0, 0], [0, 0]) == 3     # nothing live
 
 
-def test_device_plan_of_joint_c128_launches():
-    """C128 launches whose live rows all fit one window and one compressed
-    tile (longest live sequence // 128 <= 128) run one partition per row
-    with joint rows; not above eight heads, with explicit slots, or (for
-    more than one partition) with a separate merge launch."""
+def test_device_plan_of_joint_launches():
+    """C128 and C4 launches whose live rows all fit one window and one
+    compressed tile (longest live sequence // ratio <= 128; C4 also needs a
+    compressed block table of at most 128 rows per sequence) run one
+    partition per row with joint rows; not above eight heads, with explicit
+    slots, for window-only launches, or (for more than one partition) with a
+    separate merge launch."""
     plan = c8_attention.device_splits
     short = [0, 1, 2, 3, 4]
     assert plan(5, 4, 8, 128, 0, short, [4096] * 4) == 1
@@ -185,10 +187,20 @@ def test_device_plan_of_joint_c128_launches():
     assert plan(5, 4, 8, 128, 0, short, [16511] * 4) == 1 and plan(5, 4, 8, 128, 0, short, [16512] * 4) == 5
     assert plan(5, 4, 16, 128, 0, short, [4096] * 4) == 5                      # no residual codes
     assert plan(5, 4, 8, 128, 0, short, [4096] * 4, ori_topk=128) == 5         # explicit slots
-    assert plan(5, 4, 8, 4, 1024, short, [4096] * 4) == 5                      # C4 keeps its plan
+    # C4: also a compressed block table of at most 128 rows per sequence.
+    assert plan(5, 4, 8, 4, 1024, short, [4096] * 4, cmp_rows=1024) == 5      # long C4 rows keep the plan
+    assert plan(5, 4, 8, 4, 1024, short, [515] * 4, cmp_rows=128) == 1
+    assert plan(5, 4, 8, 4, 1024, short, [516] * 4, cmp_rows=160) == 5
+    assert plan(5, 4, 8, 4, 1024, short, [515] * 4, cmp_rows=160) == 5        # wide table: tiled kernel
+    assert plan(5, 4, 8, 4, 1024, short, [515] * 4) == 5                      # table unknown
+    assert plan(5, 4, 8, 4, 1024, short, [515] * 4, ori_topk=128, cmp_rows=128) == 5   # explicit slots
+    assert plan(5, 4, 8, 1, 0, short, [100] * 4) == 5                          # window only: no joint rows
     assert plan(3, 64, 8, 128, 0, list(range(9)) + [8] * 56, [4096] * 8 + [0] * 56) == 1   # padded
-    assert c8_attention.joint_dense_plan(128, 8, False) and c8_attention.joint_dense_plan(128, 4, False)
-    assert not c8_attention.joint_dense_plan(128, 9, False) and not c8_attention.joint_dense_plan(4, 8, False)
+    assert plan(3, 64, 8, 4, 1024, list(range(9)) + [8] * 56, [300] * 8 + [0] * 56, cmp_rows=96) == 1
+    joint = c8_attention.joint_plan
+    assert joint(128, 8, False) and joint(128, 4, False) and joint(4, 8, False) and joint(4, 1, False)
+    assert not joint(128, 9, False) and not joint(4, 16, False) and not joint(1, 8, False)
+    assert not joint(4, 8, True) and not joint(128, 8, True)
 
 
 def test_device_plan_constants_match_the_host_rule():

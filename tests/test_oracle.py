@@ -90,6 +90,31 @@ def test_plan_families_are_covered():
     assert any(p[5] for p in golden_plans(dense_dups))
 
 
+def test_count_log_is_correctly_rounded():
+    """The multiplicity bias log(count) (reference.py:249, 261; the checker's
+    log_count and the kernel's, both the FP32 rounding of a double log):
+    for every count 1..1024 the exact ln(k) (50 digits) lies at least 4e-4
+    FP32 ulp from an FP32 rounding midpoint, so the double log rounds to the
+    correctly rounded value, which torch.log gives too."""
+    from decimal import Decimal, getcontext
+    import torch
+    getcontext().prec = 50
+    ours = np.array([np.float32(math.log(k)) for k in range(1, 1025)])
+    theirs = torch.log(torch.arange(1, 1025, dtype=torch.float32)).numpy()
+    assert np.array_equal(ours, theirs)
+    for k in range(2, 1025):
+        exact = Decimal(k).ln()
+        f = ours[k - 1]
+        up, down = np.nextafter(f, np.float32(np.inf)), np.nextafter(f, np.float32(-np.inf))
+        ulp = Decimal(float(up)) - Decimal(float(f))
+        # f is the nearest float, and ln(k) is far from both midpoints.
+        assert abs(exact - Decimal(float(f))) <= ulp / 2
+        for other in (up, down):
+            midpoint = (Decimal(float(f)) + Decimal(float(other))) / 2
+            assert abs(exact - midpoint) >= Decimal("4e-4") * ulp, k
+    assert ours[0] == 0.0
+
+
 def test_joint_plans_need_residual_codes():
     """reference.py:258 asserts residual quantization (at most eight heads)
     for joint rows; the checker refuses such a plan outright."""
