@@ -1,7 +1,8 @@
 """Seeded random launches against the CPU checker: mixed ratios, head counts,
-explicit original slots, C4 index modes, graph-capacity padding rows, KV
-partitions (1-8) and both merge placements, all bit-exact (BF16 outputs) with the
-checker on the launch's own plan and LSE within 2e-6."""
+explicit original slots, C4 index modes, short contexts (joint rows),
+graph-capacity padding rows, KV partitions (1-8) and both merge placements,
+all bit-exact (BF16 outputs) with the checker on the launch's own plan and LSE
+within 2e-6."""
 import os
 import sys
 
@@ -25,7 +26,9 @@ def random_case(seed):
     ratio = int(rng.choice([1, 4, 128]))
     batch = int(rng.integers(1, 6))
     queries = [int(q) for q in rng.integers(1, 5, batch)]
-    lengths = [int(max(q, rng.integers(1, 9000))) for q in queries]
+    # One launch in five is short-context (joint rows for C4 and C128).
+    longest = 516 if rng.random() < 0.2 else 9000
+    lengths = [int(max(q, rng.integers(1, longest))) for q in queries]
     heads = int(rng.choice([8, 8, 8, 4, 12, 16]))
     mode = str(rng.choice(["uniform", "holes", "dups", "mixed"] + list(workloads.EDGE_MODES)))
     slots = rng.random() < 0.25
@@ -54,7 +57,7 @@ def random_case(seed):
                 case[key] = np.concatenate([case[key], filler])
     return case, (None if splits is None else int(splits)), merge, dict(
         ratio=ratio, queries=queries, lengths=lengths, heads=heads, mode=mode, slots=slot_mode, topk=topk,
-        pad=pad)
+        pad=pad, joint=bool(ratio != 1 and max(lengths) // ratio <= 128 and heads <= 8 and not slot_mode))
 
 
 @pytest.mark.parametrize("seed", range(CASES))
