@@ -421,7 +421,7 @@ __device__ __forceinline__ void fold_row(const __amdgpu_buffer_rsrc_t states, in
 // written.  Above eight heads the Q and P residual codes are zero
 // (reference.py:221-222: residual quantization only for <= 8 heads), which
 // leaves every other operation as it is.  Without ANYH, heads == 8.
-template <int RATIO, bool DEBUG, bool SLOTS, bool ANYH, bool STREAM, bool JOINT>
+template <int RATIO, bool DEBUG, bool SLOTS, bool ANYH, bool STREAM, bool JOINT, bool PERSIST>
 __global__ void __launch_bounds__(THREADS, 1)   // one work-group per CU: the 128 KiB tile ring fills the LDS
 c8_attention(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, const uint64_t cmp_indices,
              const uint32_t batch_arg, const uint32_t topk_arg, const uint32_t heads_arg, const uint32_t splits,
@@ -429,7 +429,8 @@ c8_attention(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base
              const uint32_t fused)
 {
     __shared__ Shared s;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, n = lane & 15;
+    // (Non-const: a persistent work-group re-derives them for every row.)
+    int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, n = lane & 15;
 
     // XCD-aware order: consecutive work items (the partitions of one row,
     // then the next row) stay on one XCD and share its L2.
@@ -593,536 +594,707 @@ c8_attention(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base
             find_request(t, false);
         }
     }
-    // Every metadata load has landed: said explicitly (vmcnt(0)) so that the
-    // compiler's own wait tracking does not hold back the block-table reads
-    // issued next for these registers.
-    __builtin_amdgcn_s_waitcnt(0x0F70);
-    const int batch = uni(s.misc[1]);
-    uint16_t *out_row = reinterpret_cast<uint16_t *>(p.out) + ((int64_t)t * H + hbase) * D;
-    float *lse_row = p.lse ? reinterpret_cast<float *>(p.lse) + (int64_t)t * H + hbase : nullptr;
-    // A row without keys is zero-filled by partition 0: output and LSE, and
-    // with a separate merge launch its partition count (0: nothing to fold).
-    auto zero_row = [&]() {
-        if (part != 0) return;
-        if (!ANYH || tid < hlive * (D / 8)) reinterpret_cast<v4i *>(out_row)[tid] = v4i{0, 0, 0, 0};
-        if (lse_row && tid < hlive) lse_row[tid] = 0.0f;
-        if (S > 1 && !fused && tid == 0)
-            reinterpret_cast<float *>(p.partial)[(int64_t)qrow * S * HEADS * PART_FLOATS + FOLD_SLOT] = 0.0f;
-    };
-    if (t >= live_tokens || batch < 0) {
-        zero_row();   // graph padding rows (attention_impl.h:443-460)
-        return;
-    }
-    // Sinks and the scales of both kinds (kind = tid / 256, 2 channels per
-    // thread): their addresses come from the argument block, which is read
-    // while the metadata above is in flight, so they are requested only now;
-    // the scales go to LDS after the block-table reads have been issued.
-    const __attribute__((address_space(1))) float *sinks = gptr<float>(p.sinks);
-    const float sink0 = (!ANYH || 2 * g < hlive) ? sinks[hbase + 2 * g] : 0.0f;
-    const float sink1 = (!ANYH || 2 * g + 1 < hlive) ? sinks[hbase + 2 * g + 1] : 0.0f;
-    const f32x2 scale_pair = *gptr<f32x2>(((tid >> 8) && RATIO != 1 ? p.cmpScale : p.oriScale) +
-                                          (uint64_t)((tid & 255) * 2) * 4);
+    // One row (a work item: query row qrow, partition part) from its row
+    // request onwards.  PERSIST work-groups run it for rows qrow, qrow + G,
+    // ... in turn (one-partition launches with more rows than CUs), each next
+    // row's Q and indices loaded while the current row's first tile lands.
+    v4i qv_next = {0, 0, 0, 0};
+    int ix_next[2] = {-1, -1};
+    bool prefetched = false;          // a row that ends early loads nothing ahead
+    auto run_row = [&]() {
+        // Every metadata load has landed: said explicitly (vmcnt(0)) so that the
+        // compiler's own wait tracking does not hold back the block-table reads
+        // issued next for these registers.
+        __builtin_amdgcn_s_waitcnt(0x0F70);
+        const int batch = uni(s.misc[1]);
+        uint16_t *out_row = reinterpret_cast<uint16_t *>(p.out) + ((int64_t)t * H + hbase) * D;
+        float *lse_row = p.lse ? reinterpret_cast<float *>(p.lse) + (int64_t)t * H + hbase : nullptr;
+        // A row without keys is zero-filled by partition 0: output and LSE, and
+        // with a separate merge launch its partition count (0: nothing to fold).
+        auto zero_row = [&]() {
+            if (part != 0) return;
+            if (!ANYH || tid < hlive * (D / 8)) reinterpret_cast<v4i *>(out_row)[tid] = v4i{0, 0, 0, 0};
+            if (lse_row && tid < hlive) lse_row[tid] = 0.0f;
+            if (S > 1 && !fused && tid == 0)
+                reinterpret_cast<float *>(p.partial)[(int64_t)qrow * S * HEADS * PART_FLOATS + FOLD_SLOT] = 0.0f;
+        };
+        if (t >= live_tokens || batch < 0) {
+            zero_row();   // graph padding rows (attention_impl.h:443-460)
+            return;
+        }
+        // Sinks and the scales of both kinds (kind = tid / 256, 2 channels per
+        // thread): their addresses come from the argument block, which is read
+        // while the metadata above is in flight, so they are requested only now;
+        // the scales go to LDS after the block-table reads have been issued.
+        const __attribute__((address_space(1))) float *sinks = gptr<float>(p.sinks);
+        const float sink0 = (!ANYH || 2 * g < hlive) ? sinks[hbase + 2 * g] : 0.0f;
+        const float sink1 = (!ANYH || 2 * g + 1 < hlive) ? sinks[hbase + 2 * g + 1] : 0.0f;
+        const f32x2 scale_pair = *gptr<f32x2>(((tid >> 8) && RATIO != 1 ? p.cmpScale : p.oriScale) +
+                                              (uint64_t)((tid & 255) * 2) * 4);
 
-    // ---- selection (attention_impl.h:58-73, reference.py:228-253) ----
-    Row m;
-    m.batch = batch;
-    m.position = uni(s.misc[3]) - uni(s.misc[4]) + t;
-    m.first_ori = m.position + 1 > WINDOW ? m.position + 1 - WINDOW : 0;
-    m.ori_count = m.position + 1 - m.first_ori;
-    if (m.ori_count < 0) m.ori_count = 0;
-    if (SLOTS) {
-        m.first_ori = 0;
-        m.ori_count = (int)p.oriTopk;
-    }
-    m.count = RATIO == 1 ? 0 : (m.position + 1) / RATIO;
-    // Global-space views: flat loads would also hold the LDS counter that the
-    // fence-free barriers below wait on.
-    const __attribute__((address_space(1))) int32_t *otab = gptr<int32_t>(p.oriTable) + (int64_t)m.batch * p.oriTableWidth;
-    const __attribute__((address_space(1))) int32_t *ctab = gptr<int32_t>(p.cmpTable) + (int64_t)m.batch * p.cmpTableWidth;
-    // C4: every block-table read of the row (the window tile, held by
-    // partition 0, and the thread's two index entries) is issued here, so
-    // the compaction scan below runs while they are in flight.  A C4 row
-    // has at most 1 + MAX_LIST / N <= CODE_TILES tiles: one chunk of codes
-    // (explicit slots read theirs per chunk, below).
-    const __attribute__((address_space(1))) int32_t *oslots =
-        gptr<int32_t>(p.oriIndices) + (int64_t)t * p.oriTopk;
-    int wpage = -1, widx = -1, cpage_raw[2] = {-1, -1};
-    if (RATIO == 4) {
-        if (!SLOTS && part == 0 && tid < m.ori_count) {
-            const int idx = m.first_ori + tid;
-            if (idx / BLOCK_ROWS < (int)p.oriTableWidth) {
-                widx = idx;
-                wpage = otab[idx / BLOCK_ROWS];
-            }
+        // ---- selection (attention_impl.h:58-73, reference.py:228-253) ----
+        Row m;
+        m.batch = batch;
+        m.position = uni(s.misc[3]) - uni(s.misc[4]) + t;
+        m.first_ori = m.position + 1 > WINDOW ? m.position + 1 - WINDOW : 0;
+        m.ori_count = m.position + 1 - m.first_ori;
+        if (m.ori_count < 0) m.ori_count = 0;
+        if (SLOTS) {
+            m.first_ori = 0;
+            m.ori_count = (int)p.oriTopk;
         }
-#pragma unroll
-        for (int e = 0; e < 2; ++e)
-            if (ix[e] >= 0 && ix[e] < m.count && ix[e] / BLOCK_ROWS < (int)p.cmpTableWidth)
-                cpage_raw[e] = ctab[ix[e] / BLOCK_ROWS];
-    }
-    static_assert(1 + MAX_LIST / N <= CODE_TILES, "a C4 row's codes fit one chunk");
-    int ipos[2] = {-1, -1};   // list position of each owned C4 entry (-1: none)
-    if (RATIO == 4) {
-        const int topk = (int)p.topk;
-        const bool compact = m.count < topk && topk <= MAX_LIST;   // reference.py:250
-        bool ok[2];
-#pragma unroll
-        for (int i = 0; i < 2; ++i) ok[i] = ix[i] >= 0 && ix[i] < m.count;
-        if (compact) {
-            // Entry 2 tid + i goes to place (valid entries of lower lanes and
-            // waves) + (entry 0 of this lane, for i = 1): two ballots, counted
-            // below the lane with mbcnt.
-            const uint64_t v0 = __ballot(ok[0]), v1 = __ballot(ok[1]);
-            const int below = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(v0 >> 32),
-                                                             __builtin_amdgcn_mbcnt_lo((uint32_t)v0, 0u)) +
-                              (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(v1 >> 32),
-                                                             __builtin_amdgcn_mbcnt_lo((uint32_t)v1, 0u));
-            if (lane == 0) s.scan[wave] = __popcll(v0) + __popcll(v1);
-            lds_barrier();                    // no fence: the table reads stay in flight
-            int at = below, total = 0;
-#pragma unroll
-            for (int w = 0; w < WAVES; ++w) {
-                at += w < wave ? s.scan[w] : 0;
-                total += s.scan[w];
-            }
-#pragma unroll
-            for (int i = 0; i < 2; ++i)
-                if (ok[i]) ipos[i] = at++;
-            m.list_len = uni(total);
-        } else {
-#pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const int j = tid * 2 + i;
-                if (j < topk) ipos[i] = j;
-                if (!ok[i]) ix[i] = -1;        // hole: a masked column in place
-            }
-            m.list_len = topk;
-        }
-    } else if (RATIO == 128) {
-        m.list_len = m.count > 0 ? m.count : 0;
-    } else {
-        m.list_len = 0;   // window only
-    }
-    m.t0 = (m.ori_count + N - 1) / N;
-    m.total = m.t0 + (m.list_len + N - 1) / N;
-    // Joint sparse row (C4, reference.py:246-267 with joint_sparse; JOINT
-    // instantiations only): in a launch of the joint plan (every live row's
-    // compressed rows fit one tile: count <= N) a row's compressed list is
-    // dense: every row below
-    // count that some valid top-k entry names, once, in row order, with
-    // log(multiplicity) added to its logits (built with the row codes,
-    // below).  reference.py switches every C4 row of such a plan to the
-    // dense list, so a launch with a longer row has no joint C4 rows (the
-    // reference device decides per launch too, c4.cpp:35-58).  A joint C4
-    // row is two tiles even when it lists no compressed row (reference.py:257
-    // takes the joint route then too): its compressed tile is then all
-    // masked.  The joint route rounds the PV dequantization differently from
-    // the tiled one, so the row keeps it.
-    const bool joint4 = RATIO == 4 && joint_launch && m.count <= N;
-    if (joint4 && m.position >= 0) m.total = 2;
-    const int my_tiles = m.total > part ? (m.total - part + S - 1) / S : 0;   // tiles part, part + S, ...
-    // A live row's window list holds at least its own position, so it has a
-    // tile, unless its request lists more query tokens than its sequence
-    // length (a negative position, which reference.py:104-105 rejects): that
-    // row is zero-filled, explicit original slots or not.
-    if (m.total == 0 || m.position < 0) {
-        zero_row();
-        return;
-    }
-    // Partitions that own no tile (part >= total) hold the initial state
-    // (max = sink <= every owning partition's max, numerator and denominator
-    // 0), which folds to exactly nothing: they publish nothing, and a row
-    // whose tiles all sit in partition 0 is finalized by it directly.  The
-    // numbers equal the fold over all S partitions bit for bit.
-    const int folded = S < m.total ? S : m.total;    // partitions that own tiles (>= 1)
-    if (part >= folded) return;
-    // Joint row (reference.py:254-267 with joint_dense for C128, joint_sparse
-    // for C4; the reference device's two-kind pipeline, attention_impl.h:
-    // 94-100, and C4 task batches): a row run as one partition whose window
-    // and compressed lists each fit one tile takes one softmax over both
-    // kinds (joint_quantized_row, reference.py:175-207) instead of two
-    // online tiles.  Tile 0 holds the window's keys in order, tile 1 the
-    // compressed list's, the order in which the reference concatenates
-    // them; the weight sum is one pairwise tree per kind, added in kind
-    // order.  Explicit original slots, more than eight heads (no residual
-    // codes) and the debug entry keep the tiled plan.
-    const bool joint = RATIO == 128 ? !DEBUG && !SLOTS && resid && S == 1 && m.t0 == 1 && m.list_len >= 1 &&
-                                          m.list_len <= N
-                                    : joint4 && m.total == 2;
-
-    // ---- per-lane softmax state for heads 2g and 2g+1 ----
-    float mx[2] = {sink0, sink1}, den[2], num[2][4];
-#pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-        den[hh] = part == 0 ? 1.0f : 0.0f;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) num[hh][j] = 0.0f;
-    }
-
-    // PV integers of the last computed tile, awaiting the FP32 epilogue
-    // (reference.py:313-316): num = num * factor + (V_hi + V_lo/127) * scale/127.
-    v4i held_acc[4];
-    float held_sc[4], held_factor[2];
-    bool held = false;
-    auto epilogue = [&]() {
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                float dots = (float)held_acc[j][2 * hh];
-                dots = dots + (float)held_acc[j][2 * hh + 1] * (float)(1.0 / 127.0);
-                const float pv = dots * held_sc[j] * (float)(1.0 / 127.0);
-                num[hh][j] = num[hh][j] * held_factor[hh] + pv;
-            }
-        }
-        held = false;
-    };
-
-    const int positions = 128 + (int)dbg.cmpCapacity;
-    const int c0 = 64 * wave;       // this wave's 64 PV output columns: c0 + 16 j + n
-
-    // Q folding and residual split for both kinds (reference.py:274-279),
-    // done once while the first tile's rows are in flight.  Thread = head
-    // `wave`, channels qd0 .. qd0 + 7.  Codes are staged in tile buffer 1
-    // (before any tile is requested into it) and picked up in the MFMA A
-    // layout.
-    v4i qa0[8], qa1[8];   // Q codes per 64-byte D block, window / compressed kind
-    // Its inputs pass through opaque copies, so the compiler computes the
-    // encode where it is called instead of ahead of the row codes.
-    auto encode_q = [&](bool want0, bool want1) {
-        v4i qx = qv;
-        int lx = lane;
-        asm volatile("" : "+v"(qx), "+v"(lx));
-        const int qe0 = lx * 8, ne = lx & 15, ge = lx >> 4;
-        const uint32_t qw[4] = {(uint32_t)qx.x, (uint32_t)qx.y, (uint32_t)qx.z, (uint32_t)qx.w};
-#pragma unroll
-        for (int kind = 0; kind < 2; ++kind) {
-            if (!(kind ? want1 : want0)) continue;
-            const float *scale = s.scale[kind] + qe0;
-            float f[8];
-            float amax = 0.0f;
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                f[e] = bf16_to_f32((qw[e >> 1] >> (16 * (e & 1))) & 0xffffu) * scale[e];
-                amax = fmaxf(amax, fabsf(f[e]));
-            }
-            amax = wave_max(amax);              // the head's 512 channels
-            float alpha = amax * (float)(1.0 / 127.0);
-            alpha = alpha < 1e-12f ? 1e-12f : alpha;
-            const float inv = 1.0f / alpha;
-            uint32_t hiw[2] = {0, 0}, low[2] = {0, 0};
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float x = clamp127(f[e] * inv);
-                const float hi = __builtin_rintf(x);
-                const float lo = resid ? __builtin_rintf((x - hi) * 127.0f) : 0.0f;
-                hiw[e >> 2] |= ((uint32_t)(int32_t)hi & 0xffu) << (8 * (e & 3));
-                low[e >> 2] |= ((uint32_t)(int32_t)lo & 0xffu) << (8 * (e & 3));
-            }
-            int8_t *stage = s.tile[1] + kind * 16 * QSTAGE;
-            *reinterpret_cast<u32x2 *>(stage + row_of(wave, 0) * QSTAGE + qe0) = u32x2{hiw[0], hiw[1]};
-            *reinterpret_cast<u32x2 *>(stage + row_of(wave, 1) * QSTAGE + qe0) = u32x2{low[0], low[1]};
-            if (lane == 0) s.asc[kind][wave] = alpha * p.softmaxScale;
-            if (DEBUG) {
-                if (dbg.qcodes) {
-                    int8_t *qc = reinterpret_cast<int8_t *>(dbg.qcodes) + (((int64_t)t * 2 + kind) * 16) * D;
-                    *reinterpret_cast<u32x2 *>(qc + wave * D + qe0) = u32x2{hiw[0], hiw[1]};
-                    *reinterpret_cast<u32x2 *>(qc + (8 + wave) * D + qe0) = u32x2{low[0], low[1]};
-                }
-                if (dbg.alpha && lane == 0)
-                    reinterpret_cast<float *>(dbg.alpha)[((int64_t)t * 2 + kind) * 8 + wave] = alpha;
-            }
-        }
-        lds_barrier();
-        const int8_t *st0 = s.tile[1], *st1 = s.tile[1] + 16 * QSTAGE;
-#pragma unroll
-        for (int jj = 0; jj < 8; ++jj) {
-            qa0[jj] = want0 ? *reinterpret_cast<const v4i *>(st0 + ne * QSTAGE + 64 * jj + 16 * ge) : v4i{0, 0, 0, 0};
-            qa1[jj] = want1 ? *reinterpret_cast<const v4i *>(st1 + ne * QSTAGE + 64 * jj + 16 * ge) : v4i{0, 0, 0, 0};
-        }
-    };
-
-    // LDS DMA of resident tile `i` into ring buffer `buf`: 8 instructions per
-    // wave, always all 64 lanes (masked keys read a harmless in-bounds
-    // address instead), so each tile is exactly DMA_PER_TILE vector-memory
-    // operations per wave for vm_wait.
-    // Instructions [r0, r0 + count) of the tile's DMA.  The row addresses
-    // of a batch are read before its first copy is issued (each copy is a
-    // compiler barrier for LDS accesses).
-    auto issue_rows = [&](int i, int buf, int r0, int count) {
-        const int h = lane >> 5, c = lane & 31;
-        typedef uint64_t u64x2 __attribute__((ext_vector_type(2)));
-        const u64x2 *rows = reinterpret_cast<const u64x2 *>(s.addr + i * N + 16 * wave + 8 * h + r0);   // keys 16 wave + 8 h + r
-        u64x2 ra[DMA_PER_TILE / 2];
-#pragma unroll
-        for (int r = 0; r < DMA_PER_TILE / 2; ++r)
-            if (2 * r < count) ra[r] = rows[r];
-        const uint32_t dst = (uint32_t)(uintptr_t)(lds_i8 *)(s.tile[buf]) + 16 * wave * D;
-        const int hx = (h ^ wave) & 1;
-#pragma unroll
-        for (int k = 0; k < DMA_PER_TILE; ++k) {
-            if (k >= count) break;
-            const int r = r0 + k;
-            const int chunk = c ^ r ^ (hx << 3);   // swz(16 wave + 2 r + h)
-            dma16<STREAM>(ra[k >> 1][k & 1] + (uint32_t)(chunk << 4), (uint32_t)uni((int)(dst + 2 * r * D)));
-        }
-    };
-    auto issue_tile = [&](int i, int buf) { issue_rows(i, buf, 0, DMA_PER_TILE); };
-    // The next tile's copies are spread over four points of the current
-    // tile's body, two instructions each, so no wave stalls behind a full
-    // tile's worth of queued copies.
-    constexpr int DMA_STEP = DMA_PER_TILE / 4;
-
-    // A C4 row without explicit slots has one chunk of codes: saying so lets
-    // the compiler end the live ranges of its selection values there.
-    constexpr bool ONE_CHUNK = RATIO == 4 && !SLOTS;
-    for (int first = 0; first < my_tiles && (!ONE_CHUNK || first == 0); first += CODE_TILES) {
-        const int ntiles = my_tiles - first < CODE_TILES ? my_tiles - first : CODE_TILES;
-        // ---- row codes of partition tiles [first, first + ntiles) ----
-        for (int i = tid; i < ntiles * N; i += THREADS) {
-            s.code[i] = -1;
-            s.addr[i] = p.q;              // masked rows: DMA reads 512 B of Q, never used
-        }
-        // Window / C128 rows: at most CODE_TILES * N / THREADS entries per
-        // thread, all block-table reads issued before any is used.  Rows
-        // whose logical page lies outside the block table, or whose physical
-        // page is negative or (window cache) past the pool, stay masked.
-        constexpr int PER = CODE_TILES * N / THREADS;
-        int tpage[PER], tidx[PER];
-#pragma unroll
-        for (int e = 0; e < PER; ++e) {
-            const int i = tid + e * THREADS;
-            tidx[e] = -1;
-            tpage[e] = -1;
-            if (RATIO == 4 && !SLOTS) {       // read before the compaction scan
-                if (e == 0) {
-                    tidx[0] = widx;
-                    tpage[0] = wpage;
-                }
-                continue;
-            }
-            if (i >= ntiles * N) continue;
-            const int k = part + S * (first + i / N), r = i % N;
-            if (SLOTS && k < m.t0) {
-                const int j = k * N + r;      // place in the slot list
-                if (j < m.ori_count) {
-                    tidx[e] = j;
-                    tpage[e] = oslots[j];     // the physical slot
-                }
-            } else if (k < m.t0) {
-                if (r < m.ori_count) {
-                    const int idx = m.first_ori + r;
-                    if (idx / BLOCK_ROWS < (int)p.oriTableWidth) {
-                        tidx[e] = idx;
-                        tpage[e] = otab[idx / BLOCK_ROWS];
-                    }
-                }
-            } else if (RATIO == 128) {
-                const int idx = (k - m.t0) * N + r;
-                if (idx < m.list_len && idx / BLOCK_ROWS < (int)p.cmpTableWidth) {
-                    tidx[e] = idx;
-                    tpage[e] = ctab[idx / BLOCK_ROWS];
-                }
-            }
-        }
-        int cslot[2] = {-1, -1};
-        if (RATIO == 4 && !joint) {       // joint rows take the dense list (below)
-#pragma unroll
-            for (int e = 0; e < 2; ++e) {
-                if (ipos[e] < 0 || ix[e] < 0) continue;
-                const int k = m.t0 + ipos[e] / N;
-                if (k < part || (k - part) % S) continue;
-                const int i = (k - part) / S - first;
-                if (i < 0 || i >= ntiles || ix[e] / BLOCK_ROWS >= (int)p.cmpTableWidth) continue;
-                cslot[e] = i * N + ipos[e] % N;
-            }
-        }
-        if (first == 0) *reinterpret_cast<f32x2 *>(&s.scale[tid >> 8][(tid & 255) * 2]) = scale_pair;
-        if (RATIO == 4 && joint && tid < N) s.mult[tid] = 0;
-        lds_barrier();                    // the -1 fill is complete before the writes below
-#pragma unroll
-        for (int e = 0; e < PER; ++e) {
-            if (tidx[e] < 0) continue;
-            const int i = tid + e * THREADS;
-            const bool window = part + S * (first + i / N) < m.t0;
-            if (SLOTS && window) {
-                const int slot = tpage[e];
-                if (slot >= 0 && (uint32_t)slot < p.oriPages * BLOCK_ROWS) {
-                    s.code[i] = slot;
-                    s.addr[i] = p.ori + (uint64_t)(slot / BLOCK_ROWS) * p.oriStride + (uint64_t)((slot % BLOCK_ROWS) * D);
-                }
-                continue;
-            }
-            const bool ok = tpage[e] >= 0 && (!window || (uint32_t)tpage[e] < p.oriPages);
-            if (ok) {
-                s.code[i] = tpage[e] * BLOCK_ROWS + tidx[e] % BLOCK_ROWS;
-                s.addr[i] = (window ? p.ori : p.cmp) + (uint64_t)tpage[e] * (window ? p.oriStride : p.cmpStride) +
-                            (uint64_t)((tidx[e] % BLOCK_ROWS) * D);
-            }
-        }
+        m.count = RATIO == 1 ? 0 : (m.position + 1) / RATIO;
+        // Global-space views: flat loads would also hold the LDS counter that the
+        // fence-free barriers below wait on.
+        const __attribute__((address_space(1))) int32_t *otab = gptr<int32_t>(p.oriTable) + (int64_t)m.batch * p.oriTableWidth;
+        const __attribute__((address_space(1))) int32_t *ctab = gptr<int32_t>(p.cmpTable) + (int64_t)m.batch * p.cmpTableWidth;
+        // C4: every block-table read of the row (the window tile, held by
+        // partition 0, and the thread's two index entries) is issued here, so
+        // the compaction scan below runs while they are in flight.  A C4 row
+        // has at most 1 + MAX_LIST / N <= CODE_TILES tiles: one chunk of codes
+        // (explicit slots read theirs per chunk, below).
+        const __attribute__((address_space(1))) int32_t *oslots =
+            gptr<int32_t>(p.oriIndices) + (int64_t)t * p.oriTopk;
+        int wpage = -1, widx = -1, cpage_raw[2] = {-1, -1};
         if (RATIO == 4) {
+            if (!SLOTS && part == 0 && tid < m.ori_count) {
+                const int idx = m.first_ori + tid;
+                if (idx / BLOCK_ROWS < (int)p.oriTableWidth) {
+                    widx = idx;
+                    wpage = otab[idx / BLOCK_ROWS];
+                }
+            }
 #pragma unroll
             for (int e = 0; e < 2; ++e)
-                if (cslot[e] >= 0 && cpage_raw[e] >= 0) {
-                    s.code[cslot[e]] = cpage_raw[e] * BLOCK_ROWS + ix[e] % BLOCK_ROWS;
-                    s.addr[cslot[e]] = p.cmp + (uint64_t)cpage_raw[e] * p.cmpStride + (uint64_t)((ix[e] % BLOCK_ROWS) * D);
+                if (ix[e] >= 0 && ix[e] < m.count && ix[e] / BLOCK_ROWS < (int)p.cmpTableWidth)
+                    cpage_raw[e] = ctab[ix[e] / BLOCK_ROWS];
+        }
+        static_assert(1 + MAX_LIST / N <= CODE_TILES, "a C4 row's codes fit one chunk");
+        int ipos[2] = {-1, -1};   // list position of each owned C4 entry (-1: none)
+        if (RATIO == 4) {
+            const int topk = (int)p.topk;
+            const bool compact = m.count < topk && topk <= MAX_LIST;   // reference.py:250
+            bool ok[2];
+#pragma unroll
+            for (int i = 0; i < 2; ++i) ok[i] = ix[i] >= 0 && ix[i] < m.count;
+            if (compact) {
+                // Entry 2 tid + i goes to place (valid entries of lower lanes and
+                // waves) + (entry 0 of this lane, for i = 1): two ballots, counted
+                // below the lane with mbcnt.
+                const uint64_t v0 = __ballot(ok[0]), v1 = __ballot(ok[1]);
+                const int below = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(v0 >> 32),
+                                                                 __builtin_amdgcn_mbcnt_lo((uint32_t)v0, 0u)) +
+                                  (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(v1 >> 32),
+                                                                 __builtin_amdgcn_mbcnt_lo((uint32_t)v1, 0u));
+                if (lane == 0) s.scan[wave] = __popcll(v0) + __popcll(v1);
+                lds_barrier();                    // no fence: the table reads stay in flight
+                int at = below, total = 0;
+#pragma unroll
+                for (int w = 0; w < WAVES; ++w) {
+                    at += w < wave ? s.scan[w] : 0;
+                    total += s.scan[w];
                 }
-            if (joint) {
-                // Tile 1 = the dense compressed list (reference.py:246-249):
-                // each row's multiplicity among the valid entries, then the
-                // listed rows (multiplicity > 0) in row order.  The owner of
-                // an entry writes its row's code at the row's list place
-                // (entries naming one row write the same code), from the
-                // table entry it read for the tiled plan; thread r writes
-                // row r's bias.
 #pragma unroll
-                for (int e = 0; e < 2; ++e)
-                    if (ix[e] >= 0 && ix[e] < m.count) atomicAdd(&s.mult[ix[e]], 1);
-                lds_barrier();
-                const int times = tid < N ? s.mult[tid] : 0;
-                const uint64_t listed = __ballot(times > 0);
-                if (lane == 0 && wave < 2) s.listed[wave] = listed;
-                lds_barrier();
-                const uint64_t lo = s.listed[0], hi = s.listed[1];
-                auto place = [&](int r) {   // listed rows below r
-                    return r < 64 ? __popcll(lo & ((1ull << r) - 1)) : __popcll(lo) + __popcll(hi & ((1ull << (r - 64)) - 1));
-                };
-                if (times > 0) s.bias[place(tid)] = (float)log((double)times);   // exact: see the oracle's log_count
+                for (int i = 0; i < 2; ++i)
+                    if (ok[i]) ipos[i] = at++;
+                m.list_len = uni(total);
+            } else {
 #pragma unroll
-                for (int e = 0; e < 2; ++e)
-                    if (ix[e] >= 0 && ix[e] < m.count && cpage_raw[e] >= 0) {
-                        const int j = N + place(ix[e]);
-                        s.code[j] = cpage_raw[e] * BLOCK_ROWS + ix[e] % BLOCK_ROWS;
-                        s.addr[j] = p.cmp + (uint64_t)cpage_raw[e] * p.cmpStride + (uint64_t)((ix[e] % BLOCK_ROWS) * D);
+                for (int i = 0; i < 2; ++i) {
+                    const int j = tid * 2 + i;
+                    if (j < topk) ipos[i] = j;
+                    if (!ok[i]) ix[i] = -1;        // hole: a masked column in place
+                }
+                m.list_len = topk;
+            }
+        } else if (RATIO == 128) {
+            m.list_len = m.count > 0 ? m.count : 0;
+        } else {
+            m.list_len = 0;   // window only
+        }
+        m.t0 = (m.ori_count + N - 1) / N;
+        m.total = m.t0 + (m.list_len + N - 1) / N;
+        // Joint sparse row (C4, reference.py:246-267 with joint_sparse; JOINT
+        // instantiations only): in a launch of the joint plan (every live row's
+        // compressed rows fit one tile: count <= N) a row's compressed list is
+        // dense: every row below
+        // count that some valid top-k entry names, once, in row order, with
+        // log(multiplicity) added to its logits (built with the row codes,
+        // below).  reference.py switches every C4 row of such a plan to the
+        // dense list, so a launch with a longer row has no joint C4 rows (the
+        // reference device decides per launch too, c4.cpp:35-58).  A joint C4
+        // row is two tiles even when it lists no compressed row (reference.py:257
+        // takes the joint route then too): its compressed tile is then all
+        // masked.  The joint route rounds the PV dequantization differently from
+        // the tiled one, so the row keeps it.
+        const bool joint4 = RATIO == 4 && joint_launch && m.count <= N;
+        if (joint4 && m.position >= 0) m.total = 2;
+        const int my_tiles = m.total > part ? (m.total - part + S - 1) / S : 0;   // tiles part, part + S, ...
+        // A live row's window list holds at least its own position, so it has a
+        // tile, unless its request lists more query tokens than its sequence
+        // length (a negative position, which reference.py:104-105 rejects): that
+        // row is zero-filled, explicit original slots or not.
+        if (m.total == 0 || m.position < 0) {
+            zero_row();
+            return;
+        }
+        // Partitions that own no tile (part >= total) hold the initial state
+        // (max = sink <= every owning partition's max, numerator and denominator
+        // 0), which folds to exactly nothing: they publish nothing, and a row
+        // whose tiles all sit in partition 0 is finalized by it directly.  The
+        // numbers equal the fold over all S partitions bit for bit.
+        const int folded = S < m.total ? S : m.total;    // partitions that own tiles (>= 1)
+        if (part >= folded) return;
+        // Joint row (reference.py:254-267 with joint_dense for C128, joint_sparse
+        // for C4; the reference device's two-kind pipeline, attention_impl.h:
+        // 94-100, and C4 task batches): a row run as one partition whose window
+        // and compressed lists each fit one tile takes one softmax over both
+        // kinds (joint_quantized_row, reference.py:175-207) instead of two
+        // online tiles.  Tile 0 holds the window's keys in order, tile 1 the
+        // compressed list's, the order in which the reference concatenates
+        // them; the weight sum is one pairwise tree per kind, added in kind
+        // order.  Explicit original slots, more than eight heads (no residual
+        // codes) and the debug entry keep the tiled plan.
+        const bool joint = RATIO == 128 ? !DEBUG && !SLOTS && resid && S == 1 && m.t0 == 1 && m.list_len >= 1 &&
+                                              m.list_len <= N
+                                        : joint4 && m.total == 2;
+
+        // ---- per-lane softmax state for heads 2g and 2g+1 ----
+        float mx[2] = {sink0, sink1}, den[2], num[2][4];
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            den[hh] = part == 0 ? 1.0f : 0.0f;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) num[hh][j] = 0.0f;
+        }
+
+        // PV integers of the last computed tile, awaiting the FP32 epilogue
+        // (reference.py:313-316): num = num * factor + (V_hi + V_lo/127) * scale/127.
+        v4i held_acc[4];
+        float held_sc[4], held_factor[2];
+        bool held = false;
+        auto epilogue = [&]() {
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    float dots = (float)held_acc[j][2 * hh];
+                    dots = dots + (float)held_acc[j][2 * hh + 1] * (float)(1.0 / 127.0);
+                    const float pv = dots * held_sc[j] * (float)(1.0 / 127.0);
+                    num[hh][j] = num[hh][j] * held_factor[hh] + pv;
+                }
+            }
+            held = false;
+        };
+
+        const int positions = 128 + (int)dbg.cmpCapacity;
+        const int c0 = 64 * wave;       // this wave's 64 PV output columns: c0 + 16 j + n
+
+        // Q folding and residual split for both kinds (reference.py:274-279),
+        // done once while the first tile's rows are in flight.  Thread = head
+        // `wave`, channels qd0 .. qd0 + 7.  Codes are staged in tile buffer 1
+        // (before any tile is requested into it) and picked up in the MFMA A
+        // layout.
+        v4i qa0[8], qa1[8];   // Q codes per 64-byte D block, window / compressed kind
+        // Its inputs pass through opaque copies, so the compiler computes the
+        // encode where it is called instead of ahead of the row codes.
+        auto encode_q = [&](bool want0, bool want1) {
+            v4i qx = qv;
+            int lx = lane;
+            asm volatile("" : "+v"(qx), "+v"(lx));
+            const int qe0 = lx * 8, ne = lx & 15, ge = lx >> 4;
+            const uint32_t qw[4] = {(uint32_t)qx.x, (uint32_t)qx.y, (uint32_t)qx.z, (uint32_t)qx.w};
+#pragma unroll
+            for (int kind = 0; kind < 2; ++kind) {
+                if (!(kind ? want1 : want0)) continue;
+                const float *scale = s.scale[kind] + qe0;
+                float f[8];
+                float amax = 0.0f;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    f[e] = bf16_to_f32((qw[e >> 1] >> (16 * (e & 1))) & 0xffffu) * scale[e];
+                    amax = fmaxf(amax, fabsf(f[e]));
+                }
+                amax = wave_max(amax);              // the head's 512 channels
+                float alpha = amax * (float)(1.0 / 127.0);
+                alpha = alpha < 1e-12f ? 1e-12f : alpha;
+                const float inv = 1.0f / alpha;
+                uint32_t hiw[2] = {0, 0}, low[2] = {0, 0};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const float x = clamp127(f[e] * inv);
+                    const float hi = __builtin_rintf(x);
+                    const float lo = resid ? __builtin_rintf((x - hi) * 127.0f) : 0.0f;
+                    hiw[e >> 2] |= ((uint32_t)(int32_t)hi & 0xffu) << (8 * (e & 3));
+                    low[e >> 2] |= ((uint32_t)(int32_t)lo & 0xffu) << (8 * (e & 3));
+                }
+                int8_t *stage = s.tile[1] + kind * 16 * QSTAGE;
+                *reinterpret_cast<u32x2 *>(stage + row_of(wave, 0) * QSTAGE + qe0) = u32x2{hiw[0], hiw[1]};
+                *reinterpret_cast<u32x2 *>(stage + row_of(wave, 1) * QSTAGE + qe0) = u32x2{low[0], low[1]};
+                if (lane == 0) s.asc[kind][wave] = alpha * p.softmaxScale;
+                if (DEBUG) {
+                    if (dbg.qcodes) {
+                        int8_t *qc = reinterpret_cast<int8_t *>(dbg.qcodes) + (((int64_t)t * 2 + kind) * 16) * D;
+                        *reinterpret_cast<u32x2 *>(qc + wave * D + qe0) = u32x2{hiw[0], hiw[1]};
+                        *reinterpret_cast<u32x2 *>(qc + (8 + wave) * D + qe0) = u32x2{low[0], low[1]};
                     }
-            }
-        }
-        lds_barrier();                    // codes visible
-
-        // Tile 0's rows are requested first; the Q encode (staged in tile
-        // buffer 1) and the tile loop's per-lane set-up run while they are in
-        // flight, then tile 1 follows into the freed buffer.
-        issue_tile(0, 0);
-        if (first == 0) {
-            bool want0 = false, want1 = false;
-            for (int i = 0; i < my_tiles; ++i) {
-                const bool kind1 = part + S * i >= m.t0;
-                want0 |= !kind1;
-                want1 |= kind1;
-            }
-            encode_q(want0, want1);
-            lds_barrier();                // every wave holds its Q codes: buffer 1 is free
-        }
-        if (ntiles > 1) issue_tile(1, 1);
-
-        // The tile loop's per-lane LDS addresses derive from an opaque copy
-        // of the lane index, so they are computed here, while the first rows
-        // are in flight, rather than ahead of the row codes.
-        int lane_x = lane;
-        asm volatile("" : "+v"(lane_x));
-        const int gx = lane_x >> 4, nx = lane_x & 15;
-
-        if (joint) {
-            // ---- joint row: both tiles resident (tile 0 = window in buffer
-            // 0, tile 1 = compressed rows in buffer 1) ----
-            vm_wait<0>();
-            lds_barrier();
-            const int key = 16 * wave + nx;
-            const int sl = slot_of(key);
-            // QK of both kinds, each with its own Q encoding (reference.py:181-188).
-            v4i sacc[2] = {v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}};
-#pragma unroll
-            for (int kind = 0; kind < 2; ++kind) {
-                v4i b[8];
-#pragma unroll
-                for (int j = 0; j < 8; ++j) b[j] = *reinterpret_cast<const v4i *>(s.tile[kind] + tile_offset(sl, 4 * j + gx));
-#pragma unroll
-                for (int j = 0; j < 8; ++j)
-                    sacc[kind] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kind ? qa1[j] : qa0[j], b[j], sacc[kind], 0, 0, 0);
-            }
-            float lg[2][2];   // [kind][head 2g + hh]
-#pragma unroll
-            for (int kind = 0; kind < 2; ++kind) {
-                const bool valid = s.code[kind * N + key] >= 0;
-#pragma unroll
-                for (int hh = 0; hh < 2; ++hh) {
-                    float dots = (float)sacc[kind][2 * hh];
-                    dots = dots + (float)sacc[kind][2 * hh + 1] * (float)(1.0 / 127.0);
-                    float l = dots * s.asc[kind][2 * gx + hh];
-                    if (RATIO == 4 && kind == 1) l = l + s.bias[key];   // reference.py:189-190, 261
-                    lg[kind][hh] = valid ? l : -1e30f;
+                    if (dbg.alpha && lane == 0)
+                        reinterpret_cast<float *>(dbg.alpha)[((int64_t)t * 2 + kind) * 8 + wave] = alpha;
                 }
             }
-            // maximum = max(sink, every score of both kinds) (reference.py:193)
-#pragma unroll
-            for (int hh = 0; hh < 2; ++hh) {
-                const int kmax = row16_max_key(max(fkey(lg[0][hh]), fkey(lg[1][hh])));
-                if (nx == 0) s.redmax[2 * gx + hh][wave] = kmax;
-            }
             lds_barrier();
-            float mnew[2], factor[2];
+            const int8_t *st0 = s.tile[1], *st1 = s.tile[1] + 16 * QSTAGE;
 #pragma unroll
-            for (int hh = 0; hh < 2; ++hh) {
-                const int h = 2 * gx + hh;
-                const v4i a = *reinterpret_cast<const v4i *>(&s.redmax[h][0]);
-                const v4i b = *reinterpret_cast<const v4i *>(&s.redmax[h][4]);
-                const int k = max(max(max(fkey(mx[hh]), a.x), max(a.y, a.z)), max(max(a.w, b.x), max(max(b.y, b.z), b.w)));
-                mnew[hh] = fkey_value(k);
+            for (int jj = 0; jj < 8; ++jj) {
+                qa0[jj] = want0 ? *reinterpret_cast<const v4i *>(st0 + ne * QSTAGE + 64 * jj + 16 * ge) : v4i{0, 0, 0, 0};
+                qa1[jj] = want1 ? *reinterpret_cast<const v4i *>(st1 + ne * QSTAGE + 64 * jj + 16 * ge) : v4i{0, 0, 0, 0};
             }
-            {
-                const bool odd = nx & 1;   // exp(sink - maximum), one exponential per lane pair
-                const float mine = sk_expf_nonpos(odd ? mx[1] - mnew[1] : mx[0] - mnew[0]);
-                const float other = dpp<DPP_XOR1>(mine);
-                factor[0] = odd ? other : mine;
-                factor[1] = odd ? mine : other;
-            }
-            // Weights and P codes (reference.py:194-198); the compressed
-            // tile's P codes go to the free address table.
-            int8_t *p1 = reinterpret_cast<int8_t *>(s.addr);
-            static_assert(16 * PROW <= (int)sizeof(s.addr), "P codes of the second tile fit the address table");
+        };
+
+        // LDS DMA of resident tile `i` into ring buffer `buf`: 8 instructions per
+        // wave, always all 64 lanes (masked keys read a harmless in-bounds
+        // address instead), so each tile is exactly DMA_PER_TILE vector-memory
+        // operations per wave for vm_wait.
+        // Instructions [r0, r0 + count) of the tile's DMA.  The row addresses
+        // of a batch are read before its first copy is issued (each copy is a
+        // compiler barrier for LDS accesses).
+        auto issue_rows = [&](int i, int buf, int r0, int count) {
+            const int h = lane >> 5, c = lane & 31;
+            typedef uint64_t u64x2 __attribute__((ext_vector_type(2)));
+            const u64x2 *rows = reinterpret_cast<const u64x2 *>(s.addr + i * N + 16 * wave + 8 * h + r0);   // keys 16 wave + 8 h + r
+            u64x2 ra[DMA_PER_TILE / 2];
 #pragma unroll
-            for (int kind = 0; kind < 2; ++kind) {
-                int8_t *pk = kind ? p1 : s.p;
+            for (int r = 0; r < DMA_PER_TILE / 2; ++r)
+                if (2 * r < count) ra[r] = rows[r];
+            const uint32_t dst = (uint32_t)(uintptr_t)(lds_i8 *)(s.tile[buf]) + 16 * wave * D;
+            const int hx = (h ^ wave) & 1;
+#pragma unroll
+            for (int k = 0; k < DMA_PER_TILE; ++k) {
+                if (k >= count) break;
+                const int r = r0 + k;
+                const int chunk = c ^ r ^ (hx << 3);   // swz(16 wave + 2 r + h)
+                dma16<STREAM>(ra[k >> 1][k & 1] + (uint32_t)(chunk << 4), (uint32_t)uni((int)(dst + 2 * r * D)));
+            }
+        };
+        auto issue_tile = [&](int i, int buf) { issue_rows(i, buf, 0, DMA_PER_TILE); };
+        // The next tile's copies are spread over four points of the current
+        // tile's body, two instructions each, so no wave stalls behind a full
+        // tile's worth of queued copies.
+        constexpr int DMA_STEP = DMA_PER_TILE / 4;
+
+        // A C4 row without explicit slots has one chunk of codes: saying so lets
+        // the compiler end the live ranges of its selection values there.
+        constexpr bool ONE_CHUNK = RATIO == 4 && !SLOTS;
+        for (int first = 0; first < my_tiles && (!ONE_CHUNK || first == 0); first += CODE_TILES) {
+            const int ntiles = my_tiles - first < CODE_TILES ? my_tiles - first : CODE_TILES;
+            // ---- row codes of partition tiles [first, first + ntiles) ----
+            for (int i = tid; i < ntiles * N; i += THREADS) {
+                s.code[i] = -1;
+                s.addr[i] = p.q;              // masked rows: DMA reads 512 B of Q, never used
+            }
+            // Window / C128 rows: at most CODE_TILES * N / THREADS entries per
+            // thread, all block-table reads issued before any is used.  Rows
+            // whose logical page lies outside the block table, or whose physical
+            // page is negative or (window cache) past the pool, stay masked.
+            constexpr int PER = CODE_TILES * N / THREADS;
+            int tpage[PER], tidx[PER];
+#pragma unroll
+            for (int e = 0; e < PER; ++e) {
+                const int i = tid + e * THREADS;
+                tidx[e] = -1;
+                tpage[e] = -1;
+                if (RATIO == 4 && !SLOTS) {       // read before the compaction scan
+                    if (e == 0) {
+                        tidx[0] = widx;
+                        tpage[0] = wpage;
+                    }
+                    continue;
+                }
+                if (i >= ntiles * N) continue;
+                const int k = part + S * (first + i / N), r = i % N;
+                if (SLOTS && k < m.t0) {
+                    const int j = k * N + r;      // place in the slot list
+                    if (j < m.ori_count) {
+                        tidx[e] = j;
+                        tpage[e] = oslots[j];     // the physical slot
+                    }
+                } else if (k < m.t0) {
+                    if (r < m.ori_count) {
+                        const int idx = m.first_ori + r;
+                        if (idx / BLOCK_ROWS < (int)p.oriTableWidth) {
+                            tidx[e] = idx;
+                            tpage[e] = otab[idx / BLOCK_ROWS];
+                        }
+                    }
+                } else if (RATIO == 128) {
+                    const int idx = (k - m.t0) * N + r;
+                    if (idx < m.list_len && idx / BLOCK_ROWS < (int)p.cmpTableWidth) {
+                        tidx[e] = idx;
+                        tpage[e] = ctab[idx / BLOCK_ROWS];
+                    }
+                }
+            }
+            int cslot[2] = {-1, -1};
+            if (RATIO == 4 && !joint) {       // joint rows take the dense list (below)
+#pragma unroll
+                for (int e = 0; e < 2; ++e) {
+                    if (ipos[e] < 0 || ix[e] < 0) continue;
+                    const int k = m.t0 + ipos[e] / N;
+                    if (k < part || (k - part) % S) continue;
+                    const int i = (k - part) / S - first;
+                    if (i < 0 || i >= ntiles || ix[e] / BLOCK_ROWS >= (int)p.cmpTableWidth) continue;
+                    cslot[e] = i * N + ipos[e] % N;
+                }
+            }
+            if (first == 0) *reinterpret_cast<f32x2 *>(&s.scale[tid >> 8][(tid & 255) * 2]) = scale_pair;
+            if (RATIO == 4 && joint && tid < N) s.mult[tid] = 0;
+            lds_barrier();                    // the -1 fill is complete before the writes below
+#pragma unroll
+            for (int e = 0; e < PER; ++e) {
+                if (tidx[e] < 0) continue;
+                const int i = tid + e * THREADS;
+                const bool window = part + S * (first + i / N) < m.t0;
+                if (SLOTS && window) {
+                    const int slot = tpage[e];
+                    if (slot >= 0 && (uint32_t)slot < p.oriPages * BLOCK_ROWS) {
+                        s.code[i] = slot;
+                        s.addr[i] = p.ori + (uint64_t)(slot / BLOCK_ROWS) * p.oriStride + (uint64_t)((slot % BLOCK_ROWS) * D);
+                    }
+                    continue;
+                }
+                const bool ok = tpage[e] >= 0 && (!window || (uint32_t)tpage[e] < p.oriPages);
+                if (ok) {
+                    s.code[i] = tpage[e] * BLOCK_ROWS + tidx[e] % BLOCK_ROWS;
+                    s.addr[i] = (window ? p.ori : p.cmp) + (uint64_t)tpage[e] * (window ? p.oriStride : p.cmpStride) +
+                                (uint64_t)((tidx[e] % BLOCK_ROWS) * D);
+                }
+            }
+            if (RATIO == 4) {
+#pragma unroll
+                for (int e = 0; e < 2; ++e)
+                    if (cslot[e] >= 0 && cpage_raw[e] >= 0) {
+                        s.code[cslot[e]] = cpage_raw[e] * BLOCK_ROWS + ix[e] % BLOCK_ROWS;
+                        s.addr[cslot[e]] = p.cmp + (uint64_t)cpage_raw[e] * p.cmpStride + (uint64_t)((ix[e] % BLOCK_ROWS) * D);
+                    }
+                if (joint) {
+                    // Tile 1 = the dense compressed list (reference.py:246-249):
+                    // each row's multiplicity among the valid entries, then the
+                    // listed rows (multiplicity > 0) in row order.  The owner of
+                    // an entry writes its row's code at the row's list place
+                    // (entries naming one row write the same code), from the
+                    // table entry it read for the tiled plan; thread r writes
+                    // row r's bias.
+#pragma unroll
+                    for (int e = 0; e < 2; ++e)
+                        if (ix[e] >= 0 && ix[e] < m.count) atomicAdd(&s.mult[ix[e]], 1);
+                    lds_barrier();
+                    const int times = tid < N ? s.mult[tid] : 0;
+                    const uint64_t listed = __ballot(times > 0);
+                    if (lane == 0 && wave < 2) s.listed[wave] = listed;
+                    lds_barrier();
+                    const uint64_t lo = s.listed[0], hi = s.listed[1];
+                    auto place = [&](int r) {   // listed rows below r
+                        return r < 64 ? __popcll(lo & ((1ull << r) - 1)) : __popcll(lo) + __popcll(hi & ((1ull << (r - 64)) - 1));
+                    };
+                    if (times > 0) s.bias[place(tid)] = (float)log((double)times);   // exact: see the oracle's log_count
+#pragma unroll
+                    for (int e = 0; e < 2; ++e)
+                        if (ix[e] >= 0 && ix[e] < m.count && cpage_raw[e] >= 0) {
+                            const int j = N + place(ix[e]);
+                            s.code[j] = cpage_raw[e] * BLOCK_ROWS + ix[e] % BLOCK_ROWS;
+                            s.addr[j] = p.cmp + (uint64_t)cpage_raw[e] * p.cmpStride + (uint64_t)((ix[e] % BLOCK_ROWS) * D);
+                        }
+                }
+            }
+            lds_barrier();                    // codes visible
+
+            // Tile 0's rows are requested first; the Q encode (staged in tile
+            // buffer 1) and the tile loop's per-lane set-up run while they are in
+            // flight, then tile 1 follows into the freed buffer.
+            issue_tile(0, 0);
+            if (PERSIST && first == 0 && qrow + (int32_t)G < (int32_t)rows_arg) {
+                // The next row's Q and indices, behind this tile's copies
+                // (the first tile wait covers them).
+                const int32_t nrow = qrow + (int32_t)G, nt = ANYH ? nrow / HG : nrow;
+                const int32_t nbase = ANYH ? HEADS * (nrow % HG) : 0;
+                const int nlive = ANYH ? (H - nbase < HEADS ? H - nbase : HEADS) : HEADS;
+                qv_next = v4i{0, 0, 0, 0};
+                if (!ANYH || wave < nlive)
+                    qv_next = *gptr<v4i>(q_base + (((uint64_t)nt * H + nbase + wave) * D + qd0) * 2);
+                if (RATIO == 4) {
+                    const int topk = (int)topk_arg;
+                    const __attribute__((address_space(1))) int32_t *next_ix = gptr<int32_t>(cmp_indices) + (int64_t)nt * topk;
+#pragma unroll
+                    for (int i = 0; i < 2; ++i) ix_next[i] = tid * 2 + i < topk ? next_ix[tid * 2 + i] : -1;
+                }
+                prefetched = true;
+            }
+            if (first == 0) {
+                bool want0 = false, want1 = false;
+                for (int i = 0; i < my_tiles; ++i) {
+                    const bool kind1 = part + S * i >= m.t0;
+                    want0 |= !kind1;
+                    want1 |= kind1;
+                }
+                encode_q(want0, want1);
+                lds_barrier();                // every wave holds its Q codes: buffer 1 is free
+            }
+            if (ntiles > 1) issue_tile(1, 1);
+
+            // The tile loop's per-lane LDS addresses derive from an opaque copy
+            // of the lane index, so they are computed here, while the first rows
+            // are in flight, rather than ahead of the row codes.
+            int lane_x = lane;
+            asm volatile("" : "+v"(lane_x));
+            const int gx = lane_x >> 4, nx = lane_x & 15;
+
+            if (joint) {
+                // ---- joint row: both tiles resident (tile 0 = window in buffer
+                // 0, tile 1 = compressed rows in buffer 1) ----
+                vm_wait<0>();
+                lds_barrier();
+                const int key = 16 * wave + nx;
+                const int sl = slot_of(key);
+                // QK of both kinds, each with its own Q encoding (reference.py:181-188).
+                v4i sacc[2] = {v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}};
+#pragma unroll
+                for (int kind = 0; kind < 2; ++kind) {
+                    v4i b[8];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) b[j] = *reinterpret_cast<const v4i *>(s.tile[kind] + tile_offset(sl, 4 * j + gx));
+#pragma unroll
+                    for (int j = 0; j < 8; ++j)
+                        sacc[kind] = __builtin_amdgcn_mfma_i32_16x16x64_i8(kind ? qa1[j] : qa0[j], b[j], sacc[kind], 0, 0, 0);
+                }
+                float lg[2][2];   // [kind][head 2g + hh]
+#pragma unroll
+                for (int kind = 0; kind < 2; ++kind) {
+                    const bool valid = s.code[kind * N + key] >= 0;
+#pragma unroll
+                    for (int hh = 0; hh < 2; ++hh) {
+                        float dots = (float)sacc[kind][2 * hh];
+                        dots = dots + (float)sacc[kind][2 * hh + 1] * (float)(1.0 / 127.0);
+                        float l = dots * s.asc[kind][2 * gx + hh];
+                        if (RATIO == 4 && kind == 1) l = l + s.bias[key];   // reference.py:189-190, 261
+                        lg[kind][hh] = valid ? l : -1e30f;
+                    }
+                }
+                // maximum = max(sink, every score of both kinds) (reference.py:193)
 #pragma unroll
                 for (int hh = 0; hh < 2; ++hh) {
-                    const float w = sk_expf_nonpos(lg[kind][hh] - mnew[hh]);
+                    const int kmax = row16_max_key(max(fkey(lg[0][hh]), fkey(lg[1][hh])));
+                    if (nx == 0) s.redmax[2 * gx + hh][wave] = kmax;
+                }
+                lds_barrier();
+                float mnew[2], factor[2];
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    const int h = 2 * gx + hh;
+                    const v4i a = *reinterpret_cast<const v4i *>(&s.redmax[h][0]);
+                    const v4i b = *reinterpret_cast<const v4i *>(&s.redmax[h][4]);
+                    const int k = max(max(max(fkey(mx[hh]), a.x), max(a.y, a.z)), max(max(a.w, b.x), max(max(b.y, b.z), b.w)));
+                    mnew[hh] = fkey_value(k);
+                }
+                {
+                    const bool odd = nx & 1;   // exp(sink - maximum), one exponential per lane pair
+                    const float mine = sk_expf_nonpos(odd ? mx[1] - mnew[1] : mx[0] - mnew[0]);
+                    const float other = dpp<DPP_XOR1>(mine);
+                    factor[0] = odd ? other : mine;
+                    factor[1] = odd ? mine : other;
+                }
+                // Weights and P codes (reference.py:194-198); the compressed
+                // tile's P codes go to the free address table.
+                int8_t *p1 = reinterpret_cast<int8_t *>(s.addr);
+                static_assert(16 * PROW <= (int)sizeof(s.addr), "P codes of the second tile fit the address table");
+#pragma unroll
+                for (int kind = 0; kind < 2; ++kind) {
+                    int8_t *pk = kind ? p1 : s.p;
+#pragma unroll
+                    for (int hh = 0; hh < 2; ++hh) {
+                        const float w = sk_expf_nonpos(lg[kind][hh] - mnew[hh]);
+                        const float x = w * 127.0f;
+                        const float ph = __builtin_rintf(x);
+                        const float pl = __builtin_rintf((x - ph) * 127.0f);
+                        pk[row_of(2 * gx + hh, 0) * PROW + key] = (int8_t)(int32_t)ph;
+                        pk[row_of(2 * gx + hh, 1) * PROW + key] = (int8_t)(int32_t)pl;
+                        const float wsum = row16_tree_sum(w);
+                        if (nx == 0) (kind ? s.redsum1 : s.redsum)[2 * gx + hh][wave] = wsum;
+                    }
+                }
+                lds_barrier();
+                // denominator = exp(sink - maximum) + (window tile's pairwise
+                // tree + compressed tile's); zero leaves past a kind's keys
+                // change neither tree.
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    const int h = 2 * gx + hh;
+                    const f32x4 a0 = *reinterpret_cast<const f32x4 *>(&s.redsum[h][0]);
+                    const f32x4 b0 = *reinterpret_cast<const f32x4 *>(&s.redsum[h][4]);
+                    const f32x4 a1 = *reinterpret_cast<const f32x4 *>(&s.redsum1[h][0]);
+                    const f32x4 b1 = *reinterpret_cast<const f32x4 *>(&s.redsum1[h][4]);
+                    const float t0 = ((a0.x + a0.y) + (a0.z + a0.w)) + ((b0.x + b0.y) + (b0.z + b0.w));
+                    const float t1 = ((a1.x + a1.y) + (a1.z + a1.w)) + ((b1.x + b1.y) + (b1.z + b1.w));
+                    den[hh] = factor[hh] + (t0 + t1);
+                }
+                // PV per kind, each added to the output as it completes:
+                // output = sum over kinds of dot * (scale / 127) in kind order
+                // (reference.py:199-206).
+#pragma unroll
+                for (int kind = 0; kind < 2; ++kind) {
+                    v4i vacc[4];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) vacc[j] = v4i{0, 0, 0, 0};
+                    const lds_i8 *vbase = (const lds_i8 *)(s.tile[kind]);
+#pragma unroll
+                    for (int kb = 0; kb < 2; ++kb) {
+                        const v4i pa = kind ? *reinterpret_cast<const v4i *>(p1 + nx * PROW + 64 * kb + 16 * gx)
+                                            : *reinterpret_cast<const v4i *>(s.p + nx * PROW + 64 * kb + 16 * gx);
+                        const int sl_lo = slot_of(64 * kb + 16 * gx + (nx >> 1));
+                        const int sl_hi = slot_of(64 * kb + 16 * gx + 8 + (nx >> 1));
+                        v2i b0[4], b1[4];
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            const int chunk = 4 * wave + j;
+                            b0[j] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i *)(vbase + tile_offset(sl_lo, chunk) + 8 * (nx & 1)));
+                            b1[j] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i *)(vbase + tile_offset(sl_hi, chunk) + 8 * (nx & 1)));
+                        }
+                        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            const v4i vb = {b0[j].x, b0[j].y, b1[j].x, b1[j].y};
+                            vacc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(pa, vb, vacc[j], 0, 0, 0);
+                        }
+                    }
+#pragma unroll
+                    for (int hh = 0; hh < 2; ++hh) {
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            float dots = (float)vacc[j][2 * hh];
+                            dots = dots + (float)vacc[j][2 * hh + 1] * (float)(1.0 / 127.0);
+                            const float sc = s.scale[kind][c0 + 16 * j + nx] * (float)(1.0 / 127.0);
+                            num[hh][j] = (kind ? num[hh][j] : 0.0f) + dots * sc;   // acc starts at 0
+                        }
+                    }
+                }
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) mx[hh] = mnew[hh];
+            } else
+            for (int i = 0; i < ntiles; ++i) {
+                const int k = part + S * (first + i);
+                const int kind = k >= m.t0 ? 1 : 0;
+                const int start = (k - (kind ? m.t0 : 0)) * N;
+                const int klen = kind ? m.list_len : m.ori_count;
+                const int buf = i & 1;
+                // Outstanding DMA: tile i, and tile 1 while tile 0 is awaited.
+                if (!DEBUG && i == 0 && ntiles > 1) vm_wait<DMA_PER_TILE>();
+                else vm_wait<0>();
+                lds_barrier();   // every wave's DMA of tile i has landed; every wave is done with tile i - 1
+                const bool stream_next = i >= 1 && i + 1 < ntiles;   // tiles 0 and 1 were issued up front
+                if (stream_next) issue_rows(i + 1, buf ^ 1, 0, DMA_STEP);
+                const int8_t *tb = s.tile[buf];
+                const int key = 16 * wave + nx;   // this lane's key in QK and softmax
+
+                // ---- QK: S[16 rows][16 keys of this wave] (reference.py:286-289) ----
+                v4i sacc = {0, 0, 0, 0};
+                {
+                    const int sl = slot_of(key);
+                    v4i b[8];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) b[j] = *reinterpret_cast<const v4i *>(tb + tile_offset(sl, 4 * j + gx));
+                    if (kind) {
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) sacc = __builtin_amdgcn_mfma_i32_16x16x64_i8(qa1[j], b[j], sacc, 0, 0, 0);
+                    } else {
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) sacc = __builtin_amdgcn_mfma_i32_16x16x64_i8(qa0[j], b[j], sacc, 0, 0, 0);
+                    }
+                }
+                if (stream_next) issue_rows(i + 1, buf ^ 1, DMA_STEP, DMA_STEP);
+                if (held) epilogue();            // the previous tile's, behind this tile's QK
+                const bool valid = s.code[i * N + key] >= 0;
+                float asc[2];
+                asc[0] = s.asc[kind][2 * gx];
+                asc[1] = s.asc[kind][2 * gx + 1];
+
+                // ---- logits, running max (reference.py:288-303) ----
+                float lg[2];
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    const int32_t hi = sacc[2 * hh], lo = sacc[2 * hh + 1];
+                    float dots = (float)hi;
+                    dots = dots + (float)lo * (float)(1.0 / 127.0);
+                    const float l = dots * asc[hh];
+                    lg[hh] = valid ? l : -1e30f;
+                    if (DEBUG && dbg.scores && start + key < klen) {
+                        // masked rows are zero rows in the reference (reference.py:283-286)
+                        int32_t *drow = reinterpret_cast<int32_t *>(dbg.scores) + ((int64_t)t * positions + (kind ? 128 : 0) + start + key) * 16;
+                        drow[2 * gx + hh] = valid ? hi : 0;
+                        drow[8 + 2 * gx + hh] = valid ? lo : 0;
+                    }
+                    const int tmax = row16_max_key(fkey(lg[hh]));
+                    if (nx == 0) s.redmax[2 * gx + hh][wave] = tmax;
+                }
+                lds_barrier();
+                if (stream_next) issue_rows(i + 1, buf ^ 1, 2 * DMA_STEP, DMA_STEP);
+                float mnew[2], factor[2];
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    const int h = 2 * gx + hh;
+                    const v4i a = *reinterpret_cast<const v4i *>(&s.redmax[h][0]);
+                    const v4i b = *reinterpret_cast<const v4i *>(&s.redmax[h][4]);
+                    const int k = max(max(max(fkey(mx[hh]), a.x), max(a.y, a.z)), max(max(a.w, b.x), max(max(b.y, b.z), b.w)));
+                    mnew[hh] = fkey_value(k);
+                }
+                {
+                    // One exponential per lane: even lanes take head 2g, odd lanes
+                    // head 2g+1; each lane gets the other head's factor from its
+                    // neighbour.
+                    const bool odd = nx & 1;
+                    const float mine = sk_expf_nonpos(odd ? mx[1] - mnew[1] : mx[0] - mnew[0]);
+                    const float other = dpp<DPP_XOR1>(mine);
+                    factor[0] = odd ? other : mine;
+                    factor[1] = odd ? mine : other;
+                }
+                // ---- weights, pairwise tile sum, P codes (reference.py:304-312) ----
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    const float w = sk_expf_nonpos(lg[hh] - mnew[hh]);
                     const float x = w * 127.0f;
                     const float ph = __builtin_rintf(x);
-                    const float pl = __builtin_rintf((x - ph) * 127.0f);
-                    pk[row_of(2 * gx + hh, 0) * PROW + key] = (int8_t)(int32_t)ph;
-                    pk[row_of(2 * gx + hh, 1) * PROW + key] = (int8_t)(int32_t)pl;
-                    const float wsum = row16_tree_sum(w);
-                    if (nx == 0) (kind ? s.redsum1 : s.redsum)[2 * gx + hh][wave] = wsum;
+                    const float pl = resid ? __builtin_rintf((x - ph) * 127.0f) : 0.0f;
+                    s.p[row_of(2 * gx + hh, 0) * PROW + key] = (int8_t)(int32_t)ph;
+                    s.p[row_of(2 * gx + hh, 1) * PROW + key] = (int8_t)(int32_t)pl;
+                    if (DEBUG && dbg.probs && start + key < klen) {
+                        int8_t *drow = reinterpret_cast<int8_t *>(dbg.probs) + ((int64_t)t * positions + (kind ? 128 : 0) + start + key) * 16;
+                        drow[2 * gx + hh] = (int8_t)(int32_t)ph;
+                        drow[8 + 2 * gx + hh] = (int8_t)(int32_t)pl;
+                    }
+                    const float wsum = row16_tree_sum(w);   // this wave's 16 keys
+                    if (nx == 0) s.redsum[2 * gx + hh][wave] = wsum;
                 }
-            }
-            lds_barrier();
-            // denominator = exp(sink - maximum) + (window tile's pairwise
-            // tree + compressed tile's); zero leaves past a kind's keys
-            // change neither tree.
+                lds_barrier();
+                if (stream_next) issue_rows(i + 1, buf ^ 1, 3 * DMA_STEP, DMA_STEP);
 #pragma unroll
-            for (int hh = 0; hh < 2; ++hh) {
-                const int h = 2 * gx + hh;
-                const f32x4 a0 = *reinterpret_cast<const f32x4 *>(&s.redsum[h][0]);
-                const f32x4 b0 = *reinterpret_cast<const f32x4 *>(&s.redsum[h][4]);
-                const f32x4 a1 = *reinterpret_cast<const f32x4 *>(&s.redsum1[h][0]);
-                const f32x4 b1 = *reinterpret_cast<const f32x4 *>(&s.redsum1[h][4]);
-                const float t0 = ((a0.x + a0.y) + (a0.z + a0.w)) + ((b0.x + b0.y) + (b0.z + b0.w));
-                const float t1 = ((a1.x + a1.y) + (a1.z + a1.w)) + ((b1.x + b1.y) + (b1.z + b1.w));
-                den[hh] = factor[hh] + (t0 + t1);
-            }
-            // PV per kind, each added to the output as it completes:
-            // output = sum over kinds of dot * (scale / 127) in kind order
-            // (reference.py:199-206).
-#pragma unroll
-            for (int kind = 0; kind < 2; ++kind) {
+                for (int hh = 0; hh < 2; ++hh) {
+                    // Pairwise over the eight 16-key blocks.
+                    const int h = 2 * gx + hh;
+                    const f32x4 a = *reinterpret_cast<const f32x4 *>(&s.redsum[h][0]);
+                    const f32x4 b = *reinterpret_cast<const f32x4 *>(&s.redsum[h][4]);
+                    const float tile_sum = ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w));
+                    den[hh] = den[hh] * factor[hh] + tile_sum;
+                }
+
+                // ---- PV: [16 rows][this wave's 64 columns] (reference.py:310-316) ----
                 v4i vacc[4];
 #pragma unroll
                 for (int j = 0; j < 4; ++j) vacc[j] = v4i{0, 0, 0, 0};
-                const lds_i8 *vbase = (const lds_i8 *)(s.tile[kind]);
+                const lds_i8 *vbase = (const lds_i8 *)(tb);   // generic -> LDS address space
 #pragma unroll
                 for (int kb = 0; kb < 2; ++kb) {
-                    const v4i pa = kind ? *reinterpret_cast<const v4i *>(p1 + nx * PROW + 64 * kb + 16 * gx)
-                                        : *reinterpret_cast<const v4i *>(s.p + nx * PROW + 64 * kb + 16 * gx);
+                    // A: P row nx, keys 64 kb + 16 gx .. + 15.  B: two transposed
+                    // 8-key reads; lanes 2r / 2r+1 address the two 8-column halves
+                    // of key row r, lane nx receives column nx of the 16-column block.
+                    const v4i pa = *reinterpret_cast<const v4i *>(s.p + nx * PROW + 64 * kb + 16 * gx);
                     const int sl_lo = slot_of(64 * kb + 16 * gx + (nx >> 1));
                     const int sl_hi = slot_of(64 * kb + 16 * gx + 8 + (nx >> 1));
                     v2i b0[4], b1[4];
@@ -1132,236 +1304,128 @@ c8_attention(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base
                         b0[j] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i *)(vbase + tile_offset(sl_lo, chunk) + 8 * (nx & 1)));
                         b1[j] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i *)(vbase + tile_offset(sl_hi, chunk) + 8 * (nx & 1)));
                     }
-                    __builtin_amdgcn_sched_barrier(0);
+                    __builtin_amdgcn_sched_barrier(0);   // all reads in flight before the first MFMA waits
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
                         const v4i vb = {b0[j].x, b0[j].y, b1[j].x, b1[j].y};
                         vacc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(pa, vb, vacc[j], 0, 0, 0);
                     }
                 }
+                if (DEBUG && dbg.values && k < (int)dbg.tileCapacity) {
+                    int32_t *vout = reinterpret_cast<int32_t *>(dbg.values) + ((int64_t)t * dbg.tileCapacity + k) * 16 * D;
 #pragma unroll
-                for (int hh = 0; hh < 2; ++hh) {
+                    for (int j = 0; j < 4; ++j)
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        float dots = (float)vacc[j][2 * hh];
-                        dots = dots + (float)vacc[j][2 * hh + 1] * (float)(1.0 / 127.0);
-                        const float sc = s.scale[kind][c0 + 16 * j + nx] * (float)(1.0 / 127.0);
-                        num[hh][j] = (kind ? num[hh][j] : 0.0f) + dots * sc;   // acc starts at 0
-                    }
+                        for (int hh = 0; hh < 2; ++hh) {
+                            vout[(2 * gx + hh) * D + c0 + 16 * j + nx] = vacc[j][2 * hh];
+                            vout[(8 + 2 * gx + hh) * D + c0 + 16 * j + nx] = vacc[j][2 * hh + 1];
+                        }
                 }
-            }
-#pragma unroll
-            for (int hh = 0; hh < 2; ++hh) mx[hh] = mnew[hh];
-        } else
-        for (int i = 0; i < ntiles; ++i) {
-            const int k = part + S * (first + i);
-            const int kind = k >= m.t0 ? 1 : 0;
-            const int start = (k - (kind ? m.t0 : 0)) * N;
-            const int klen = kind ? m.list_len : m.ori_count;
-            const int buf = i & 1;
-            // Outstanding DMA: tile i, and tile 1 while tile 0 is awaited.
-            if (!DEBUG && i == 0 && ntiles > 1) vm_wait<DMA_PER_TILE>();
-            else vm_wait<0>();
-            lds_barrier();   // every wave's DMA of tile i has landed; every wave is done with tile i - 1
-            const bool stream_next = i >= 1 && i + 1 < ntiles;   // tiles 0 and 1 were issued up front
-            if (stream_next) issue_rows(i + 1, buf ^ 1, 0, DMA_STEP);
-            const int8_t *tb = s.tile[buf];
-            const int key = 16 * wave + nx;   // this lane's key in QK and softmax
-
-            // ---- QK: S[16 rows][16 keys of this wave] (reference.py:286-289) ----
-            v4i sacc = {0, 0, 0, 0};
-            {
-                const int sl = slot_of(key);
-                v4i b[8];
-#pragma unroll
-                for (int j = 0; j < 8; ++j) b[j] = *reinterpret_cast<const v4i *>(tb + tile_offset(sl, 4 * j + gx));
-                if (kind) {
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) sacc = __builtin_amdgcn_mfma_i32_16x16x64_i8(qa1[j], b[j], sacc, 0, 0, 0);
-                } else {
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) sacc = __builtin_amdgcn_mfma_i32_16x16x64_i8(qa0[j], b[j], sacc, 0, 0, 0);
-                }
-            }
-            if (stream_next) issue_rows(i + 1, buf ^ 1, DMA_STEP, DMA_STEP);
-            if (held) epilogue();            // the previous tile's, behind this tile's QK
-            const bool valid = s.code[i * N + key] >= 0;
-            float asc[2];
-            asc[0] = s.asc[kind][2 * gx];
-            asc[1] = s.asc[kind][2 * gx + 1];
-
-            // ---- logits, running max (reference.py:288-303) ----
-            float lg[2];
-#pragma unroll
-            for (int hh = 0; hh < 2; ++hh) {
-                const int32_t hi = sacc[2 * hh], lo = sacc[2 * hh + 1];
-                float dots = (float)hi;
-                dots = dots + (float)lo * (float)(1.0 / 127.0);
-                const float l = dots * asc[hh];
-                lg[hh] = valid ? l : -1e30f;
-                if (DEBUG && dbg.scores && start + key < klen) {
-                    // masked rows are zero rows in the reference (reference.py:283-286)
-                    int32_t *drow = reinterpret_cast<int32_t *>(dbg.scores) + ((int64_t)t * positions + (kind ? 128 : 0) + start + key) * 16;
-                    drow[2 * gx + hh] = valid ? hi : 0;
-                    drow[8 + 2 * gx + hh] = valid ? lo : 0;
-                }
-                const int tmax = row16_max_key(fkey(lg[hh]));
-                if (nx == 0) s.redmax[2 * gx + hh][wave] = tmax;
-            }
-            lds_barrier();
-            if (stream_next) issue_rows(i + 1, buf ^ 1, 2 * DMA_STEP, DMA_STEP);
-            float mnew[2], factor[2];
-#pragma unroll
-            for (int hh = 0; hh < 2; ++hh) {
-                const int h = 2 * gx + hh;
-                const v4i a = *reinterpret_cast<const v4i *>(&s.redmax[h][0]);
-                const v4i b = *reinterpret_cast<const v4i *>(&s.redmax[h][4]);
-                const int k = max(max(max(fkey(mx[hh]), a.x), max(a.y, a.z)), max(max(a.w, b.x), max(max(b.y, b.z), b.w)));
-                mnew[hh] = fkey_value(k);
-            }
-            {
-                // One exponential per lane: even lanes take head 2g, odd lanes
-                // head 2g+1; each lane gets the other head's factor from its
-                // neighbour.
-                const bool odd = nx & 1;
-                const float mine = sk_expf_nonpos(odd ? mx[1] - mnew[1] : mx[0] - mnew[0]);
-                const float other = dpp<DPP_XOR1>(mine);
-                factor[0] = odd ? other : mine;
-                factor[1] = odd ? mine : other;
-            }
-            // ---- weights, pairwise tile sum, P codes (reference.py:304-312) ----
-#pragma unroll
-            for (int hh = 0; hh < 2; ++hh) {
-                const float w = sk_expf_nonpos(lg[hh] - mnew[hh]);
-                const float x = w * 127.0f;
-                const float ph = __builtin_rintf(x);
-                const float pl = resid ? __builtin_rintf((x - ph) * 127.0f) : 0.0f;
-                s.p[row_of(2 * gx + hh, 0) * PROW + key] = (int8_t)(int32_t)ph;
-                s.p[row_of(2 * gx + hh, 1) * PROW + key] = (int8_t)(int32_t)pl;
-                if (DEBUG && dbg.probs && start + key < klen) {
-                    int8_t *drow = reinterpret_cast<int8_t *>(dbg.probs) + ((int64_t)t * positions + (kind ? 128 : 0) + start + key) * 16;
-                    drow[2 * gx + hh] = (int8_t)(int32_t)ph;
-                    drow[8 + 2 * gx + hh] = (int8_t)(int32_t)pl;
-                }
-                const float wsum = row16_tree_sum(w);   // this wave's 16 keys
-                if (nx == 0) s.redsum[2 * gx + hh][wave] = wsum;
-            }
-            lds_barrier();
-            if (stream_next) issue_rows(i + 1, buf ^ 1, 3 * DMA_STEP, DMA_STEP);
-#pragma unroll
-            for (int hh = 0; hh < 2; ++hh) {
-                // Pairwise over the eight 16-key blocks.
-                const int h = 2 * gx + hh;
-                const f32x4 a = *reinterpret_cast<const f32x4 *>(&s.redsum[h][0]);
-                const f32x4 b = *reinterpret_cast<const f32x4 *>(&s.redsum[h][4]);
-                const float tile_sum = ((a.x + a.y) + (a.z + a.w)) + ((b.x + b.y) + (b.z + b.w));
-                den[hh] = den[hh] * factor[hh] + tile_sum;
-            }
-
-            // ---- PV: [16 rows][this wave's 64 columns] (reference.py:310-316) ----
-            v4i vacc[4];
-#pragma unroll
-            for (int j = 0; j < 4; ++j) vacc[j] = v4i{0, 0, 0, 0};
-            const lds_i8 *vbase = (const lds_i8 *)(tb);   // generic -> LDS address space
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
-                // A: P row nx, keys 64 kb + 16 gx .. + 15.  B: two transposed
-                // 8-key reads; lanes 2r / 2r+1 address the two 8-column halves
-                // of key row r, lane nx receives column nx of the 16-column block.
-                const v4i pa = *reinterpret_cast<const v4i *>(s.p + nx * PROW + 64 * kb + 16 * gx);
-                const int sl_lo = slot_of(64 * kb + 16 * gx + (nx >> 1));
-                const int sl_hi = slot_of(64 * kb + 16 * gx + 8 + (nx >> 1));
-                v2i b0[4], b1[4];
+                // The FP32 epilogue of this tile runs in the next tile's body,
+                // after its QK is issued, so its VALU work overlaps that tile's
+                // LDS reads and MFMAs (or after the last tile).
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    const int chunk = 4 * wave + j;
-                    b0[j] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i *)(vbase + tile_offset(sl_lo, chunk) + 8 * (nx & 1)));
-                    b1[j] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i *)(vbase + tile_offset(sl_hi, chunk) + 8 * (nx & 1)));
+                    held_acc[j] = vacc[j];
+                    held_sc[j] = s.scale[kind][c0 + 16 * j + nx];
                 }
-                __builtin_amdgcn_sched_barrier(0);   // all reads in flight before the first MFMA waits
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const v4i vb = {b0[j].x, b0[j].y, b1[j].x, b1[j].y};
-                    vacc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(pa, vb, vacc[j], 0, 0, 0);
-                }
+                held_factor[0] = factor[0];
+                held_factor[1] = factor[1];
+                held = true;
+                mx[0] = mnew[0];
+                mx[1] = mnew[1];
             }
-            if (DEBUG && dbg.values && k < (int)dbg.tileCapacity) {
-                int32_t *vout = reinterpret_cast<int32_t *>(dbg.values) + ((int64_t)t * dbg.tileCapacity + k) * 16 * D;
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-#pragma unroll
-                    for (int hh = 0; hh < 2; ++hh) {
-                        vout[(2 * gx + hh) * D + c0 + 16 * j + nx] = vacc[j][2 * hh];
-                        vout[(8 + 2 * gx + hh) * D + c0 + 16 * j + nx] = vacc[j][2 * hh + 1];
-                    }
-            }
-            // The FP32 epilogue of this tile runs in the next tile's body,
-            // after its QK is issued, so its VALU work overlaps that tile's
-            // LDS reads and MFMAs (or after the last tile).
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                held_acc[j] = vacc[j];
-                held_sc[j] = s.scale[kind][c0 + 16 * j + nx];
-            }
-            held_factor[0] = factor[0];
-            held_factor[1] = factor[1];
-            held = true;
-            mx[0] = mnew[0];
-            mx[1] = mnew[1];
+            if (first + CODE_TILES < my_tiles) __syncthreads();   // s.code and the tile buffers are rebuilt next
         }
-        if (first + CODE_TILES < my_tiles) __syncthreads();   // s.code and the tile buffers are rebuilt next
-    }
-    if (held) epilogue();
+        if (held) epilogue();
 
-    if (folded == 1) {
-        // ---- finalize (reference.py:317-323 with one partition) ----
+        if (folded == 1) {
+            // ---- finalize (reference.py:317-323 with one partition) ----
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                const int h = 2 * g + hh;
+                if (ANYH && h >= hlive) continue;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) out_row[h * D + c0 + 16 * j + n] = (uint16_t)pack_bf16(num[hh][j] / den[hh], 0.0f);
+                if (lse_row && wave == 0 && n == 0) lse_row[h] = mx[hh] + logf(den[hh]);
+            }
+            if (S > 1 && !fused && tid == 0)
+                reinterpret_cast<float *>(p.partial)[(int64_t)qrow * S * HEADS * PART_FLOATS + FOLD_SLOT] = 0.0f;
+            return;
+        }
+
+        // ---- publish this partition: [num 512, max, den] per head ----
+        float *row_partial = reinterpret_cast<float *>(p.partial) + (int64_t)qrow * S * HEADS * PART_FLOATS;
+        const __amdgpu_buffer_rsrc_t states = row_states(row_partial);
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
             const int h = 2 * g + hh;
-            if (ANYH && h >= hlive) continue;
+            const int base = ((part * HEADS + h) * PART_FLOATS) * 4;   // byte offset in the row's states
 #pragma unroll
-            for (int j = 0; j < 4; ++j) out_row[h * D + c0 + 16 * j + n] = (uint16_t)pack_bf16(num[hh][j] / den[hh], 0.0f);
-            if (lse_row && wave == 0 && n == 0) lse_row[h] = mx[hh] + logf(den[hh]);
+            for (int j = 0; j < 4; ++j)
+                state_store<SC1>(num[hh][j], states, base + (c0 + 16 * j + n) * 4);
+            if (wave == 0 && n == 0) {
+                state_store<SC1>(mx[hh], states, base + 512 * 4);
+                state_store<SC1>(den[hh], states, base + 513 * 4);
+            }
         }
-        if (S > 1 && !fused && tid == 0)
-            reinterpret_cast<float *>(p.partial)[(int64_t)qrow * S * HEADS * PART_FLOATS + FOLD_SLOT] = 0.0f;
-        return;
-    }
-
-    // ---- publish this partition: [num 512, max, den] per head ----
-    float *row_partial = reinterpret_cast<float *>(p.partial) + (int64_t)qrow * S * HEADS * PART_FLOATS;
-    const __amdgpu_buffer_rsrc_t states = row_states(row_partial);
-#pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-        const int h = 2 * g + hh;
-        const int base = ((part * HEADS + h) * PART_FLOATS) * 4;   // byte offset in the row's states
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-            state_store<SC1>(num[hh][j], states, base + (c0 + 16 * j + n) * 4);
-        if (wave == 0 && n == 0) {
-            state_store<SC1>(mx[hh], states, base + 512 * 4);
-            state_store<SC1>(den[hh], states, base + 513 * 4);
+        if (!fused) {
+            if (part == 0 && tid == 0) state_store<SC1>((float)folded, states, FOLD_SLOT * 4);
+            return;
         }
-    }
-    if (!fused) {
-        if (part == 0 && tid == 0) state_store<SC1>((float)folded, states, FOLD_SLOT * 4);
-        return;
-    }
 
-    // ---- the last partition of the row to finish folds all of them ----
-    // Every state store above has completed (vmcnt 0) before the ticket is
-    // taken; the partition that takes the last ticket reads the states back
-    // with device-coherent (sc1) loads.
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    uint32_t *tickets = reinterpret_cast<uint32_t *>(p.workspace);
-    if (tid == 0) s.misc[5] = (int)__hip_atomic_fetch_add(&tickets[qrow], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __syncthreads();
-    if (s.misc[5] != folded - 1) return;
-    if (tid == 0) __hip_atomic_store(&tickets[qrow], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-    fold_row<SC1>(states, folded, tid, out_row, lse_row, ANYH ? hlive : HEADS);
+        // ---- the last partition of the row to finish folds all of them ----
+        // Every state store above has completed (vmcnt 0) before the ticket is
+        // taken; the partition that takes the last ticket reads the states back
+        // with device-coherent (sc1) loads.
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        uint32_t *tickets = reinterpret_cast<uint32_t *>(p.workspace);
+        if (tid == 0) s.misc[5] = (int)__hip_atomic_fetch_add(&tickets[qrow], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        if (s.misc[5] != folded - 1) return;
+        if (tid == 0) __hip_atomic_store(&tickets[qrow], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        fold_row<SC1>(states, folded, tid, out_row, lse_row, ANYH ? hlive : HEADS);
+    };
+    for (;;) {
+        if (PERSIST) {
+            // Lane coordinates from an opaque copy of the thread index, so
+            // the compiler derives the row's lane addresses inside the row
+            // loop instead of holding them across rows.
+            asm volatile("" : "+v"(tid));
+            lane = tid & 63;
+            wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+            g = lane >> 4;
+            n = lane & 15;
+        }
+        run_row();
+        if (!PERSIST) return;
+        qrow += (int32_t)G;
+        if (qrow >= (int32_t)rows_arg) return;
+        t = ANYH ? qrow / HG : qrow;
+        hbase = ANYH ? HEADS * (qrow % HG) : 0;
+        hlive = ANYH ? (H - hbase < HEADS ? H - hbase : HEADS) : HEADS;
+        if (prefetched) {
+            qv = qv_next;
+            ix[0] = ix_next[0];
+            ix[1] = ix_next[1];
+        } else {
+            qv = v4i{0, 0, 0, 0};
+            if (!ANYH || wave < hlive) qv = *gptr<v4i>(q_base + (((uint64_t)t * H + hbase + wave) * D + qd0) * 2);
+            if (RATIO == 4) {
+                const int topk = (int)topk_arg;
+                const __attribute__((address_space(1))) int32_t *row_ix = gptr<int32_t>(cmp_indices) + (int64_t)t * topk;
+#pragma unroll
+                for (int i = 0; i < 2; ++i) ix[i] = tid * 2 + i < topk ? row_ix[tid * 2 + i] : -1;
+            }
+        }
+        prefetched = false;
+        if (tid == 0) s.misc[1] = -1;
+        __syncthreads();                  // also: every wave is done with the previous row's tiles
+        find_request(t, false);
+    }
 }
 
 // Partition merge as a second launch (merge mode 1): one 512-thread group
@@ -1477,20 +1541,32 @@ void launch_variant(hipStream_t stream, const SharedKVArgs *a, const SharedKVDeb
     // sequence (C4 joint rows cost the tiled C4 path about 3 % where they
     // are compiled in, so only such launches get them).
     const bool joint4 = !DEBUG && !slots && a->heads <= HEADS && (uint64_t)a->cmpTableWidth * BLOCK_ROWS <= (uint64_t)N;
-    auto kernel = slots ? &c8_attention<1, DEBUG, true, ANYH, false, false> : &c8_attention<1, DEBUG, false, ANYH, false, false>;
-    if (a->ratio == 4 && joint4)
-        kernel = streamed ? &c8_attention<4, DEBUG, false, ANYH, !DEBUG, !DEBUG>
-                          : &c8_attention<4, DEBUG, false, ANYH, false, !DEBUG>;
-    else if (a->ratio == 4)
-        kernel = slots ? (streamed ? &c8_attention<4, DEBUG, true, ANYH, !DEBUG, false>
-                                   : &c8_attention<4, DEBUG, true, ANYH, false, false>)
-                       : (streamed ? &c8_attention<4, DEBUG, false, ANYH, !DEBUG, false>
-                                   : &c8_attention<4, DEBUG, false, ANYH, false, false>);
-    else if (a->ratio == 128)
-        kernel = slots ? (streamed ? &c8_attention<128, DEBUG, true, ANYH, !DEBUG, true>
-                                   : &c8_attention<128, DEBUG, true, ANYH, false, true>)
-                       : (streamed ? &c8_attention<128, DEBUG, false, ANYH, !DEBUG, true>
-                                   : &c8_attention<128, DEBUG, false, ANYH, false, true>);
+    // One-partition C4 launches of more rows than CUs (prefill) run
+    // persistent work-groups (PERSIST: one per CU, each taking rows in turn).
+    // The C128 and window-only kernels would spill in the row loop.
+    const bool persist = !DEBUG && !slots && a->ratio == 4 && !joint4 && splits == 1 && rows > (uint32_t)PLAN_CUS;
+    decltype(&c8_attention<1, false, false, ANYH, false, false, false>) kernel;
+    if (persist) {
+        grid = (uint32_t)PLAN_CUS;
+        kernel = streamed ? &c8_attention<4, false, false, ANYH, true, false, true>
+                          : &c8_attention<4, false, false, ANYH, false, false, true>;
+    } else {
+        kernel = slots ? &c8_attention<1, DEBUG, true, ANYH, false, false, false>
+                       : &c8_attention<1, DEBUG, false, ANYH, false, false, false>;
+        if (a->ratio == 4 && joint4)
+            kernel = streamed ? &c8_attention<4, DEBUG, false, ANYH, !DEBUG, !DEBUG, false>
+                              : &c8_attention<4, DEBUG, false, ANYH, false, !DEBUG, false>;
+        else if (a->ratio == 4)
+            kernel = slots ? (streamed ? &c8_attention<4, DEBUG, true, ANYH, !DEBUG, false, false>
+                                       : &c8_attention<4, DEBUG, true, ANYH, false, false, false>)
+                           : (streamed ? &c8_attention<4, DEBUG, false, ANYH, !DEBUG, false, false>
+                                       : &c8_attention<4, DEBUG, false, ANYH, false, false, false>);
+        else if (a->ratio == 128)
+            kernel = slots ? (streamed ? &c8_attention<128, DEBUG, true, ANYH, !DEBUG, true, false>
+                                       : &c8_attention<128, DEBUG, true, ANYH, false, true, false>)
+                           : (streamed ? &c8_attention<128, DEBUG, false, ANYH, !DEBUG, true, false>
+                                       : &c8_attention<128, DEBUG, false, ANYH, false, true, false>);
+    }
     // The leading scalar arguments are the ones the first loads need; the
     // build preloads them into SGPRs (-amdgpu-kernarg-preload-count), so
     // those loads do not wait for a read of the argument block.

@@ -272,6 +272,37 @@ def test_joint_c4_rows(mode, heads):
         compare(long_case, out, lse, splits, tag=f"{mode} with a long row, splits {splits}")
 
 
+@pytest.mark.parametrize("heads", [8, 12])
+def test_persistent_rows(heads):
+    """One-partition C4 launches of more rows than CUs run persistent
+    work-groups (one per CU, each taking rows in turn, the next row's Q and
+    indices loaded ahead): bit-exact with the checker.  The launch mixes a
+    long request, short ones, a request listing more query tokens than its
+    sequence length (a keyless row, which ends early and loads nothing
+    ahead) and graph-padding rows; twelve heads make two rows per token."""
+    case = workloads.make_case(81, 4, [290, 5, 2], [3000, 40, 1], heads=heads, index_mode="holes")
+    pad = 12
+    live = int(case["cu_q"][-1])
+    case["q"] = np.concatenate([case["q"], np.full((pad, heads, 512), 0x7FC0, np.uint16)])
+    case["cu_q"] = np.concatenate([case["cu_q"], [live + pad]]).astype(np.int32)
+    case["seq_lens"] = np.concatenate([case["seq_lens"], [0]]).astype(np.int32)
+    case["ori"].table = np.concatenate([case["ori"].table, case["ori"].table[:1]])
+    case["cmp"].table = np.concatenate([case["cmp"].table, case["cmp"].table[:1]])
+    case["cmp_indices"] = np.concatenate([case["cmp_indices"], np.full((pad, 1, 1024), -1, np.int32)])
+    say(f"[persistent] heads {heads}: {(live + pad) * ((heads + 7) // 8)} rows")
+    out, lse, op = run_hip(case, splits=1)
+    assert op.splits == 1 and op.device_splits() == 1
+    assert not out[live:].any() and not lse[live:].any(), "padding rows are not zero"
+    keyless = live - 2                                   # position -1
+    assert not out[keyless].any() and not lse[keyless].any()
+    # The checker rejects the keyless row's request (reference.py:104-105):
+    # every other live row is checked as its own one-token request.
+    live_case = dict(case, q=case["q"][:live], cu_q=case["cu_q"][:-1], seq_lens=case["seq_lens"][:-1],
+                     cmp_indices=case["cmp_indices"][:live])
+    rows = [r for r in range(live) if r != keyless]
+    compare(live_case, out[:live], lse[:live], 1, rows=rows, tag=f"persistent heads {heads}")
+
+
 @pytest.mark.parametrize("name", GOLDEN_NAMES)
 def test_against_reference_vectors(name):
     """HIP output vs reference.py's own tiled_quantized_reference output on
