@@ -275,12 +275,14 @@ def test_joint_c4_rows(mode, heads):
 @pytest.mark.parametrize("heads", [8, 12])
 def test_persistent_rows(heads):
     """One-partition C4 launches of more rows than CUs run persistent
-    work-groups (one per CU, each taking rows in turn, the next row's Q and
-    indices loaded ahead): bit-exact with the checker.  The launch mixes a
-    long request, short ones, a request listing more query tokens than its
-    sequence length (a keyless row, which ends early and loads nothing
-    ahead) and graph-padding rows; twelve heads make two rows per token."""
-    case = workloads.make_case(81, 4, [290, 5, 2], [3000, 40, 1], heads=heads, index_mode="holes")
+    work-groups (one per CU, each taking up to three rows here in turn, the
+    next row's Q and indices loaded ahead): bit-exact with the checker.  The
+    launch mixes a long request, short ones, a request listing more query
+    tokens than its sequence length (a keyless row, which ends early and
+    loads nothing ahead) and graph-padding rows, so work-groups pass between
+    rows with and without the loads ahead; twelve heads make two rows per
+    token."""
+    case = workloads.make_case(81, 4, [600, 5, 2], [3000, 40, 1], heads=heads, index_mode="holes")
     pad = 12
     live = int(case["cu_q"][-1])
     case["q"] = np.concatenate([case["q"], np.full((pad, heads, 512), 0x7FC0, np.uint16)])
