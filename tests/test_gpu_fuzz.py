@@ -1,6 +1,7 @@
 """Seeded random launches against the CPU checker: mixed ratios, head counts,
 explicit original slots, C4 index modes, short contexts (joint rows),
-graph-capacity padding rows, KV partitions (1-8) and both merge placements,
+prefill-like chunks of 260-400 tokens (persistent work-groups), graph-capacity
+padding rows, KV partitions (1-8) and both merge placements,
 all bit-exact (BF16 outputs) with the checker on the launch's own plan and LSE
 within 2e-6."""
 import os
@@ -29,11 +30,21 @@ def random_case(seed):
     # One launch in five is short-context (joint rows for C4 and C128).
     longest = 516 if rng.random() < 0.2 else 9000
     lengths = [int(max(q, rng.integers(1, longest))) for q in queries]
+    prefill = rng.random() < 0.08
+    if prefill:
+        # Prefill-like: one long chunk of 260-400 query tokens (a
+        # one-partition eight-head C4 launch of it runs persistent work-groups).
+        queries[0] = int(rng.integers(260, 401))
+        lengths[0] = int(queries[0] + rng.integers(0, 2500))
     heads = int(rng.choice([8, 8, 8, 4, 12, 16]))
+    if prefill and rng.random() < 0.75:
+        heads = 8
     mode = str(rng.choice(["uniform", "holes", "dups", "mixed"] + list(workloads.EDGE_MODES)))
-    slots = rng.random() < 0.25
+    slots = rng.random() < 0.25 and not prefill      # a draft's slots cover at most 384 rows
     slot_mode = str(rng.choice(["draft", "shuffled", "pool"])) if slots else None
     splits = rng.choice([None, 1, 2, 3, 4, 5, 6, 8])
+    if prefill and rng.random() < 0.6:
+        splits = None                                 # the host plan: one partition
     merge = int(rng.integers(0, 2))
     topk = int(rng.choice([1024, 512, 256]))
     need = max(q + 128 for q in queries) if slot_mode in ("draft", "shuffled") else 0
