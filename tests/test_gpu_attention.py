@@ -725,6 +725,57 @@ def test_one_graph_across_live_batch_and_length_states(ratio):
     del graph
 
 
+def test_persistent_graph_across_live_states():
+    """A one-partition C4 launch of more rows than CUs (persistent
+    work-groups) captured at a capacity of 4 requests x 100 query tokens and
+    replayed twice per live state while the live batch and lengths change
+    (4, 2, 1, 0 and 3 live requests).  Outputs and LSE are poisoned with NaN
+    before each state; padding rows must come back zero and live rows
+    bit-exact with the checker."""
+    import torch
+    from npu_sparse_attn_sharedkv_int8 import PreparedAttention
+    full = workloads.make_case(91, 4, [100] * 4, [1600] * 4, index_mode="holes")
+    dev, oscale, cscale, keep = to_device(full)
+    op = PreparedAttention(dev, oscale, cscale, return_lse=True)
+    assert op.splits == 1
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        op.run()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            op.run()
+    torch.cuda.current_stream().wait_stream(stream)
+    states = [(4, [1600] * 4), (2, [1200, 1599]), (1, [101]), (0, []), (3, [1600, 350, 999])]
+    for batch, lengths in states:
+        cu = np.array([min(100 * b, 100 * batch) for b in range(5)], np.int32)
+        lens = np.array(lengths + [0] * (4 - batch), np.int32)
+        q = full["q"].copy()
+        q[100 * batch:] = 0x7FC0
+        dev.q.copy_(torch_bf16(q, "cuda"))
+        dev.cu_q.copy_(torch.from_numpy(cu))
+        dev.seq_lens.copy_(torch.from_numpy(lens))
+        op.out.fill_(float("nan"))
+        op.lse.fill_(float("nan"))
+        torch.cuda.synchronize()
+        say(f"[persistent graph] {batch} live, lengths {lengths}")
+        for _ in range(2):
+            graph.replay()
+        torch.cuda.synchronize()
+        out, lse = bits_of(op.out), op.lse.cpu().numpy()
+        live = 100 * batch
+        assert not out[live:].any() and not lse[live:].any(), "padding rows are not zero"
+        if not batch:
+            continue
+        sub = dict(full, q=q[:live], cu_q=cu[:batch + 1], seq_lens=lens[:batch])
+        ref, ref_lse, _ = run_oracle(sub, 1)
+        diff = out[:live] != ref
+        assert not diff.any(), f"{batch} live: {int(diff.sum())} BF16 mismatches"
+        np.testing.assert_allclose(lse[:live], ref_lse, rtol=0, atol=2e-6)
+    del graph
+
+
 @pytest.mark.parametrize("ratio", [1, 4, 128])
 def test_queued_launches_with_rapid_rebinding(ratio):
     """Flow of the reference's tests/npu/test_queue.py:17-60: per stream (the
