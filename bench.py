@@ -73,7 +73,19 @@ def workload(name, rng):
 
 
 WORKLOADS = ["headline", "cfg0", "cfg1", "cfg2_c4", "cfg2_c128", "cfg3_prefill", "cfg4_c4", "cfg4_c128", "c128",
-             "cfg4_writer"]
+             "cfg4_writer", "custom"]
+
+
+def custom_workload(args, rng):
+    """A decode or prefill shape outside the BASELINE configs (--workload
+    custom): --batch sequences of --query-tokens each, lengths uniform in
+    --ctx LO:HI, ratio --ratio, at the serving page stride."""
+    lo, hi = (int(x) for x in args.ctx.split(":"))
+    if not args.query_tokens <= lo <= hi:
+        raise SystemExit("--ctx LO:HI needs query-tokens <= LO <= HI")
+    lengths = rng.integers(lo, hi + 1, args.batch)
+    return (20, args.ratio, [args.query_tokens] * args.batch, lengths, SERVING_STRIDE,
+            f"custom: C{args.ratio}, B={args.batch} x T={args.query_tokens}, ctx~U[{lo},{hi}]")
 
 
 def copy_calibration(mib, torch):
@@ -275,6 +287,10 @@ def main():
     ap.add_argument("--live", type=int, default=None, metavar="SEQS",
                     help="also replay the captured graph with only SEQS sequences live (graph padding; the "
                          "kernel re-plans partitions on the device); default 8 for the headline, 0 = skip")
+    ap.add_argument("--ratio", type=int, default=4, choices=[1, 4, 128], help="custom workload: cache ratio")
+    ap.add_argument("--batch", type=int, default=32, help="custom workload: sequences")
+    ap.add_argument("--query-tokens", type=int, default=2, help="custom workload: query tokens per sequence")
+    ap.add_argument("--ctx", default="2048:65536", help="custom workload: sequence lengths LO:HI (uniform)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="also run a plain device copy of MIB MiB four times (the reference kernel "
                          "for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
@@ -299,7 +315,8 @@ def main():
     if library().sharedkv_c8_set_merge_mode(args.merge):
         raise SystemExit(f"unknown merge mode {args.merge}")
     rng = np.random.default_rng(2026)
-    seed, ratio, queries, lengths, stride, description = workload(args.workload, rng)
+    seed, ratio, queries, lengths, stride, description = (
+        custom_workload(args, rng) if args.workload == "custom" else workload(args.workload, rng))
     stride = args.page_stride or stride
     layers = max(1, min(args.layers, stride // 16384))
     log(f"[bench] generating {description}; {layers} layers at page stride {stride}")
