@@ -107,7 +107,11 @@ class PreparedAttention:
         # build's numerics (tile_size, splits) are honoured; the rest are
         # validated for type and recorded.  adaptive_splits has nothing left
         # to switch: the kernel always adapts the partition count to the live
-        # rows of a padded launch (c8_attention.device_splits).
+        # rows of a padded launch (c8_attention.device_splits).  query_group
+        # is validated and not applied: every query row runs its own key list,
+        # and self.query_group = 1 tells callers which plan ran (the
+        # reference's tests rebuild their oracle plan from tile_size,
+        # query_group and splits).
         if tile_size is not None and tile_size != c8_attention.TILE:
             raise ValueError(f"This build tiles keys in groups of {c8_attention.TILE}; tile_size must be None or "
                              f"{c8_attention.TILE}")

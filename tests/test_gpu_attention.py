@@ -915,6 +915,30 @@ def test_empty_launch_is_a_no_op():
     torch.cuda.synchronize()
 
 
+def test_planner_knobs_report_the_plan_that_ran():
+    """The Ascend planner's knobs (attention.py:27-30 of the reference) are
+    validated; query_group and the planner switches are not applied, and the
+    operator reports the plan that ran (tile_size, query_group, splits), the
+    fields the reference's tests rebuild their oracle plan from."""
+    import torch
+    from npu_sparse_attn_sharedkv_int8 import PreparedAttention
+    case = workloads.make_case(27, 4, [2, 2], [700, 3000], index_mode="uniform")
+    dev, oscale, cscale, keep = to_device(case)
+    plain = PreparedAttention(dev, oscale, cscale, return_lse=True)
+    plain.run()
+    for kw in ({"query_group": 2}, {"query_group": 4, "max_seq_len": 1024}, {"adaptive_splits": True},
+               {"trim_cube_tails": True, "dynamic_c4": True}):
+        op = PreparedAttention(dev, oscale, cscale, return_lse=True, **kw)
+        assert (op.tile_size, op.query_group, op.splits) == (128, 1, plain.splits), kw
+        op.run()
+        torch.cuda.synchronize()
+        assert torch.equal(op.out, plain.out) and torch.equal(op.lse, plain.lse), kw
+    for kw in ({"query_group": 3}, {"tile_size": 256}, {"splits": 0}):
+        with pytest.raises(ValueError):
+            PreparedAttention(dev, oscale, cscale, **kw)
+    compare(case, bits_of(plain.out), plain.lse.cpu().numpy(), plain.splits, tag="knobs")
+
+
 @pytest.mark.parametrize("mode", [0, 1])
 def test_merge_modes_match_checker(mode):
     """Partition states folded by the last partition of each row (mode 0,
