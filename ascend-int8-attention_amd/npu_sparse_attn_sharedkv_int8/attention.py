@@ -109,9 +109,10 @@ class PreparedAttention:
         # to switch: the kernel always adapts the partition count to the live
         # rows of a padded launch (c8_attention.device_splits).  query_group
         # is validated and not applied: every query row runs its own key list,
-        # and self.query_group = 1 tells callers which plan ran (the
-        # reference's tests rebuild their oracle plan from tile_size,
-        # query_group and splits).
+        # and self.query_group = 1 tells callers which plan ran.  The
+        # reference's C8 path likewise runs its kernel's own plan whatever
+        # query_group asks (c8_attention.py:74-113; its tests rebuild the
+        # oracle plan from the device's choice, attention_cases.py:56-111).
         if tile_size is not None and tile_size != c8_attention.TILE:
             raise ValueError(f"This build tiles keys in groups of {c8_attention.TILE}; tile_size must be None or "
                              f"{c8_attention.TILE}")
