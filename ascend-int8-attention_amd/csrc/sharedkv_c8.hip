@@ -1448,6 +1448,408 @@ c8_merge(const SharedKVArgs p, uint32_t splits)
                 H - hbase < HEADS ? H - hbase : HEADS);
 }
 
+// ---- c8_rows: one-partition C4 launches of many query rows (prefill) ----
+// The same numerics as c8_attention with one partition (128-key tiles,
+// reference.py:210-323), laid out so that two work-groups share a CU: four
+// waves and one tile buffer each (80 KiB of LDS), each work-group taking rows
+// r, r + grid, ... in turn.  A row's tiles are a chain (QK -> tile maximum ->
+// exponentials and P codes -> PV) through work-group barriers; with one row
+// per CU nothing fills those waits, with two rows per CU the other work-group
+// computes while this one waits for its barrier or its next tile.  Each wave
+// takes 32 keys in QK (two 16-key blocks) and 128 output columns in PV.
+// Eight heads, no explicit original slots.
+#ifndef SHAREDKV_ROWS_KERNEL
+#define SHAREDKV_ROWS_KERNEL 1
+#endif
+constexpr bool ROWS_KERNEL = SHAREDKV_ROWS_KERNEL;
+constexpr int ROWS_THREADS = 256;
+constexpr int ROWS_WAVES = ROWS_THREADS / 64;
+constexpr int ROWS_TILES = 1 + MAX_LIST / N;                       // a C4 row: window tile + compressed tiles
+constexpr int ROWS_DMA = N * D / 1024 / ROWS_WAVES;               // LDS DMA instructions per wave and tile
+constexpr int ROWS_IX = MAX_LIST / ROWS_THREADS;                  // C4 index entries per thread
+static_assert(ROWS_DMA == 16 && ROWS_IX == 4, "four waves: 32 keys and 16 copies per wave and tile");
+
+struct alignas(16) RowsShared {
+    int32_t redmax[HEADS][ROWS_WAVES];   // per-wave maxima of the tile (fkey)
+    float redsum[HEADS][ROWS_WAVES];     // per-wave sums of the wave's two 16-key blocks
+    float asc[2][HEADS];                 // alpha * softmax_scale per kind
+    int32_t scan[ROWS_WAVES];
+    int32_t misc[8];
+    float scale[2][D];                   // channel scales of the window / compressed cache
+    int8_t p[16 * PROW];                 // P codes [MFMA row][key]
+    uint64_t addr[ROWS_TILES * N];       // HBM address of each row of the row's tiles (masked: the Q base)
+    int8_t tile[N * D];                  // the tile buffer; Q code staging before the first tile
+};
+static_assert(sizeof(RowsShared) <= 80 * 1024, "two work-groups per CU");
+
+template <bool STREAM>
+__global__ void __launch_bounds__(ROWS_THREADS, 2)
+c8_rows(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, const uint64_t cmp_indices,
+        const uint32_t batch_arg, const uint32_t topk_arg, const uint32_t rows_arg, const uint32_t grid,
+        const SharedKVArgs p)
+{
+    __shared__ RowsShared s;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, n = lane & 15;
+    // XCD-aware order: consecutive rows stay on one XCD (their windows overlap).
+    const uint32_t G = grid;
+    int32_t qrow = (int32_t)((blockIdx.x & 7u) * (G >> 3) + (blockIdx.x >> 3));
+    if (qrow >= (int32_t)rows_arg) return;
+    const __attribute__((address_space(1))) int32_t *cu = gptr<int32_t>(cu_q);
+    const __attribute__((address_space(1))) int32_t *lens = gptr<int32_t>(seq_lens);
+    const int batch_n = (int)batch_arg, topk = (int)topk_arg;
+
+    // ---- live shape (attention_impl.h:121-137), once per work-group ----
+    if (tid == 0) s.misc[0] = 0;
+    __syncthreads();
+    for (int b = tid; b < batch_n; b += ROWS_THREADS)
+        if (lens[b] > 0 && cu[b + 1] >= 0) atomicMax(&s.misc[0], b + 1);
+    __syncthreads();
+    const int live_batch = uni(s.misc[0]);
+    const int end = live_batch ? cu[live_batch] : 0;
+    const int live_tokens = end <= 0 ? 0 : (end < (int)p.tokens ? end : (int)p.tokens);
+    const float sink0 = gptr<float>(p.sinks)[2 * g], sink1 = gptr<float>(p.sinks)[2 * g + 1];
+    *reinterpret_cast<f32x4 *>(&s.scale[tid >> 7][(tid & 127) * 4]) =
+        *gptr<f32x4>(((tid >> 7) ? p.cmpScale : p.oriScale) + (uint64_t)((tid & 127) * 4) * 4);
+    const int c0 = 128 * wave;   // this wave's PV output columns: c0 + 16 j + n
+
+    for (;; qrow += (int32_t)G) {
+        if (qrow >= (int32_t)rows_arg) return;
+        const int t = qrow;
+        uint16_t *out_row = reinterpret_cast<uint16_t *>(p.out) + (int64_t)t * HEADS * D;
+        float *lse_row = p.lse ? reinterpret_cast<float *>(p.lse) + (int64_t)t * HEADS : nullptr;
+        // Q (heads wave and wave + 4, channels 8 lane ..) and the row's index
+        // entries 4 tid .. 4 tid + 3, requested with the request search (the
+        // other work-group of the CU computes meanwhile).
+        v4i qv[2];
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+            qv[hh] = *gptr<v4i>(q_base + (((uint64_t)t * HEADS + wave + 4 * hh) * D + lane * 8) * 2);
+        int ix[ROWS_IX];
+        const __attribute__((address_space(1))) int32_t *row_ix = gptr<int32_t>(cmp_indices) + (int64_t)t * topk;
+#pragma unroll
+        for (int e = 0; e < ROWS_IX; ++e) ix[e] = tid * ROWS_IX + e < topk ? row_ix[tid * ROWS_IX + e] : -1;
+        __syncthreads();   // every wave is done with the previous row's shared data
+        if (tid == 0) s.misc[1] = -1;
+        __syncthreads();
+        for (int b = tid; b < live_batch; b += ROWS_THREADS) {
+            const int b0 = cu[b], b1 = cu[b + 1];
+            if (b0 <= t && t < b1) {
+                s.misc[1] = b;
+                s.misc[3] = lens[b];
+                s.misc[4] = b1;
+            }
+        }
+        __syncthreads();
+        const int batch = uni(s.misc[1]);
+        const int position = batch < 0 ? -1 : uni(s.misc[3]) - uni(s.misc[4]) + t;
+        // Padding rows of a captured graph (attention_impl.h:443-460) and rows
+        // with a negative position (reference.py:104-105 rejects them) are zero.
+        if (t >= live_tokens || batch < 0 || position < 0) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) reinterpret_cast<v4i *>(out_row)[tid + ROWS_THREADS * i] = v4i{0, 0, 0, 0};
+            if (lse_row && tid < HEADS) lse_row[tid] = 0.0f;
+            continue;
+        }
+
+        // ---- selection (attention_impl.h:58-73, reference.py:228-253) ----
+        const int first_ori = position + 1 > WINDOW ? position + 1 - WINDOW : 0;
+        const int ori_count = position + 1 - first_ori;
+        const int count = (position + 1) / 4;
+        const __attribute__((address_space(1))) int32_t *otab = gptr<int32_t>(p.oriTable) + (int64_t)batch * p.oriTableWidth;
+        const __attribute__((address_space(1))) int32_t *ctab = gptr<int32_t>(p.cmpTable) + (int64_t)batch * p.cmpTableWidth;
+        int wpage = -1, widx = -1, cpage[ROWS_IX];
+        if (tid < ori_count) {
+            const int idx = first_ori + tid;
+            if (idx / BLOCK_ROWS < (int)p.oriTableWidth) {
+                widx = idx;
+                wpage = otab[idx / BLOCK_ROWS];
+            }
+        }
+        bool ok[ROWS_IX];
+#pragma unroll
+        for (int e = 0; e < ROWS_IX; ++e) {
+            ok[e] = ix[e] >= 0 && ix[e] < count;
+            cpage[e] = ok[e] && ix[e] / BLOCK_ROWS < (int)p.cmpTableWidth ? ctab[ix[e] / BLOCK_ROWS] : -1;
+        }
+        // List place of each entry: compacted (count < topk <= 1024,
+        // reference.py:250) or in place with holes masked.
+        int ipos[ROWS_IX];
+        int list_len = topk;
+        if (count < topk) {
+            uint64_t v[ROWS_IX];
+            int below = 0, mine = 0;
+#pragma unroll
+            for (int e = 0; e < ROWS_IX; ++e) {
+                v[e] = __ballot(ok[e]);
+                below += (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(v[e] >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)v[e], 0u));
+                mine += __popcll(v[e]);
+            }
+            if (lane == 0) s.scan[wave] = mine;
+            lds_barrier();
+            int at = below, total = 0;
+#pragma unroll
+            for (int w = 0; w < ROWS_WAVES; ++w) {
+                at += w < wave ? s.scan[w] : 0;
+                total += s.scan[w];
+            }
+#pragma unroll
+            for (int e = 0; e < ROWS_IX; ++e) ipos[e] = ok[e] ? at++ : -1;
+            list_len = uni(total);
+        } else {
+#pragma unroll
+            for (int e = 0; e < ROWS_IX; ++e) ipos[e] = ok[e] ? tid * ROWS_IX + e : -1;
+        }
+        const int tiles = 1 + (list_len + N - 1) / N;   // window tile, then compressed tiles
+
+        // ---- row addresses of every tile (masked rows: the Q base, never used) ----
+        for (int i = tid; i < tiles * N; i += ROWS_THREADS) s.addr[i] = p.q;
+        lds_barrier();
+        if (widx >= 0 && wpage >= 0 && (uint32_t)wpage < p.oriPages)
+            s.addr[tid] = p.ori + (uint64_t)wpage * p.oriStride + (uint64_t)((widx % BLOCK_ROWS) * D);
+#pragma unroll
+        for (int e = 0; e < ROWS_IX; ++e)
+            if (ipos[e] >= 0 && cpage[e] >= 0)
+                s.addr[N + ipos[e]] = p.cmp + (uint64_t)cpage[e] * p.cmpStride + (uint64_t)((ix[e] % BLOCK_ROWS) * D);
+
+        // ---- Q folding and residual split per kind (reference.py:274-279) ----
+        // Staged in the tile buffer, then picked up in the MFMA A layout.
+        v4i qa0[8], qa1[8];
+        {
+            const int want = tiles > 1 ? 2 : 1;
+            const int qe0 = lane * 8;
+#pragma unroll
+            for (int kind = 0; kind < 2; ++kind) {
+                if (kind >= want) continue;
+                const float *scale = s.scale[kind] + qe0;
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    const int h = wave + 4 * hh;
+                    const uint32_t qw[4] = {(uint32_t)qv[hh].x, (uint32_t)qv[hh].y, (uint32_t)qv[hh].z, (uint32_t)qv[hh].w};
+                    float f[8];
+                    float amax = 0.0f;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        f[e] = bf16_to_f32((qw[e >> 1] >> (16 * (e & 1))) & 0xffffu) * scale[e];
+                        amax = fmaxf(amax, fabsf(f[e]));
+                    }
+                    amax = wave_max(amax);
+                    float alpha = amax * (float)(1.0 / 127.0);
+                    alpha = alpha < 1e-12f ? 1e-12f : alpha;
+                    const float inv = 1.0f / alpha;
+                    uint32_t hiw[2] = {0, 0}, low[2] = {0, 0};
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const float x = clamp127(f[e] * inv);
+                        const float hi = __builtin_rintf(x);
+                        const float lo = __builtin_rintf((x - hi) * 127.0f);
+                        hiw[e >> 2] |= ((uint32_t)(int32_t)hi & 0xffu) << (8 * (e & 3));
+                        low[e >> 2] |= ((uint32_t)(int32_t)lo & 0xffu) << (8 * (e & 3));
+                    }
+                    int8_t *stage = s.tile + kind * 16 * QSTAGE;
+                    *reinterpret_cast<u32x2 *>(stage + row_of(h, 0) * QSTAGE + qe0) = u32x2{hiw[0], hiw[1]};
+                    *reinterpret_cast<u32x2 *>(stage + row_of(h, 1) * QSTAGE + qe0) = u32x2{low[0], low[1]};
+                    if (lane == 0) s.asc[kind][h] = alpha * p.softmaxScale;
+                }
+            }
+            lds_barrier();
+            const int8_t *st0 = s.tile, *st1 = s.tile + 16 * QSTAGE;
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj) {
+                qa0[jj] = *reinterpret_cast<const v4i *>(st0 + n * QSTAGE + 64 * jj + 16 * g);
+                qa1[jj] = want > 1 ? *reinterpret_cast<const v4i *>(st1 + n * QSTAGE + 64 * jj + 16 * g) : v4i{0, 0, 0, 0};
+            }
+            lds_barrier();   // every wave holds its Q codes: the buffer is free
+        }
+
+        // ---- tiles (reference.py:280-316 with one partition) ----
+        float mx[2] = {sink0, sink1}, den[2] = {1.0f, 1.0f}, num[2][8];
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) num[hh][j] = 0.0f;
+        v4i held_acc[8];
+        float held_sc[8], held_factor[2];
+        bool held = false;
+        const uint32_t dst = (uint32_t)(uintptr_t)(lds_i8 *)(s.tile);
+        // Tile k with the Q codes of its kind: the window tile (k = 0) takes
+        // qa0, whose registers are free for the compressed tiles after it.
+        auto run_tile = [&](const int k, const v4i (&qa)[8]) {
+            const int kind = k > 0 ? 1 : 0;
+            // Lane coordinates from an opaque copy: the compiler then derives
+            // the tile's per-lane LDS and copy addresses here, instead of
+            // holding them in registers across tiles and rows.
+            int lane_x = lane;
+            asm volatile("" : "+v"(lane_x));
+            const int g = lane_x >> 4, n = lane_x & 15;
+            // Copies of tile k: instruction i of wave w moves keys 16 G + r and
+            // 16 G + 8 + r (G = 2 w + i / 8, r = i % 8) into slots 16 G + 2 r
+            // and 16 G + 2 r + 1, the layout slot_of / tile_offset read.
+            {
+                const int h = lane_x >> 5, c = lane_x & 31;
+                typedef uint64_t u64x2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+                for (int half = 0; half < 2; ++half) {
+                    const int grp = 2 * wave + half;
+                    const u64x2 *rows = reinterpret_cast<const u64x2 *>(s.addr + k * N + 16 * grp + 8 * h);
+                    u64x2 ra[4];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) ra[r] = rows[r];
+                    const int hx = (h ^ grp) & 1;
+#pragma unroll
+                    for (int r = 0; r < 8; ++r) {
+                        const int chunk = c ^ r ^ (hx << 3);
+                        dma16<STREAM>(ra[r >> 1][r & 1] + (uint32_t)(chunk << 4),
+                                      (uint32_t)uni((int)(dst + (16 * grp + 2 * r) * D)));
+                    }
+                }
+            }
+            if (held) {
+                // The previous tile's FP32 epilogue (reference.py:313-316) while
+                // this tile's rows are in flight.
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        float dots = (float)held_acc[j][2 * hh];
+                        dots = dots + (float)held_acc[j][2 * hh + 1] * (float)(1.0 / 127.0);
+                        const float pv = dots * held_sc[j] * (float)(1.0 / 127.0);
+                        num[hh][j] = num[hh][j] * held_factor[hh] + pv;
+                    }
+            }
+            vm_wait<0>();
+            lds_barrier();   // every wave's copies of tile k have landed
+
+            // ---- QK: S[16 rows][32 keys of this wave] (reference.py:286-289) ----
+            v4i sacc[2] = {v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}};
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                const int sl = slot_of(32 * wave + 16 * kb + n);
+                v4i b[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) b[j] = *reinterpret_cast<const v4i *>(s.tile + tile_offset(sl, 4 * j + g));
+#pragma unroll
+                for (int j = 0; j < 8; ++j) sacc[kb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(qa[j], b[j], sacc[kb], 0, 0, 0);
+            }
+            // ---- logits and the tile maximum (reference.py:288-303) ----
+            float lg[2][2];
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                const bool valid = s.addr[k * N + 32 * wave + 16 * kb + n] != p.q;
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    float dots = (float)sacc[kb][2 * hh];
+                    dots = dots + (float)sacc[kb][2 * hh + 1] * (float)(1.0 / 127.0);
+                    const float l = dots * s.asc[kind][2 * g + hh];
+                    lg[kb][hh] = valid ? l : -1e30f;
+                }
+            }
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                const int kmax = row16_max_key(max(fkey(lg[0][hh]), fkey(lg[1][hh])));
+                if (n == 0) s.redmax[2 * g + hh][wave] = kmax;
+            }
+            lds_barrier();
+            float mnew[2], factor[2];
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                const v4i a = *reinterpret_cast<const v4i *>(&s.redmax[2 * g + hh][0]);
+                mnew[hh] = fkey_value(max(max(fkey(mx[hh]), a.x), max(max(a.y, a.z), a.w)));
+            }
+            {
+                const bool odd = n & 1;   // exp(max_old - max_new), one exponential per lane pair
+                const float mine = sk_expf_nonpos(odd ? mx[1] - mnew[1] : mx[0] - mnew[0]);
+                const float other = dpp<DPP_XOR1>(mine);
+                factor[0] = odd ? other : mine;
+                factor[1] = odd ? mine : other;
+            }
+            // ---- weights, pairwise tile sum, P codes (reference.py:304-312) ----
+            float wsum[2];
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                float blk[2];
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb) {
+                    const int key = 32 * wave + 16 * kb + n;
+                    const float w = sk_expf_nonpos(lg[kb][hh] - mnew[hh]);
+                    const float x = w * 127.0f;
+                    const float ph = __builtin_rintf(x);
+                    const float pl = __builtin_rintf((x - ph) * 127.0f);
+                    s.p[row_of(2 * g + hh, 0) * PROW + key] = (int8_t)(int32_t)ph;
+                    s.p[row_of(2 * g + hh, 1) * PROW + key] = (int8_t)(int32_t)pl;
+                    blk[kb] = row16_tree_sum(w);   // one 16-key block
+                }
+                wsum[hh] = blk[0] + blk[1];        // blocks 2 w and 2 w + 1
+                if (n == 0) s.redsum[2 * g + hh][wave] = wsum[hh];
+            }
+            lds_barrier();
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                const f32x4 a = *reinterpret_cast<const f32x4 *>(&s.redsum[2 * g + hh][0]);
+                const float tile_sum = (a.x + a.y) + (a.z + a.w);   // pairwise over the eight blocks
+                den[hh] = den[hh] * factor[hh] + tile_sum;
+            }
+            // ---- PV: [16 rows][this wave's 128 columns] (reference.py:310-316) ----
+            v4i vacc[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) vacc[j] = v4i{0, 0, 0, 0};
+            const lds_i8 *vbase = (const lds_i8 *)(s.tile);
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                const v4i pa = *reinterpret_cast<const v4i *>(s.p + n * PROW + 64 * kb + 16 * g);
+                const int sl_lo = slot_of(64 * kb + 16 * g + (n >> 1));
+                const int sl_hi = slot_of(64 * kb + 16 * g + 8 + (n >> 1));
+#pragma unroll
+                for (int jh = 0; jh < 2; ++jh) {
+                    v2i b0[4], b1[4];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const int chunk = 8 * wave + 4 * jh + j;
+                        b0[j] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i *)(vbase + tile_offset(sl_lo, chunk) + 8 * (n & 1)));
+                        b1[j] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i *)(vbase + tile_offset(sl_hi, chunk) + 8 * (n & 1)));
+                    }
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const v4i vb = {b0[j].x, b0[j].y, b1[j].x, b1[j].y};
+                        vacc[4 * jh + j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(pa, vb, vacc[4 * jh + j], 0, 0, 0);
+                    }
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                held_acc[j] = vacc[j];
+                held_sc[j] = s.scale[kind][c0 + 16 * j + n];
+            }
+            held_factor[0] = factor[0];
+            held_factor[1] = factor[1];
+            held = true;
+            mx[0] = mnew[0];
+            mx[1] = mnew[1];
+            lds_barrier();   // every wave is done with tile k and the P codes
+        };
+        run_tile(0, qa0);
+        for (int k = 1; k < tiles; ++k) run_tile(k, qa1);
+        if (held) {
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    float dots = (float)held_acc[j][2 * hh];
+                    dots = dots + (float)held_acc[j][2 * hh + 1] * (float)(1.0 / 127.0);
+                    const float pv = dots * held_sc[j] * (float)(1.0 / 127.0);
+                    num[hh][j] = num[hh][j] * held_factor[hh] + pv;
+                }
+        }
+        // ---- finalize (reference.py:317-323 with one partition) ----
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            const int h = 2 * g + hh;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) out_row[h * D + c0 + 16 * j + n] = (uint16_t)pack_bf16(num[hh][j] / den[hh], 0.0f);
+            if (lse_row && wave == 0 && n == 0) lse_row[h] = mx[hh] + logf(den[hh]);
+        }
+    }
+}
+
 // ---- INT8 cache writer (cache_write.cpp:9-88): one wave per update row ----
 template <typename Index, bool Paired>
 __global__ void __launch_bounds__(256)
@@ -1545,6 +1947,14 @@ void launch_variant(hipStream_t stream, const SharedKVArgs *a, const SharedKVDeb
     // persistent work-groups (PERSIST: one per CU, each taking rows in turn).
     // The C128 and window-only kernels would spill in the row loop.
     const bool persist = !DEBUG && !slots && a->ratio == 4 && !joint4 && splits == 1 && rows > (uint32_t)PLAN_CUS;
+    if (ROWS_KERNEL && persist && !streamed && !ANYH) {
+        // Eight heads, prefill-shaped (more than four query tokens per
+        // sequence slot): two four-wave work-groups per CU (c8_rows).
+        const uint32_t g2 = 2u * (uint32_t)PLAN_CUS;
+        hipLaunchKernelGGL(c8_rows<false>, dim3(g2), dim3(ROWS_THREADS), 0, stream, a->cuQ, a->seqLens, a->q,
+                           a->indices, a->batch, a->topk, rows, g2, *a);
+        return;
+    }
     decltype(&c8_attention<1, false, false, ANYH, false, false, false>) kernel;
     if (persist) {
         grid = (uint32_t)PLAN_CUS;
