@@ -1489,7 +1489,8 @@ c8_rows(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, con
         const SharedKVArgs p)
 {
     __shared__ RowsShared s;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, n = lane & 15;
+    const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, n = lane & 15;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // scalar: copy destinations on the SALU
     // XCD-aware order: consecutive rows stay on one XCD (their windows overlap).
     const uint32_t G = grid;
     int32_t qrow = (int32_t)((blockIdx.x & 7u) * (G >> 3) + (blockIdx.x >> 3));
@@ -1675,12 +1676,7 @@ c8_rows(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, con
         // qa0, whose registers are free for the compressed tiles after it.
         auto run_tile = [&](const int k, const v4i (&qa)[8]) {
             const int kind = k > 0 ? 1 : 0;
-            // Lane coordinates from an opaque copy: the compiler then derives
-            // the tile's per-lane LDS and copy addresses here, instead of
-            // holding them in registers across tiles and rows.
-            int lane_x = lane;
-            asm volatile("" : "+v"(lane_x));
-            const int g = lane_x >> 4, n = lane_x & 15;
+            const int lane_x = lane;
             // Copies of tile k: instruction i of wave w moves keys 16 G + r and
             // 16 G + 8 + r (G = 2 w + i / 8, r = i % 8) into slots 16 G + 2 r
             // and 16 G + 2 r + 1, the layout slot_of / tile_offset read.
