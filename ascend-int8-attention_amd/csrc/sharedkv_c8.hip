@@ -1712,8 +1712,10 @@ c8_rows(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, con
                         num[hh][j] = num[hh][j] * held_factor[hh] + pv;
                     }
             }
+            // This wave's copies of tile k have landed.  Its QK keys are the
+            // rows it copied itself, so QK needs no barrier; the tile-maximum
+            // barrier below makes every wave's rows visible before PV.
             vm_wait<0>();
-            lds_barrier();   // every wave's copies of tile k have landed
 
             // ---- QK: S[16 rows][32 keys of this wave] (reference.py:286-289) ----
             v4i sacc[2] = {v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}};
