@@ -34,6 +34,9 @@
 //   partials   with S > 1 partitions, FP32 [num, max, den] go to `partial`;
 //              the last partition of a row to finish (a ticket per row in
 //              `workspace`) folds them, or c8_merge does in a second launch
+// One-partition C4 launches of more rows than CUs (prefill) run c8_rows
+// instead: two four-wave work-groups per CU with one tile buffer each, each
+// taking rows in turn, so that one row's tile chain fills the other's waits.
 // Integer partials are exact, so any assignment of keys to lanes gives the
 // reference's integers; the FP32 sequence below is kept in the reference's
 // order with contraction disabled.
@@ -1458,10 +1461,6 @@ c8_merge(const SharedKVArgs p, uint32_t splits)
 // computes while this one waits for its barrier or its next tile.  Each wave
 // takes 32 keys in QK (two 16-key blocks) and 128 output columns in PV.
 // Eight heads, no explicit original slots.
-#ifndef SHAREDKV_ROWS_KERNEL
-#define SHAREDKV_ROWS_KERNEL 1
-#endif
-constexpr bool ROWS_KERNEL = SHAREDKV_ROWS_KERNEL;
 constexpr int ROWS_THREADS = 256;
 constexpr int ROWS_WAVES = ROWS_THREADS / 64;
 constexpr int ROWS_TILES = 1 + MAX_LIST / N;                       // a C4 row: window tile + compressed tiles
@@ -1945,7 +1944,7 @@ void launch_variant(hipStream_t stream, const SharedKVArgs *a, const SharedKVDeb
     // persistent work-groups (PERSIST: one per CU, each taking rows in turn).
     // The C128 and window-only kernels would spill in the row loop.
     const bool persist = !DEBUG && !slots && a->ratio == 4 && !joint4 && splits == 1 && rows > (uint32_t)PLAN_CUS;
-    if (ROWS_KERNEL && persist && !streamed && !ANYH) {
+    if (persist && !streamed && !ANYH) {
         // Eight heads, prefill-shaped (more than four query tokens per
         // sequence slot): two four-wave work-groups per CU (c8_rows).
         const uint32_t g2 = 2u * (uint32_t)PLAN_CUS;
