@@ -1944,12 +1944,11 @@ void launch_variant(hipStream_t stream, const SharedKVArgs *a, const SharedKVDeb
     // persistent work-groups (PERSIST: one per CU, each taking rows in turn).
     // The C128 and window-only kernels would spill in the row loop.
     const bool persist = !DEBUG && !slots && a->ratio == 4 && !joint4 && splits == 1 && rows > (uint32_t)PLAN_CUS;
-    if (persist && !streamed && !ANYH) {
-        // Eight heads, prefill-shaped (more than four query tokens per
-        // sequence slot): two four-wave work-groups per CU (c8_rows), at most
+    if (persist && !ANYH) {
+        // Eight heads: two four-wave work-groups per CU (c8_rows), at most
         // one per row, so that every XCD gets its share of the rows.
         const uint32_t g2 = rows < 2u * (uint32_t)PLAN_CUS ? (rows + 7u) & ~7u : 2u * (uint32_t)PLAN_CUS;
-        hipLaunchKernelGGL(c8_rows<false>, dim3(g2), dim3(ROWS_THREADS), 0, stream, a->cuQ, a->seqLens, a->q,
+        hipLaunchKernelGGL(streamed ? c8_rows<true> : c8_rows<false>, dim3(g2), dim3(ROWS_THREADS), 0, stream, a->cuQ, a->seqLens, a->q,
                            a->indices, a->batch, a->topk, rows, g2, *a);
         return;
     }

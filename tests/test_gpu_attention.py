@@ -431,6 +431,27 @@ def test_baseline_configs(index):
         torch.cuda.empty_cache()
 
 
+@pytest.mark.parametrize("batch,tokens", [(300, 1), (160, 2)])
+def test_many_row_decode_launches(batch, tokens):
+    """Decode-shaped C4 launches of more rows than CUs (one partition, KV
+    copies with the non-temporal policy, work-groups taking rows in turn),
+    at the serving page stride: 96 rows spread over the launch against the
+    checker."""
+    import torch
+    from npu_sparse_attn_sharedkv_int8 import PreparedAttention
+    from tests.device_cases import DeviceCase
+    rng = np.random.default_rng(200 + batch)
+    lengths = rng.integers(2048, 16385, batch)
+    say(f"[many-row decode] {batch} x {tokens}")
+    dc = DeviceCase(30 + tokens, 4, [tokens] * batch, lengths, page_stride=SERVING_STRIDE)
+    op = PreparedAttention(dc.dev, dc.ori_scale, dc.cmp_scale, return_lse=True)
+    assert op.splits == 1
+    op.run()
+    torch.cuda.synchronize()
+    rows = np.linspace(0, batch * tokens - 1, 96).astype(int)
+    compare(dc.host(), bits_of(op.out), op.lse.cpu().numpy(), op.splits, rows=rows, tag=f"{batch} x {tokens}")
+
+
 @pytest.mark.parametrize("mode,heads", [(0, 8), (1, 8), (0, 12), (1, 12)])
 def test_padded_graph_rows_are_zero_and_guards_hold(mode, heads):
     """Capacity rows past the live tokens (seq_len 0 / cu_q sentinel) are
