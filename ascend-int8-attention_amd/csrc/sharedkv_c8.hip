@@ -34,9 +34,10 @@
 //   partials   with S > 1 partitions, FP32 [num, max, den] go to `partial`;
 //              the last partition of a row to finish (a ticket per row in
 //              `workspace`) folds them, or c8_merge does in a second launch
-// One-partition C4 launches of more rows than CUs (prefill) run c8_rows
-// instead: two four-wave work-groups per CU with one tile buffer each, each
-// taking rows in turn, so that one row's tile chain fills the other's waits.
+// Eight-head one-partition C4 launches of more rows than CUs (prefill, large
+// decode batches) run c8_rows instead: two four-wave work-groups per CU with
+// one tile buffer each, each taking rows in turn, so that one row's tile
+// chain fills the other's waits.
 // Integer partials are exact, so any assignment of keys to lanes gives the
 // reference's integers; the FP32 sequence below is kept in the reference's
 // order with contraction disabled.
@@ -1451,7 +1452,7 @@ c8_merge(const SharedKVArgs p, uint32_t splits)
                 H - hbase < HEADS ? H - hbase : HEADS);
 }
 
-// ---- c8_rows: one-partition C4 launches of many query rows (prefill) ----
+// ---- c8_rows: one-partition C4 launches of many query rows ----
 // The same numerics as c8_attention with one partition (128-key tiles,
 // reference.py:210-323), laid out so that two work-groups share a CU: four
 // waves and one tile buffer each (80 KiB of LDS), each work-group taking rows
@@ -1460,7 +1461,8 @@ c8_merge(const SharedKVArgs p, uint32_t splits)
 // per CU nothing fills those waits, with two rows per CU the other work-group
 // computes while this one waits for its barrier or its next tile.  Each wave
 // takes 32 keys in QK (two 16-key blocks) and 128 output columns in PV.
-// Eight heads, no explicit original slots.
+// Eight heads, no explicit original slots.  STREAM: non-temporal KV copies
+// (decode-shaped launches).
 constexpr int ROWS_THREADS = 256;
 constexpr int ROWS_WAVES = ROWS_THREADS / 64;
 constexpr int ROWS_TILES = 1 + MAX_LIST / N;                       // a C4 row: window tile + compressed tiles
