@@ -1717,6 +1717,11 @@ c8_rows(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, con
             // rows it copied itself, so QK needs no barrier; the tile-maximum
             // barrier below makes every wave's rows visible before PV.
             vm_wait<0>();
+            // Prefill (rows from L2): the wave in its tile chain issues ahead
+            // of the other work-group's wave on the SIMD (copies, epilogue)
+            // until the tile ends.  Decode launches, bound by the stream,
+            // keep equal priority.
+            if (!STREAM) __builtin_amdgcn_s_setprio(1);
 
             // ---- QK: S[16 rows][32 keys of this wave] (reference.py:286-289) ----
             v4i sacc[2] = {v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}};
@@ -1823,6 +1828,7 @@ c8_rows(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, con
             held = true;
             mx[0] = mnew[0];
             mx[1] = mnew[1];
+            if (!STREAM) __builtin_amdgcn_s_setprio(0);
             lds_barrier();   // every wave is done with tile k and the P codes
         };
         run_tile(0, qa0);
