@@ -1461,8 +1461,10 @@ c8_merge(const SharedKVArgs p, uint32_t splits)
 // per CU nothing fills those waits, with two rows per CU the other work-group
 // computes while this one waits for its barrier or its next tile.  Each wave
 // takes 32 keys in QK (two 16-key blocks) and 128 output columns in PV.
-// Eight heads, no explicit original slots.  STREAM: non-temporal KV copies
-// (decode-shaped launches).
+// No explicit original slots.  STREAM: non-temporal KV copies (decode-shaped
+// launches).  ANYH: 1..128 heads, a row being one group of eight heads of a
+// token (residual codes off above eight heads, reference.py:221-222), as in
+// c8_attention.
 constexpr int ROWS_THREADS = 256;
 constexpr int ROWS_WAVES = ROWS_THREADS / 64;
 constexpr int ROWS_TILES = 1 + MAX_LIST / N;                       // a C4 row: window tile + compressed tiles
@@ -1483,11 +1485,11 @@ struct alignas(16) RowsShared {
 };
 static_assert(sizeof(RowsShared) <= 80 * 1024, "two work-groups per CU");
 
-template <bool STREAM>
+template <bool STREAM, bool ANYH>
 __global__ void __launch_bounds__(ROWS_THREADS, 2)
 c8_rows(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, const uint64_t cmp_indices,
         const uint32_t batch_arg, const uint32_t topk_arg, const uint32_t rows_arg, const uint32_t grid,
-        const SharedKVArgs p)
+        const uint32_t heads_arg, const SharedKVArgs p)
 {
     __shared__ RowsShared s;
     const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, n = lane & 15;
@@ -1509,23 +1511,29 @@ c8_rows(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, con
     const int live_batch = uni(s.misc[0]);
     const int end = live_batch ? cu[live_batch] : 0;
     const int live_tokens = end <= 0 ? 0 : (end < (int)p.tokens ? end : (int)p.tokens);
-    const float sink0 = gptr<float>(p.sinks)[2 * g], sink1 = gptr<float>(p.sinks)[2 * g + 1];
+    const int H = ANYH ? (int)heads_arg : HEADS;                 // heads of a query token
+    const int HG = ANYH ? (H + HEADS - 1) / HEADS : 1;           // groups of eight
+    const bool resid = !ANYH || H <= HEADS;
     *reinterpret_cast<f32x4 *>(&s.scale[tid >> 7][(tid & 127) * 4]) =
         *gptr<f32x4>(((tid >> 7) ? p.cmpScale : p.oriScale) + (uint64_t)((tid & 127) * 4) * 4);
     const int c0 = 128 * wave;   // this wave's PV output columns: c0 + 16 j + n
 
     for (;; qrow += (int32_t)G) {
         if (qrow >= (int32_t)rows_arg) return;
-        const int t = qrow;
-        uint16_t *out_row = reinterpret_cast<uint16_t *>(p.out) + (int64_t)t * HEADS * D;
-        float *lse_row = p.lse ? reinterpret_cast<float *>(p.lse) + (int64_t)t * HEADS : nullptr;
+        const int t = ANYH ? qrow / HG : qrow;                   // token
+        const int hbase = ANYH ? HEADS * (qrow % HG) : 0;        // first head of the row
+        const int hlive = ANYH ? (H - hbase < HEADS ? H - hbase : HEADS) : HEADS;
+        uint16_t *out_row = reinterpret_cast<uint16_t *>(p.out) + ((int64_t)t * H + hbase) * D;
+        float *lse_row = p.lse ? reinterpret_cast<float *>(p.lse) + (int64_t)t * H + hbase : nullptr;
         // Q (heads wave and wave + 4, channels 8 lane ..) and the row's index
         // entries 4 tid .. 4 tid + 3, requested with the request search (the
         // other work-group of the CU computes meanwhile).
         v4i qv[2];
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh)
-            qv[hh] = *gptr<v4i>(q_base + (((uint64_t)t * HEADS + wave + 4 * hh) * D + lane * 8) * 2);
+            qv[hh] = !ANYH || wave + 4 * hh < hlive
+                         ? *gptr<v4i>(q_base + (((uint64_t)t * H + hbase + wave + 4 * hh) * D + lane * 8) * 2)
+                         : v4i{0, 0, 0, 0};   // padding heads of the last group: zero Q, never written
         int ix[ROWS_IX];
         const __attribute__((address_space(1))) int32_t *row_ix = gptr<int32_t>(cmp_indices) + (int64_t)t * topk;
 #pragma unroll
@@ -1548,8 +1556,10 @@ c8_rows(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, con
         // with a negative position (reference.py:104-105 rejects them) are zero.
         if (t >= live_tokens || batch < 0 || position < 0) {
 #pragma unroll
-            for (int i = 0; i < 2; ++i) reinterpret_cast<v4i *>(out_row)[tid + ROWS_THREADS * i] = v4i{0, 0, 0, 0};
-            if (lse_row && tid < HEADS) lse_row[tid] = 0.0f;
+            for (int i = 0; i < 2; ++i)
+                if (!ANYH || tid + ROWS_THREADS * i < hlive * (D / 8))
+                    reinterpret_cast<v4i *>(out_row)[tid + ROWS_THREADS * i] = v4i{0, 0, 0, 0};
+            if (lse_row && tid < hlive) lse_row[tid] = 0.0f;
             continue;
         }
 
@@ -1643,7 +1653,7 @@ c8_rows(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, con
                     for (int e = 0; e < 8; ++e) {
                         const float x = clamp127(f[e] * inv);
                         const float hi = __builtin_rintf(x);
-                        const float lo = __builtin_rintf((x - hi) * 127.0f);
+                        const float lo = resid ? __builtin_rintf((x - hi) * 127.0f) : 0.0f;
                         hiw[e >> 2] |= ((uint32_t)(int32_t)hi & 0xffu) << (8 * (e & 3));
                         low[e >> 2] |= ((uint32_t)(int32_t)lo & 0xffu) << (8 * (e & 3));
                     }
@@ -1664,7 +1674,10 @@ c8_rows(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, con
         }
 
         // ---- tiles (reference.py:280-316 with one partition) ----
-        float mx[2] = {sink0, sink1}, den[2] = {1.0f, 1.0f}, num[2][8];
+        const __attribute__((address_space(1))) float *sinks = gptr<float>(p.sinks);
+        float mx[2], den[2] = {1.0f, 1.0f}, num[2][8];
+        mx[0] = (!ANYH || 2 * g < hlive) ? sinks[hbase + 2 * g] : 0.0f;
+        mx[1] = (!ANYH || 2 * g + 1 < hlive) ? sinks[hbase + 2 * g + 1] : 0.0f;
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
@@ -1777,7 +1790,7 @@ c8_rows(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, con
                     const float w = sk_expf_nonpos(lg[kb][hh] - mnew[hh]);
                     const float x = w * 127.0f;
                     const float ph = __builtin_rintf(x);
-                    const float pl = __builtin_rintf((x - ph) * 127.0f);
+                    const float pl = resid ? __builtin_rintf((x - ph) * 127.0f) : 0.0f;
                     s.p[row_of(2 * g + hh, 0) * PROW + key] = (int8_t)(int32_t)ph;
                     s.p[row_of(2 * g + hh, 1) * PROW + key] = (int8_t)(int32_t)pl;
                     blk[kb] = row16_tree_sum(w);   // one 16-key block
@@ -1848,6 +1861,7 @@ c8_rows(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, con
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
             const int h = 2 * g + hh;
+            if (ANYH && h >= hlive) continue;
 #pragma unroll
             for (int j = 0; j < 8; ++j) out_row[h * D + c0 + 16 * j + n] = (uint16_t)pack_bf16(num[hh][j] / den[hh], 0.0f);
             if (lse_row && wave == 0 && n == 0) lse_row[h] = mx[hh] + logf(den[hh]);
@@ -1948,40 +1962,36 @@ void launch_variant(hipStream_t stream, const SharedKVArgs *a, const SharedKVDeb
     // sequence (C4 joint rows cost the tiled C4 path about 3 % where they
     // are compiled in, so only such launches get them).
     const bool joint4 = !DEBUG && !slots && a->heads <= HEADS && (uint64_t)a->cmpTableWidth * BLOCK_ROWS <= (uint64_t)N;
-    // One-partition C4 launches of more rows than CUs (prefill) run
-    // persistent work-groups (PERSIST: one per CU, each taking rows in turn).
-    // The C128 and window-only kernels would spill in the row loop.
+    // One-partition C4 launches of more rows than CUs (prefill, large decode
+    // batches) run two four-wave work-groups per CU taking rows in turn
+    // (c8_rows).  C128
+    // and window-only launches keep one work-group per row.
     const bool persist = !DEBUG && !slots && a->ratio == 4 && !joint4 && splits == 1 && rows > (uint32_t)PLAN_CUS;
-    if (persist && !ANYH) {
-        // Eight heads: two four-wave work-groups per CU (c8_rows), at most
-        // one per row, so that every XCD gets its share of the rows.
+    if (persist) {
+        // Two four-wave work-groups per CU (c8_rows), at most one per row, so
+        // that every XCD gets its share of the rows.
         const uint32_t g2 = rows < 2u * (uint32_t)PLAN_CUS ? (rows + 7u) & ~7u : 2u * (uint32_t)PLAN_CUS;
-        hipLaunchKernelGGL(streamed ? c8_rows<true> : c8_rows<false>, dim3(g2), dim3(ROWS_THREADS), 0, stream, a->cuQ, a->seqLens, a->q,
-                           a->indices, a->batch, a->topk, rows, g2, *a);
+        const auto rows_kernel = streamed ? &c8_rows<true, ANYH> : &c8_rows<false, ANYH>;
+        hipLaunchKernelGGL(rows_kernel, dim3(g2), dim3(ROWS_THREADS), 0, stream, a->cuQ, a->seqLens, a->q, a->indices,
+                           a->batch, a->topk, rows, g2, a->heads, *a);
         return;
     }
-    decltype(&c8_attention<1, false, false, ANYH, false, false, false>) kernel;
-    if (persist) {
-        grid = (uint32_t)PLAN_CUS;
-        kernel = streamed ? &c8_attention<4, false, false, ANYH, true, false, true>
-                          : &c8_attention<4, false, false, ANYH, false, false, true>;
-    } else {
-        kernel = slots ? &c8_attention<1, DEBUG, true, ANYH, false, false, false>
-                       : &c8_attention<1, DEBUG, false, ANYH, false, false, false>;
-        if (a->ratio == 4 && joint4)
-            kernel = streamed ? &c8_attention<4, DEBUG, false, ANYH, !DEBUG, !DEBUG, false>
-                              : &c8_attention<4, DEBUG, false, ANYH, false, !DEBUG, false>;
-        else if (a->ratio == 4)
-            kernel = slots ? (streamed ? &c8_attention<4, DEBUG, true, ANYH, !DEBUG, false, false>
-                                       : &c8_attention<4, DEBUG, true, ANYH, false, false, false>)
-                           : (streamed ? &c8_attention<4, DEBUG, false, ANYH, !DEBUG, false, false>
-                                       : &c8_attention<4, DEBUG, false, ANYH, false, false, false>);
-        else if (a->ratio == 128)
-            kernel = slots ? (streamed ? &c8_attention<128, DEBUG, true, ANYH, !DEBUG, true, false>
-                                       : &c8_attention<128, DEBUG, true, ANYH, false, true, false>)
-                           : (streamed ? &c8_attention<128, DEBUG, false, ANYH, !DEBUG, true, false>
-                                       : &c8_attention<128, DEBUG, false, ANYH, false, true, false>);
-    }
+    decltype(&c8_attention<1, false, false, ANYH, false, false, false>) kernel =
+        slots ? &c8_attention<1, DEBUG, true, ANYH, false, false, false>
+              : &c8_attention<1, DEBUG, false, ANYH, false, false, false>;
+    if (a->ratio == 4 && joint4)
+        kernel = streamed ? &c8_attention<4, DEBUG, false, ANYH, !DEBUG, !DEBUG, false>
+                          : &c8_attention<4, DEBUG, false, ANYH, false, !DEBUG, false>;
+    else if (a->ratio == 4)
+        kernel = slots ? (streamed ? &c8_attention<4, DEBUG, true, ANYH, !DEBUG, false, false>
+                                   : &c8_attention<4, DEBUG, true, ANYH, false, false, false>)
+                       : (streamed ? &c8_attention<4, DEBUG, false, ANYH, !DEBUG, false, false>
+                                   : &c8_attention<4, DEBUG, false, ANYH, false, false, false>);
+    else if (a->ratio == 128)
+        kernel = slots ? (streamed ? &c8_attention<128, DEBUG, true, ANYH, !DEBUG, true, false>
+                                   : &c8_attention<128, DEBUG, true, ANYH, false, true, false>)
+                       : (streamed ? &c8_attention<128, DEBUG, false, ANYH, !DEBUG, true, false>
+                                   : &c8_attention<128, DEBUG, false, ANYH, false, true, false>);
     // The leading scalar arguments are the ones the first loads need; the
     // build preloads them into SGPRs (-amdgpu-kernarg-preload-count), so
     // those loads do not wait for a read of the argument block.
