@@ -425,7 +425,7 @@ __device__ __forceinline__ void fold_row(const __amdgpu_buffer_rsrc_t states, in
 // written.  Above eight heads the Q and P residual codes are zero
 // (reference.py:221-222: residual quantization only for <= 8 heads), which
 // leaves every other operation as it is.  Without ANYH, heads == 8.
-template <int RATIO, bool DEBUG, bool SLOTS, bool ANYH, bool STREAM, bool JOINT, bool PERSIST>
+template <int RATIO, bool DEBUG, bool SLOTS, bool ANYH, bool STREAM, bool JOINT>
 __global__ void __launch_bounds__(THREADS, 1)   // one work-group per CU: the 128 KiB tile ring fills the LDS
 c8_attention(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, const uint64_t cmp_indices,
              const uint32_t batch_arg, const uint32_t topk_arg, const uint32_t heads_arg, const uint32_t splits,
@@ -433,8 +433,7 @@ c8_attention(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base
              const uint32_t fused)
 {
     __shared__ Shared s;
-    // (Non-const: a persistent work-group re-derives them for every row.)
-    int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, n = lane & 15;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, n = lane & 15;
 
     // XCD-aware order: consecutive work items (the partitions of one row,
     // then the next row) stay on one XCD and share its L2.
@@ -598,13 +597,8 @@ c8_attention(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base
             find_request(t, false);
         }
     }
-    // One row (a work item: query row qrow, partition part) from its row
-    // request onwards.  PERSIST work-groups run it for rows qrow, qrow + G,
-    // ... in turn (one-partition launches with more rows than CUs), each next
-    // row's Q and indices loaded while the current row's first tile lands.
-    v4i qv_next = {0, 0, 0, 0};
-    int ix_next[2] = {-1, -1};
-    bool prefetched = false;          // a row that ends early loads nothing ahead
+    // The work item (query row qrow, partition part) from its row request
+    // onwards.
     auto run_row = [&]() {
         // Every metadata load has landed: said explicitly (vmcnt(0)) so that the
         // compiler's own wait tracking does not hold back the block-table reads
@@ -1016,23 +1010,6 @@ c8_attention(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base
             // buffer 1) and the tile loop's per-lane set-up run while they are in
             // flight, then tile 1 follows into the freed buffer.
             issue_tile(0, 0);
-            if (PERSIST && first == 0 && qrow + (int32_t)G < (int32_t)rows_arg) {
-                // The next row's Q and indices, behind this tile's copies
-                // (the first tile wait covers them).
-                const int32_t nrow = qrow + (int32_t)G, nt = ANYH ? nrow / HG : nrow;
-                const int32_t nbase = ANYH ? HEADS * (nrow % HG) : 0;
-                const int nlive = ANYH ? (H - nbase < HEADS ? H - nbase : HEADS) : HEADS;
-                qv_next = v4i{0, 0, 0, 0};
-                if (!ANYH || wave < nlive)
-                    qv_next = *gptr<v4i>(q_base + (((uint64_t)nt * H + nbase + wave) * D + qd0) * 2);
-                if (RATIO == 4) {
-                    const int topk = (int)topk_arg;
-                    const __attribute__((address_space(1))) int32_t *next_ix = gptr<int32_t>(cmp_indices) + (int64_t)nt * topk;
-#pragma unroll
-                    for (int i = 0; i < 2; ++i) ix_next[i] = tid * 2 + i < topk ? next_ix[tid * 2 + i] : -1;
-                }
-                prefetched = true;
-            }
             if (first == 0) {
                 bool want0 = false, want1 = false;
                 for (int i = 0; i < my_tiles; ++i) {
@@ -1393,43 +1370,7 @@ c8_attention(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
         fold_row<SC1>(states, folded, tid, out_row, lse_row, ANYH ? hlive : HEADS);
     };
-    for (;;) {
-        if (PERSIST) {
-            // Lane coordinates from an opaque copy of the thread index, so
-            // the compiler derives the row's lane addresses inside the row
-            // loop instead of holding them across rows.
-            asm volatile("" : "+v"(tid));
-            lane = tid & 63;
-            wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-            g = lane >> 4;
-            n = lane & 15;
-        }
-        run_row();
-        if (!PERSIST) return;
-        qrow += (int32_t)G;
-        if (qrow >= (int32_t)rows_arg) return;
-        t = ANYH ? qrow / HG : qrow;
-        hbase = ANYH ? HEADS * (qrow % HG) : 0;
-        hlive = ANYH ? (H - hbase < HEADS ? H - hbase : HEADS) : HEADS;
-        if (prefetched) {
-            qv = qv_next;
-            ix[0] = ix_next[0];
-            ix[1] = ix_next[1];
-        } else {
-            qv = v4i{0, 0, 0, 0};
-            if (!ANYH || wave < hlive) qv = *gptr<v4i>(q_base + (((uint64_t)t * H + hbase + wave) * D + qd0) * 2);
-            if (RATIO == 4) {
-                const int topk = (int)topk_arg;
-                const __attribute__((address_space(1))) int32_t *row_ix = gptr<int32_t>(cmp_indices) + (int64_t)t * topk;
-#pragma unroll
-                for (int i = 0; i < 2; ++i) ix[i] = tid * 2 + i < topk ? row_ix[tid * 2 + i] : -1;
-            }
-        }
-        prefetched = false;
-        if (tid == 0) s.misc[1] = -1;
-        __syncthreads();                  // also: every wave is done with the previous row's tiles
-        find_request(t, false);
-    }
+    run_row();
 }
 
 // Partition merge as a second launch (merge mode 1): one 512-thread group
@@ -1976,22 +1917,22 @@ void launch_variant(hipStream_t stream, const SharedKVArgs *a, const SharedKVDeb
                            a->batch, a->topk, rows, g2, a->heads, *a);
         return;
     }
-    decltype(&c8_attention<1, false, false, ANYH, false, false, false>) kernel =
-        slots ? &c8_attention<1, DEBUG, true, ANYH, false, false, false>
-              : &c8_attention<1, DEBUG, false, ANYH, false, false, false>;
+    decltype(&c8_attention<1, false, false, ANYH, false, false>) kernel =
+        slots ? &c8_attention<1, DEBUG, true, ANYH, false, false>
+              : &c8_attention<1, DEBUG, false, ANYH, false, false>;
     if (a->ratio == 4 && joint4)
-        kernel = streamed ? &c8_attention<4, DEBUG, false, ANYH, !DEBUG, !DEBUG, false>
-                          : &c8_attention<4, DEBUG, false, ANYH, false, !DEBUG, false>;
+        kernel = streamed ? &c8_attention<4, DEBUG, false, ANYH, !DEBUG, !DEBUG>
+                          : &c8_attention<4, DEBUG, false, ANYH, false, !DEBUG>;
     else if (a->ratio == 4)
-        kernel = slots ? (streamed ? &c8_attention<4, DEBUG, true, ANYH, !DEBUG, false, false>
-                                   : &c8_attention<4, DEBUG, true, ANYH, false, false, false>)
-                       : (streamed ? &c8_attention<4, DEBUG, false, ANYH, !DEBUG, false, false>
-                                   : &c8_attention<4, DEBUG, false, ANYH, false, false, false>);
+        kernel = slots ? (streamed ? &c8_attention<4, DEBUG, true, ANYH, !DEBUG, false>
+                                   : &c8_attention<4, DEBUG, true, ANYH, false, false>)
+                       : (streamed ? &c8_attention<4, DEBUG, false, ANYH, !DEBUG, false>
+                                   : &c8_attention<4, DEBUG, false, ANYH, false, false>);
     else if (a->ratio == 128)
-        kernel = slots ? (streamed ? &c8_attention<128, DEBUG, true, ANYH, !DEBUG, true, false>
-                                   : &c8_attention<128, DEBUG, true, ANYH, false, true, false>)
-                       : (streamed ? &c8_attention<128, DEBUG, false, ANYH, !DEBUG, true, false>
-                                   : &c8_attention<128, DEBUG, false, ANYH, false, true, false>);
+        kernel = slots ? (streamed ? &c8_attention<128, DEBUG, true, ANYH, !DEBUG, true>
+                                   : &c8_attention<128, DEBUG, true, ANYH, false, true>)
+                       : (streamed ? &c8_attention<128, DEBUG, false, ANYH, !DEBUG, true>
+                                   : &c8_attention<128, DEBUG, false, ANYH, false, true>);
     // The leading scalar arguments are the ones the first loads need; the
     // build preloads them into SGPRs (-amdgpu-kernarg-preload-count), so
     // those loads do not wait for a read of the argument block.

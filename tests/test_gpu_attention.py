@@ -274,12 +274,10 @@ def test_joint_c4_rows(mode, heads):
 
 @pytest.mark.parametrize("heads", [8, 12])
 def test_persistent_rows(heads):
-    """One-partition C4 launches of more rows than CUs run work-groups that
-    take rows in turn: with eight heads c8_rows (two four-wave work-groups
-    per CU, up to two rows each here), with twelve heads (two rows per
-    token) the persistent c8_attention (one work-group per CU, up to three
-    rows each, the next row's Q and indices loaded ahead).  Bit-exact with
-    the checker.  The launch mixes a long request, short ones, a request
+    """One-partition C4 launches of more rows than CUs run c8_rows: two
+    four-wave work-groups per CU taking rows in turn (up to two rows each
+    here; twelve heads make two rows per token, the second with four live
+    heads).  Bit-exact with the checker.  The launch mixes a long request, short ones, a request
     listing more query tokens than its sequence length (a keyless row, which
     ends early and loads nothing ahead) and graph-padding rows, so
     work-groups pass between rows with and without keys."""
@@ -748,8 +746,8 @@ def test_one_graph_across_live_batch_and_length_states(ratio):
 
 
 def test_persistent_graph_across_live_states():
-    """A one-partition eight-head C4 launch of more rows than CUs (c8_rows
-    work-groups taking rows in turn) captured at a capacity of 4 requests x 100 query tokens and
+    """A one-partition C4 launch of more rows than CUs (c8_rows work-groups
+    taking rows in turn) captured at a capacity of 4 requests x 100 query tokens and
     replayed twice per live state while the live batch and lengths change
     (4, 2, 1, 0 and 3 live requests).  Outputs and LSE are poisoned with NaN
     before each state; padding rows must come back zero and live rows

@@ -1,8 +1,7 @@
 """Seeded random launches against the CPU checker: mixed ratios, head counts,
 explicit original slots, C4 index modes, short contexts (joint rows),
-prefill-like chunks of 260-400 tokens (work-groups taking rows in turn:
-c8_rows for eight heads, the persistent c8_attention otherwise), graph-capacity
-padding rows, KV partitions (1-8) and both merge placements,
+prefill-like chunks of 260-400 tokens (c8_rows: work-groups taking rows in
+turn), graph-capacity padding rows, KV partitions (1-8) and both merge placements,
 all bit-exact (BF16 outputs) with the checker on the launch's own plan and LSE
 within 2e-6."""
 import os
@@ -34,7 +33,7 @@ def random_case(seed):
     prefill = rng.random() < 0.08
     if prefill:
         # Prefill-like: one long chunk of 260-400 query tokens (a
-        # one-partition eight-head C4 launch of it runs c8_rows).
+        # one-partition C4 launch of it runs c8_rows).
         queries[0] = int(rng.integers(260, 401))
         lengths[0] = int(queries[0] + rng.integers(0, 2500))
     heads = int(rng.choice([8, 8, 8, 4, 12, 16]))
