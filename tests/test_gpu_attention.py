@@ -450,6 +450,22 @@ def test_many_row_decode_launches(batch, tokens):
     compare(dc.host(), bits_of(op.out), op.lse.cpu().numpy(), op.splits, rows=rows, tag=f"{batch} x {tokens}")
 
 
+@pytest.mark.parametrize("heads", [12, 16])
+def test_many_row_decode_launches_with_head_groups(heads):
+    """Decode-shaped C4 launches of more rows than CUs with more than eight
+    heads (rows = tokens x groups of eight heads; non-temporal copies, no
+    residual codes): 64 tokens spread over the launch against the checker."""
+    batch, tokens = 150, 2
+    rng = np.random.default_rng(300 + heads)
+    lengths = [int(x) for x in rng.integers(200, 3000, batch)]
+    case = workloads.make_case(310 + heads, 4, [tokens] * batch, lengths, heads=heads, index_mode="holes")
+    say(f"[many-row decode] {batch} x {tokens}, {heads} heads")
+    out, lse, op = run_hip(case, splits=None)
+    assert op.splits == 1
+    rows = np.linspace(0, batch * tokens - 1, 64).astype(int)
+    compare(case, out, lse, op.splits, rows=rows, tag=f"{heads} heads")
+
+
 @pytest.mark.parametrize("mode,heads", [(0, 8), (1, 8), (0, 12), (1, 12)])
 def test_padded_graph_rows_are_zero_and_guards_hold(mode, heads):
     """Capacity rows past the live tokens (seq_len 0 / cu_q sentinel) are
