@@ -1,9 +1,10 @@
 """The allocation-free attention entry point (launch_sharedkv_c8_noalloc)
 against the allocating one, through the C ABI.
 
-Two calls in a row on the library's per-GPU scratch array, the second with a
-smaller input, each bit-exact with launch_sharedkv_c8_sparse / _dense on the
-same arguments (output and LSE), in both merge placements; a launch whose
+Calls in a row on the library's per-GPU scratch array, each with a smaller
+input than the one before (the first a 300-row launch that runs c8_rows),
+each bit-exact with launch_sharedkv_c8_sparse / _dense on the same
+arguments (output and LSE), in both merge placements; a launch whose
 tickets and partition states exceed the array is rejected before any work.
 """
 import ctypes
@@ -46,12 +47,13 @@ def _launch_both(case, splits):
 def test_no_alloc_entry_equals_allocating_entry(mode):
     from npu_sparse_attn_sharedkv_int8.runtime import library
     lib = library()
+    chunk = workloads.make_case(70, 4, [300], [4000], index_mode="holes")   # c8_rows: more rows than CUs
     big = workloads.make_case(71, 4, [2] * 20, list(range(3000, 3000 + 20 * 900, 900)), index_mode="mixed")
     small = workloads.make_case(72, 128, [1, 2, 1], [900, 5000, 130])
     try:
         assert lib.sharedkv_c8_set_merge_mode(mode) == 0
-        for name, case, splits in (("40 C4 rows, 3 partitions", big, 3), ("4 C128 rows, 2 partitions", small, 2),
-                                   ("4 C128 rows, 1 partition", small, 1)):
+        for name, case, splits in (("300 C4 rows, 1 partition", chunk, 1), ("40 C4 rows, 3 partitions", big, 3),
+                                   ("4 C128 rows, 2 partitions", small, 2), ("4 C128 rows, 1 partition", small, 1)):
             say(f"[no-alloc] merge mode {mode}: {name}")
             (ref, ref_lse), (got, got_lse), _ = _launch_both(case, splits)
             assert np.array_equal(got, ref), name
