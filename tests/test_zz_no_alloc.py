@@ -1,8 +1,8 @@
 """The allocation-free attention entry point (launch_sharedkv_c8_noalloc)
 against the allocating one, through the C ABI.
 
-Calls in a row on the library's per-GPU scratch array, each with a smaller
-input than the one before (the first a 300-row launch that runs c8_rows),
+Calls in a row on the library's per-GPU scratch array, inputs shrinking from
+call to call (300 rows, which run c8_rows, then 40, then 4 twice),
 each bit-exact with launch_sharedkv_c8_sparse / _dense on the same
 arguments (output and LSE), in both merge placements; a launch whose
 tickets and partition states exceed the array is rejected before any work.
