@@ -1964,12 +1964,23 @@ int launch_attention(hipStream_t stream, const SharedKVArgs *a, const SharedKVDe
 }
 
 // ---- scratch of the allocation-free entry point ----
-// One array per GPU, holding the launch's merge tickets (one uint32 per row,
-// 256-byte aligned block) followed by its partition states.  The loader
-// zero-fills it, and every launch leaves the tickets zero again.  Host code
-// never passes the array's name to a kernel: its device address is taken
-// once per device with hipGetSymbolAddress and kept in g_scratch.
+// One array per GPU with a fixed layout: the merge tickets (one uint32 per
+// row) in the first NOALLOC_TICKET_BYTES, the partition states from there to
+// the end.  The two regions never overlap, whatever the row counts of
+// successive launches, so a launch's tickets are never left non-zero by an
+// earlier launch's states: the loader zero-fills the array and every fused
+// launch leaves the tickets it took zero again.  Only launches with more than
+// one partition touch the array at all.  Host code never passes the array's
+// name to a kernel: its device address is taken once per device with
+// hipGetSymbolAddress and kept in g_scratch.
 constexpr uint64_t NOALLOC_SCRATCH_BYTES = 16ull << 20;
+constexpr uint64_t NOALLOC_TICKET_BYTES = 4096;
+constexpr uint64_t NOALLOC_STATE_BYTES = NOALLOC_SCRATCH_BYTES - NOALLOC_TICKET_BYTES;
+// Every row of a merging launch holds at least two partition states, so the
+// rows whose states fit the state region have their tickets in the ticket
+// region.
+static_assert(NOALLOC_STATE_BYTES / (2ull * HEADS * PART_FLOATS * 4) * 4 <= NOALLOC_TICKET_BYTES,
+              "the ticket region covers every launch whose states fit");
 static __device__ __align__(256) uint8_t scratch[NOALLOC_SCRATCH_BYTES];
 
 constexpr int MAX_DEVICES = 64;
@@ -1999,6 +2010,20 @@ uint64_t workspace_bytes(uint32_t rows) { return ((uint64_t)rows * 4 + 255) / 25
 uint64_t partial_bytes(uint32_t rows, uint32_t splits)
 {
     return splits > 1 ? (uint64_t)rows * splits * HEADS * PART_FLOATS * 4 : 0;
+}
+
+// Byte offsets of a launch's tickets and partition states in the
+// allocation-free scratch array (constant: 0 and NOALLOC_TICKET_BYTES);
+// non-zero when the launch does not fit.  One-partition launches use
+// neither region and always fit.
+int noalloc_layout(uint64_t rows, uint32_t splits, uint64_t *tickets, uint64_t *states)
+{
+    *tickets = 0;
+    *states = NOALLOC_TICKET_BYTES;
+    if (rows > UINT32_MAX) return 1;
+    if (splits <= 1) return 0;
+    if (rows * 4 > NOALLOC_TICKET_BYTES || partial_bytes((uint32_t)rows, splits) > NOALLOC_STATE_BYTES) return 1;
+    return 0;
 }
 
 }  // namespace
@@ -2064,20 +2089,24 @@ int launch_sharedkv_c8_noalloc(uint32_t blocks, void *stream, const SharedKVArgs
     if (args->heads == 0 || args->heads > MAX_HEADS || args->splits == 0 || args->splits > MAX_SPLITS)
         return (int)hipErrorInvalidValue;
     const uint64_t rows = (uint64_t)args->tokens * head_groups(args->heads);
-    if (rows > UINT32_MAX) return (int)hipErrorInvalidValue;
-    const uint64_t tickets = workspace_bytes((uint32_t)rows);
-    if (tickets + partial_bytes((uint32_t)rows, args->splits) > NOALLOC_SCRATCH_BYTES)
-        return (int)hipErrorInvalidValue;
+    uint64_t tickets = 0, states = 0;
+    if (noalloc_layout(rows, args->splits, &tickets, &states)) return (int)hipErrorInvalidValue;
     void *base = nullptr;
     const int e = scratch_address(&base);
     if (e) return e;
     SharedKVArgs a = *args;
-    a.workspace = (uint64_t)(uintptr_t)base;
-    a.partial = (uint64_t)(uintptr_t)base + tickets;
+    a.workspace = (uint64_t)(uintptr_t)base + tickets;
+    a.partial = (uint64_t)(uintptr_t)base + states;
     return launch_attention<false>(static_cast<hipStream_t>(stream), &a, nullptr);
 }
 
 uint64_t sharedkv_c8_noalloc_scratch_bytes(void) { return NOALLOC_SCRATCH_BYTES; }
+
+int sharedkv_c8_noalloc_layout(uint32_t rows, uint32_t splits, uint64_t *tickets_offset, uint64_t *states_offset)
+{
+    if (!tickets_offset || !states_offset || splits == 0 || splits > MAX_SPLITS) return (int)hipErrorInvalidValue;
+    return noalloc_layout(rows, splits, tickets_offset, states_offset) ? (int)hipErrorInvalidValue : (int)hipSuccess;
+}
 
 int sharedkv_c8_set_merge_mode(int mode)
 {

@@ -50,7 +50,7 @@ class SharedKVDebug(ctypes.Structure):
 EXPORTS = ("launch_sharedkv_c8_sparse", "launch_sharedkv_c8_dense", "launch_sharedkv_c8_sparse_small",
            "launch_sharedkv_c8_noalloc", "sharedkv_c8_attention_debug", "launch_cache_write",
            "sharedkv_c8_workspace_bytes", "sharedkv_c8_partial_bytes", "sharedkv_c8_noalloc_scratch_bytes",
-           "sharedkv_c8_set_merge_mode", "sharedkv_attention_args_size", "sharedkv_cache_args_size",
+           "sharedkv_c8_noalloc_layout", "sharedkv_c8_set_merge_mode", "sharedkv_attention_args_size", "sharedkv_cache_args_size",
            "sharedkv_abi_version")
 
 
@@ -80,6 +80,9 @@ def library():
         getattr(lib, name).restype = ctypes.c_uint64
     lib.sharedkv_c8_noalloc_scratch_bytes.argtypes = []
     lib.sharedkv_c8_noalloc_scratch_bytes.restype = ctypes.c_uint64
+    lib.sharedkv_c8_noalloc_layout.argtypes = [ctypes.c_uint32, ctypes.c_uint32, ctypes.POINTER(ctypes.c_uint64),
+                                               ctypes.POINTER(ctypes.c_uint64)]
+    lib.sharedkv_c8_noalloc_layout.restype = ctypes.c_int
     lib.sharedkv_c8_set_merge_mode.argtypes = [ctypes.c_int]
     lib.sharedkv_c8_set_merge_mode.restype = ctypes.c_int
     for name in ("sharedkv_attention_args_size", "sharedkv_cache_args_size", "sharedkv_abi_version"):

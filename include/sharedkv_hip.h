@@ -114,13 +114,24 @@ uint64_t sharedkv_c8_partial_bytes(uint32_t rows, uint32_t splits);
  * args->workspace and args->partial are ignored: the merge tickets and
  * partition states live in a library-owned array of
  * sharedkv_c8_noalloc_scratch_bytes() (16 MiB) per GPU, located on the first
- * call on each device (the stream's device must be current).  A launch
- * whose workspace_bytes(rows) + partial_bytes(rows, splits) exceeds it is
- * rejected with hipErrorInvalidValue.  The function calls no hipMalloc or
- * hipFree.  Every call on one GPU uses that GPU's array: calls that may
- * overlap on one GPU (other streams, other threads) race on it. */
+ * call on each device (the stream's device must be current).  The array's
+ * layout is fixed: tickets in its first 4096 bytes (1024 rows), partition
+ * states from byte 4096 on, so launches of any sizes in any order never
+ * find another launch's states where their tickets are.  One-partition
+ * launches use neither region; a launch with splits > 1 whose
+ * partial_bytes(rows, splits) exceeds the state region (16 MiB - 4 KiB: 504
+ * rows at two partitions) is rejected with hipErrorInvalidValue.  The
+ * function calls no hipMalloc or hipFree.  Every call on one GPU uses that
+ * GPU's array: calls that may overlap on one GPU (other streams, other
+ * threads) race on it. */
 int launch_sharedkv_c8_noalloc(uint32_t blocks, void *stream, const SharedKVArgs *args);
 uint64_t sharedkv_c8_noalloc_scratch_bytes(void);
+
+/* Byte offsets of the tickets and the partition states that
+ * launch_sharedkv_c8_noalloc uses for a launch of `rows` rows and `splits`
+ * partitions.  Host-only query (no device call).  Returns 0, or
+ * hipErrorInvalidValue when that launch would be rejected. */
+int sharedkv_c8_noalloc_layout(uint32_t rows, uint32_t splits, uint64_t *tickets_offset, uint64_t *states_offset);
 
 /* Partition merge placement for launches with splits > 1 (process-wide).
  * Mode 0 (default): fused; the last partition of a query row to finish

@@ -38,6 +38,38 @@ def test_library_exports_every_declared_function():
     assert set(runtime.EXPORTS) <= set(names)
 
 
+def _noalloc_layout(lib, rows, splits):
+    tickets, states = ctypes.c_uint64(), ctypes.c_uint64()
+    rc = lib.sharedkv_c8_noalloc_layout(rows, splits, ctypes.byref(tickets), ctypes.byref(states))
+    return rc, tickets.value, states.value
+
+
+def test_noalloc_ticket_and_state_regions_never_overlap():
+    """For any two launches of the allocation-free entry, in either order, no
+    byte holds one launch's merge tickets and the other's partition states
+    (a ticket left non-zero by a state float would never fold its row)."""
+    lib = runtime.library()
+    limit = lib.sharedkv_c8_noalloc_scratch_bytes()
+    per_row = 8 * 520 * 4
+    fits = []
+    for splits in (1, 2, 3, 5, 8, 16):
+        for rows in (1, 4, 20, 63, 64, 65, 100, 255, 256, 257, 300, 503, 504, 505, 1024, 1025, 4096, 1 << 20):
+            rc, tickets, states = _noalloc_layout(lib, rows, splits)
+            if splits == 1:
+                assert rc == 0, (rows, splits)        # one partition: no tickets, no states
+                continue
+            need = rows * splits * per_row
+            assert (rc == 0) == (states + need <= limit), (rows, splits)
+            if rc == 0:
+                assert tickets + 4 * rows <= states, (rows, splits)
+                fits.append((tickets, tickets + 4 * rows, states, states + need))
+    assert _noalloc_layout(lib, 504, 2)[0] == 0 and _noalloc_layout(lib, 505, 2)[0] == 1
+    for t0, t1, _, _ in fits:
+        for _, _, s0, s1 in fits:
+            assert t1 <= s0 or s1 <= t0
+    assert lib.sharedkv_c8_noalloc_layout(4, 0, ctypes.byref(ctypes.c_uint64()), ctypes.byref(ctypes.c_uint64())) == 1
+
+
 def test_argument_blocks_match_reference_layout():
     lib = runtime.library()
     assert lib.sharedkv_attention_args_size() == 200 == ctypes.sizeof(runtime.SharedKVArgs)
