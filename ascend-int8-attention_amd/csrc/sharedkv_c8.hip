@@ -34,10 +34,10 @@
 //   partials   with S > 1 partitions, FP32 [num, max, den] go to `partial`;
 //              the last partition of a row to finish (a ticket per row in
 //              `workspace`) folds them, or c8_merge does in a second launch
-// Eight-head one-partition C4 launches of more rows than CUs (prefill, large
-// decode batches) run c8_rows instead: two four-wave work-groups per CU with
-// one tile buffer each, each taking rows in turn, so that one row's tile
-// chain fills the other's waits.
+// One-partition C4 launches of more rows than CUs (prefill, large decode
+// batches; any head count) run c8_rows instead: two four-wave work-groups per
+// CU with one tile buffer each, each taking rows in turn, so that one row's
+// tile chain fills the other's waits.
 // Integer partials are exact, so any assignment of keys to lanes gives the
 // reference's integers; the FP32 sequence below is kept in the reference's
 // order with contraction disabled.
@@ -1905,8 +1905,7 @@ void launch_variant(hipStream_t stream, const SharedKVArgs *a, const SharedKVDeb
     const bool joint4 = !DEBUG && !slots && a->heads <= HEADS && (uint64_t)a->cmpTableWidth * BLOCK_ROWS <= (uint64_t)N;
     // One-partition C4 launches of more rows than CUs (prefill, large decode
     // batches) run two four-wave work-groups per CU taking rows in turn
-    // (c8_rows).  C128
-    // and window-only launches keep one work-group per row.
+    // (c8_rows).  C128 and window-only launches keep one work-group per row.
     const bool persist = !DEBUG && !slots && a->ratio == 4 && !joint4 && splits == 1 && rows > (uint32_t)PLAN_CUS;
     if (persist) {
         // Two four-wave work-groups per CU (c8_rows), at most one per row, so

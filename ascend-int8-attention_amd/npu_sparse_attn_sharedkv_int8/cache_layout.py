@@ -21,6 +21,13 @@ hooks) is injected: `types` defaults to vLLM's classes when vLLM is
 importable and to the small stand-ins below otherwise, and the allocator
 and the views are plain torch (allocate_backing, page_views) instead of
 hooks into vllm_ascend's NPU runner.
+
+Attribution: the rules above are an allocation format, kept identical so
+that a block ID and a layer offset mean the same thing to both builds.  The
+reference took the common-stride scheme from vllm-ascend's TurboQuant
+planner (vllm_ascend/quantization/methods/kv_cache/turboquant/cache.py,
+SPDX-License-Identifier: Apache-2.0, Copyright contributors to the vLLM
+project); this module restates the format in its own code and messages.
 """
 from dataclasses import dataclass, field, replace
 import logging
@@ -103,73 +110,110 @@ def _specs_of(group_spec):
 
 # --------------------------------------------------------------- planning
 
+def _is_c8_cache(spec):
+    """An INT8 D=512 DeepSeek-V4 attention cache: the kind this path reads."""
+    return (spec.dtype == torch.int8 and getattr(spec, "head_size", None) == 512
+            and getattr(spec, "model_version", None) == "deepseek_v4")
+
+
+def _leaf_specs(groups):
+    """Every per-layer spec of the engine's groups (skipping empty slots)."""
+    for group in groups:
+        spec = None if group is None else getattr(group, "kv_cache_spec", None)
+        if spec is not None:
+            yield from _specs_of(spec)
+
+
 def uses_compact(groups):
     """True when some group holds an INT8 D=512 DeepSeek-V4 cache."""
-    return any(spec.dtype == torch.int8 and getattr(spec, "head_size", None) == 512
-               and getattr(spec, "model_version", None) == "deepseek_v4"
-               for group in groups if group is not None and getattr(group, "kv_cache_spec", None) is not None
-               for spec in _specs_of(group.kv_cache_spec))
+    return any(map(_is_c8_cache, _leaf_specs(groups)))
+
+
+def _without_bucket_padding(spec):
+    """FP32 compressor states keep their values and shapes; the padding that a
+    bucketed allocator added to their page size is dropped."""
+    if spec.dtype == torch.float32 and getattr(spec, "page_size_padded", None) is not None:
+        return replace(spec, page_size_padded=None)
+    return spec
+
+
+def _runs_within(items, budget):
+    """Consecutive runs of (name, spec) whose page bytes sum to at most
+    `budget`; a run always takes at least one item."""
+    run, total = [], 0
+    for name, spec in items:
+        size = spec.page_size_bytes
+        if run and total + size > budget:
+            yield run
+            run, total = [], 0
+        run.append((name, spec))
+        total += size
+    if run:
+        yield run
 
 
 def group_specs(grouped_specs, types=None):
     """Cut the engine's uniform-type spec groups (C4 first, C128 second, then
-    window/state groups) into groups whose page bytes fit the common budget."""
+    window/state groups) into groups whose page bytes fit the common budget.
+    The budget is the larger of the C4 and C128 group pages rounded up to the
+    largest single page, so those two groups are never cut."""
     types = types or default_types()
     if len(grouped_specs) < 2:
         raise ValueError("Expected the C4 and C128 groups first")
-    largest_page = max(spec.page_size_bytes for group in grouped_specs for spec in group.kv_cache_specs.values())
-    budget = round_up(max(grouped_specs[0].page_size_bytes, grouped_specs[1].page_size_bytes), largest_page)
-    groups = []
-
-    def close(chunk):
-        merged = types.uniform.from_specs(chunk)
-        if merged is None:
-            raise ValueError("Incompatible cache specifications in a compact group")
-        groups.append(types.group(list(chunk), merged))
-
-    for original in grouped_specs:
-        chunk, used = {}, 0
-        for name, spec in original.kv_cache_specs.items():
-            # FP32 compressor states keep their values and shapes; only the
-            # padding a bucketed allocator added to their pages is dropped.
-            if spec.dtype == torch.float32 and getattr(spec, "page_size_padded", None) is not None:
-                spec = replace(spec, page_size_padded=None)
-            if chunk and used + spec.page_size_bytes > budget:
-                close(chunk)
-                chunk, used = {}, 0
-            chunk[name] = spec
-            used += spec.page_size_bytes
-        if chunk:
-            close(chunk)
-    return groups
+    largest = max(spec.page_size_bytes for source in grouped_specs for spec in source.kv_cache_specs.values())
+    budget = round_up(max(source.page_size_bytes for source in grouped_specs[:2]), largest)
+    planned = []
+    for source in grouped_specs:
+        items = [(name, _without_bucket_padding(spec)) for name, spec in source.kv_cache_specs.items()]
+        for run in _runs_within(items, budget):
+            members = dict(run)
+            merged = types.uniform.from_specs(members)
+            if merged is None:
+                raise ValueError("Specs cut into one compact group must share one block size")
+            planned.append(types.group(list(members), merged))
+    return planned
 
 
 def alignment_of(spec):
-    alignment = dtype_size(spec.dtype)
+    """Byte alignment of a layer inside a block: its element size, joined
+    (lcm) with the scale element size when it carries scales, and with the
+    512-byte row for INT8 D=512 caches (the kernels address a row as
+    page * stride + slot * 512)."""
+    parts = [dtype_size(spec.dtype)]
     if getattr(spec, "scale_dim", 0):
-        alignment = math.lcm(alignment, dtype_size(spec.scale_dtype))
+        parts.append(dtype_size(spec.scale_dtype))
     if spec.dtype == torch.int8 and getattr(spec, "head_size", None) == 512:
-        alignment = math.lcm(alignment, ROW_BYTES)
-    return alignment
+        parts.append(ROW_BYTES)
+    return math.lcm(*parts)
+
+
+def _place_group(group):
+    """({layer: offset inside a block}, bytes the group uses): layers in
+    descending page size (ties keep the group's order), each at the next
+    multiple of its alignment."""
+    specs = group.kv_cache_spec.kv_cache_specs
+    placed, cursor = {}, 0
+    for name in sorted(group.layer_names, key=lambda n: specs[n].page_size_bytes, reverse=True):
+        if name in placed:
+            raise ValueError(f"Layer {name!r} is listed twice in one compact group")
+        placed[name] = round_up(cursor, alignment_of(specs[name]))
+        cursor = placed[name] + specs[name].page_size_bytes
+    return placed, cursor
 
 
 def packed_layout(groups):
-    """(common block stride in bytes, {layer name: byte offset in a block})."""
-    offsets, maximum = {}, 0
+    """(common block stride in bytes, {layer name: byte offset in a block}).
+    Every group starts at byte 0 of a block; the stride is the largest
+    group's bytes rounded up to whole 512-byte rows."""
+    offsets, widest = {}, 0
     for group in groups:
-        specs = group.kv_cache_spec.kv_cache_specs
-        used = 0
-        for name in sorted(group.layer_names, key=lambda n: -specs[n].page_size_bytes):
-            spec = specs[name]
-            if name in offsets:
-                raise ValueError(f"Cache layer appears in multiple groups: {name}")
-            offset = round_up(used, alignment_of(spec))
-            offsets[name] = offset
-            used = offset + spec.page_size_bytes
-        maximum = max(maximum, used)
-    # The attention kernel addresses a row as page * stride + slot * 512, so
-    # the stride is a whole number of 512-byte rows (FP32 states stay aligned).
-    return round_up(maximum, ROW_BYTES), offsets
+        placed, used = _place_group(group)
+        repeated = offsets.keys() & placed.keys()
+        if repeated:
+            raise ValueError(f"Layer {min(repeated)!r} belongs to more than one compact group")
+        offsets.update(placed)
+        widest = max(widest, used)
+    return round_up(widest, ROW_BYTES), offsets
 
 
 def pool_bytes_per_block(groups):
@@ -177,16 +221,23 @@ def pool_bytes_per_block(groups):
 
 
 def max_memory_usage(config, groups):
-    return pool_bytes_per_block(groups) * sum(group.kv_cache_spec.max_memory_usage_pages(config) for group in groups)
+    pages = sum(group.kv_cache_spec.max_memory_usage_pages(config) for group in groups)
+    return pool_bytes_per_block(groups) * pages
+
+
+_UNSUPPORTED_PARALLELISM = ("pipeline_parallel_size", "decode_context_parallel_size",
+                            "prefill_context_parallel_size")
 
 
 def _check_single_stage(config):
+    """Compact pages serve one local cache per GPU: no pipeline stages, no
+    context parallelism, no KV transfer."""
     parallel = config.parallel_config
-    if any(getattr(parallel, name, 1) != 1 for name in (
-            "pipeline_parallel_size", "decode_context_parallel_size", "prefill_context_parallel_size")):
-        raise ValueError("Compact C8 pages are integrated for single-stage, non-context-parallel serving")
+    wider = [name for name in _UNSUPPORTED_PARALLELISM if getattr(parallel, name, 1) != 1]
+    if wider:
+        raise ValueError(f"Compact C8 pages need single-stage serving without context parallelism ({wider[0]} != 1)")
     if getattr(config, "kv_transfer_config", None) is not None:
-        raise ValueError("KV transfer is not part of this build; compact pages serve local caches only")
+        raise ValueError("Compact C8 pages serve local caches only; KV transfer is not part of this build")
 
 
 def cache_config(config, groups, available_memory, types=None):
@@ -194,38 +245,41 @@ def cache_config(config, groups, available_memory, types=None):
     types = types or default_types()
     _check_single_stage(config)
     stride, offsets = packed_layout(groups)
-    blocks = available_memory // stride
     override = getattr(getattr(config, "cache_config", None), "num_gpu_blocks_override", None)
-    if override is not None:
-        blocks = int(override)
-    size = blocks * stride
-    return blocks, [types.tensor(size=size, layers=[name], offset=offset, layer_stride=0, block_stride=stride)
-                    for name, offset in offsets.items()]
+    blocks = int(override) if override is not None else available_memory // stride
+    return blocks, [types.tensor(size=blocks * stride, layers=[name], offset=offset, layer_stride=0,
+                                 block_stride=stride) for name, offset in offsets.items()]
+
+
+def _descriptor_layer(descriptor, stride, size):
+    """(layer, offset) of a descriptor that covers one layer of the backing."""
+    one_layer = len(descriptor.layers) == 1 and descriptor.layer_stride == 0
+    if not one_layer or descriptor.block_stride != stride or descriptor.size != size:
+        raise ValueError(f"Descriptor {descriptor!r} is not one layer of a {size}-byte backing "
+                         f"with block stride {stride}")
+    return descriptor.layers[0], descriptor.offset
 
 
 def allocate_backing(groups, descriptors, num_blocks, layer_names, device):
     """One INT8 backing for every layer (2 MiB aligned); returns
-    {layer: backing[offset:]} after checking that the descriptors are exactly
-    the planner's (cache_layout.py:114-134)."""
-    stride, offsets = packed_layout(groups)
+    {layer: backing[offset:]}.  The descriptors must be exactly the
+    planner's: one per layer, at the planned offset, stride and size."""
+    stride, planned = packed_layout(groups)
     size = stride * num_blocks
-    actual = {}
+    bound = {}
     for descriptor in descriptors:
-        if (len(descriptor.layers) != 1 or descriptor.layer_stride != 0 or descriptor.block_stride != stride
-                or descriptor.size != size):
-            raise ValueError("Invalid compact C8 backing descriptor")
-        name = descriptor.layers[0]
-        if name in actual or descriptor.offset != offsets.get(name):
-            raise ValueError("Invalid compact C8 layer offset")
-        actual[name] = descriptor.offset
-    if set(actual) != set(layer_names):
-        raise ValueError("Compact C8 descriptor/spec coverage differs")
+        name, offset = _descriptor_layer(descriptor, stride, size)
+        if name in bound or planned.get(name) != offset:
+            raise ValueError(f"Layer {name!r}: descriptor offset {offset} is not the planned one")
+        bound[name] = offset
+    if bound.keys() != set(layer_names):
+        raise ValueError("The descriptors do not cover exactly the cache layers")
     raw = torch.empty(size + BACKING_ALIGNMENT, dtype=torch.int8, device=device)
     start = (-raw.data_ptr()) % BACKING_ALIGNMENT
     backing = raw[start:start + size]
-    logging.getLogger(__name__).info("Compact INT8 sharedKV: %d blocks, %d bytes/block, %d groups, one %d-byte backing",
-                                     num_blocks, stride, len(groups), size)
-    return {name: backing[offset:] for name, offset in actual.items()}
+    logging.getLogger(__name__).info("compact C8 backing of %d bytes: %d layers in %d groups, %d blocks of %d bytes",
+                                     size, len(bound), len(groups), num_blocks, stride)
+    return {name: backing[offset:] for name, offset in bound.items()}
 
 
 def page_views(raw, shapes, dtypes, stride):
