@@ -8,14 +8,24 @@ INT8 block32 pages at the serving page stride (622592 B) in a pool sized 1.25x
 the need with shuffled block tables.  Synthetic data generated on the GPU.
 
 A step is one attention launch (one layer of one decode step).  Steps rotate
-over `--layers` layers whose pages interleave in the 622592-B page stride the
-way a serving pool holds every layer's 16 KiB page, so consecutive steps read
-different HBM (the union of bytes read per rotation exceeds the 256 MB MALL).
-The K timed steps are one captured HIP graph replay (serving runs decode in
-graphs); W warmup steps run eagerly before it and the graph is replayed once
-untimed.  Kernel time per launch = HIP-event time of the replay / K, on the
-replay stream.  The CPU baseline is the C restatement (oracle/, "port")
-timed on a bounded sample on this host, rank 0 only.
+over `--layers` layers (32 by default: over 1 GiB of distinct rows) whose
+pages interleave in the 622592-B page stride the way a serving pool holds
+every layer's 16 KiB page, so consecutive steps read different HBM (the
+union of bytes read per rotation is four times the 256 MB MALL).  The K
+timed steps are one captured HIP graph of K launches (serving runs decode in
+graphs).  Protocol of the reference's capacity benchmark
+(tests/npu/test_capacity.py:166-190 of the reference checkout): W eager
+warmup launches, then the graph and its companions (below) are each
+replayed 3 times untimed, then 9 rounds in alternating order each replay
+every graph once between HIP events on the replay stream; the reported time
+per launch is the median over the 9 rounds of (round time / K).
+Companions, timed in the same rounds: the launch's data-movement floor
+(csrc/gather_floor.hip: the exact rows each work item of the launch
+gathers, copied into LDS with the same instructions, grid and two-tile
+ring, with no metadata round trips, compute or merge), and a streaming read
+of the same byte count through the same kernel.  The CPU baseline is the C
+restatement (oracle/, "port") timed on a bounded sample on this host, rank 0
+only.
 
 Prints ONE JSON line on stdout; progress goes to stderr.
 """
@@ -124,19 +134,10 @@ def bench_writer(args, torch):
     with torch.cuda.stream(stream):
         for i in range(args.warmup):
             ops[i % layers].run()
-        torch.cuda.synchronize()
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, stream=stream):
-            for i in range(args.steps):
-                ops[i % layers].run()
-        graph.replay()
-        torch.cuda.synchronize()
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        start.record(stream)
-        graph.replay()
-        end.record(stream)
-        torch.cuda.synchronize()
-    ms_per_step = start.elapsed_time(end) / args.steps
+    torch.cuda.synchronize()
+    graph = capture(stream, args.steps, lambda i: ops[i % layers].run(), torch)
+    medians, samples = timed_rounds({"writer": graph}, stream, args.steps, torch)
+    ms_per_step = medians["writer"] / 1e3
     algorithmic = rows * (512 * 2 + 512 + 4) + 512 * 4
     achieved = algorithmic / (ms_per_step * 1e-3) / 1e9
     traffic, traffic_source = recorded_traffic("cfg4_writer")
@@ -146,8 +147,10 @@ def bench_writer(args, torch):
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "i8",
         "data": "synthetic (GPU-generated, seeded)",
         "config": {"workload": "config 4 writer: 4096 BF16 rows, random unique int32 slots, page stride 622592",
-                   "rows": rows, "pages": pages, "page_stride": stride, "layers_rotated": layers},
+                   "rows": rows, "pages": pages, "page_stride": stride, "layers_rotated": layers,
+                   "timing": "median of 9 rounds, each one replay of a graph of K launches between HIP events"},
         "latency_us_per_launch": ms_per_step * 1e3,
+        "rounds_us_per_launch": samples["writer"],
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": achieved / PEAK_HBM_GBS, "traffic": traffic, "traffic_source": traffic_source,
                      "algorithmic_bytes_per_launch": algorithmic},
@@ -156,6 +159,160 @@ def bench_writer(args, torch):
         log(f"[bench] writer CPU baseline ({args.cpu_seconds:.0f} s sample)")
         record["cpu_baseline"] = writer_cpu_baseline(rows, pages, stride, args.cpu_seconds)
     return record
+
+
+def launch_rows(dc, layer, plan):
+    """Per work item (query row, partition) of a tiled launch at `plan`
+    partitions, the HBM row addresses it gathers, tile by tile, in the
+    kernel's selection order: the SWA window rows, then the compressed list
+    (C4: the valid top-k entries, compacted when the visible range is
+    shorter than top-k, masked holes in place otherwise; C128: every visible
+    compressed row), cut into 128-key tiles, tile k on partition k % plan.
+    Masked places read the Q base, as the kernel's do.  Returns (addresses
+    INT64 [items, max tiles, 128], tiles INT32 [items], bounds) where bounds
+    lists the (low, high) byte ranges every address falls in."""
+    import numpy as np
+    m = dc.meta
+    ratio, window, topk = m["ratio"], m["window"], m["topk"]
+    pos_all, owner = m["positions"], m["owner"]
+    q_base = dc.cases[layer].q.data_ptr()
+    kinds = [(dc.ori, dc.ori.flat.data_ptr() + layer * dc.ori.PAGE_BYTES)]
+    if dc.cmp is not None:
+        kinds.append((dc.cmp, dc.cmp.flat.data_ptr() + layer * dc.cmp.PAGE_BYTES))
+    rows = []
+    for t, pos in enumerate(pos_all):
+        b = int(owner[t])
+        first = max(0, int(pos) + 1 - window)
+        idx = np.arange(first, int(pos) + 1)
+        lists = [(0, idx, np.ones(len(idx), bool))]
+        count = (int(pos) + 1) // ratio if ratio != 1 else 0
+        if ratio == 4:
+            ix = dc.indices[layer][t, 0].astype(np.int64)
+            ok = (ix >= 0) & (ix < count)
+            if count < topk <= 1024:
+                lists.append((1, ix[ok], np.ones(int(ok.sum()), bool)))
+            else:
+                lists.append((1, np.where(ok, ix, 0), ok))
+        elif ratio == 128:
+            lists.append((1, np.arange(count), np.ones(count, bool)))
+        tiles = []
+        for kind, ids, ok in lists:
+            pool, base = kinds[kind]
+            page = pool.table[b][ids // 32].astype(np.int64)
+            addr = base + page * pool.page_stride + (ids % 32) * 512
+            addr = np.where(ok, addr, q_base)
+            for start in range(0, len(ids), 128):
+                tile = np.full(128, q_base, np.int64)
+                chunk = addr[start:start + 128]
+                tile[:len(chunk)] = chunk
+                tiles.append(tile)
+        rows.append(tiles)
+    items = [[tiles[k] for k in range(part, len(tiles), plan)] for tiles in rows for part in range(plan)]
+    max_tiles = max(1, max(len(x) for x in items))
+    out = np.zeros((len(items), max_tiles, 128), np.int64)
+    counts = np.zeros(len(items), np.int32)
+    for i, tiles in enumerate(items):
+        counts[i] = len(tiles)
+        for k, tile in enumerate(tiles):
+            out[i, k] = tile
+    bounds = [(q_base, q_base + 512)] + [(base, base + pool.pages * pool.page_stride) for pool, base in kinds]
+    return out, counts, bounds
+
+
+class FloorLegs:
+    """The two companion legs of the timed rounds (csrc/gather_floor.hip,
+    _native/libsharedkv_floor.so): `gather` copies each work item's rows of
+    the attention launch (launch_rows, per layer) and `stream` reads the same
+    number of bytes contiguously, with the same kernel, grid and ring.  Every
+    address is checked on the host to lie inside the pool it names before
+    any launch."""
+
+    def __init__(self, dc, layers, plan, torch, non_temporal):
+        import ctypes
+        import numpy as np
+        from npu_sparse_attn_sharedkv_int8._paths import NATIVE_DIR
+        self.lib = ctypes.CDLL(str(NATIVE_DIR / "libsharedkv_floor.so"))
+        self.lib.sharedkv_floor_gather.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                                   ctypes.c_uint32, ctypes.c_uint32, ctypes.c_int]
+        self.lib.sharedkv_floor_gather.restype = ctypes.c_int
+        self.nt = int(bool(non_temporal))
+        self.gather, self.stream = [], []
+        self.keep = []
+        for layer in range(layers):
+            addrs, tiles, bounds = launch_rows(dc, layer, plan)
+            flat = addrs.reshape(-1, 128)
+            live = np.repeat(np.arange(addrs.shape[1])[None, :], len(tiles), 0) < tiles[:, None]
+            used = addrs[live].reshape(-1)
+            inside = np.zeros(used.shape, bool)
+            for lo, hi in bounds:
+                inside |= (used >= lo) & (used + 512 <= hi)
+            if not inside.all():
+                raise SystemExit("floor leg: a row address falls outside its pool")
+            self.gather.append((torch.from_numpy(addrs).cuda(), torch.from_numpy(tiles).cuda(), len(tiles),
+                                addrs.shape[1]))
+            del flat
+        # Streaming read: each layer's tile count of contiguous 64 KiB tiles in
+        # one buffer, layers one after another.
+        tiles0 = self.gather[0][1].cpu().numpy()
+        per_layer = int(tiles0.sum())
+        self.bytes_per_launch = per_layer * 128 * 512
+        self.buffer = torch.empty(layers * self.bytes_per_launch, dtype=torch.int8, device="cuda")
+        base = self.buffer.data_ptr()
+        for layer in range(layers):
+            _, tiles_dev, items, max_tiles = self.gather[layer]
+            tiles = tiles_dev.cpu().numpy()
+            first = np.concatenate(([0], np.cumsum(tiles)[:-1]))
+            k = first[:, None] + np.arange(max_tiles)[None, :]
+            addrs = (base + layer * self.bytes_per_launch
+                     + (k[:, :, None] * 128 + np.arange(128)[None, None, :]) * 512).astype(np.int64)
+            addrs = np.where((np.arange(max_tiles)[None, :] < tiles[:, None])[:, :, None], addrs, base)
+            self.stream.append((torch.from_numpy(addrs).cuda(), tiles_dev, items, max_tiles))
+
+    def launch(self, which, layer, torch):
+        addrs, tiles, items, max_tiles = (self.gather if which == "gather" else self.stream)[layer]
+        rc = self.lib.sharedkv_floor_gather(torch.cuda.current_stream().cuda_stream, addrs.data_ptr(),
+                                            tiles.data_ptr(), items, max_tiles, self.nt)
+        if rc:
+            raise RuntimeError(f"floor launch failed: {rc}")
+
+
+def timed_rounds(graphs, stream, depth, torch, rounds=9, warm=3):
+    """The reference's paired timing (test_capacity.py:166-190): every graph
+    replayed `warm` times, then `rounds` rounds, each replaying every graph
+    once in an order that rotates and reverses from round to round, between
+    HIP events on `stream`.  Returns ({name: median us per launch},
+    {name: [us per launch of each round]})."""
+    import statistics
+    names = list(graphs)
+    with torch.cuda.stream(stream):
+        for _ in range(warm):
+            for graph in graphs.values():
+                graph.replay()
+        torch.cuda.synchronize()
+        samples = {name: [] for name in names}
+        for r in range(rounds):
+            order = names[r % len(names):] + names[:r % len(names)]
+            if r % 2:
+                order = order[::-1]
+            for name in order:
+                a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                torch.cuda.synchronize()
+                a.record(stream)
+                graphs[name].replay()
+                b.record(stream)
+                b.synchronize()
+                samples[name].append(a.elapsed_time(b) * 1e3 / depth)
+    return {name: statistics.median(v) for name, v in samples.items()}, samples
+
+
+def capture(stream, steps, launch, torch):
+    """A HIP graph of `steps` calls launch(i) captured on `stream`."""
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(stream):
+        with torch.cuda.graph(graph, stream=stream):
+            for i in range(steps):
+                launch(i)
+    return graph
 
 
 def host_cores():
@@ -276,7 +433,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=160)
     ap.add_argument("--warmup", type=int, default=32)
-    ap.add_argument("--layers", type=int, default=16, help="layers rotated over (<= 38 in the page stride)")
+    ap.add_argument("--layers", type=int, default=32, help="layers rotated over (<= 38 in the page stride)")
     ap.add_argument("--workload", default="headline", choices=WORKLOADS)
     ap.add_argument("--splits", type=int, default=None, help="override the host plan's KV partitions")
     ap.add_argument("--page-stride", type=int, default=None, help="override the workload's page stride (bytes)")
@@ -284,6 +441,7 @@ def main():
     ap.add_argument("--heads", type=int, default=8, help="query heads per token (the metric is quoted at 8)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-floor", action="store_true", help="skip the gather-floor and streaming-read legs")
     ap.add_argument("--live", type=int, default=None, metavar="SEQS",
                     help="also replay the captured graph with only SEQS sequences live (graph padding; the "
                          "kernel re-plans partitions on the device); default 8 for the headline, 0 = skip")
@@ -343,26 +501,42 @@ def main():
         log(f"[bench] warmup {args.warmup} eager launches (splits={splits})")
         for i in range(args.warmup):
             ops[i % layers].run()
-        torch.cuda.synchronize()
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph, stream=stream):
-            for i in range(args.steps):
-                ops[i % layers].run()
-        graph.replay()                      # untimed first replay (graph upload)
-        torch.cuda.synchronize()
-        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        wall0 = time.perf_counter()
-        start.record(stream)
-        graph.replay()
-        end.record(stream)
-        torch.cuda.synchronize()
-        wall = time.perf_counter() - wall0
-    event_ms = start.elapsed_time(end)
-    ms_per_step = event_ms / args.steps
-    log(f"[bench] {args.steps} steps: {event_ms:.3f} ms by events, {wall * 1e3:.3f} ms wall")
+    torch.cuda.synchronize()
+    graphs = {"attention": capture(stream, args.steps, lambda i: ops[i % layers].run(), torch)}
+    tokens = int(dc.meta["cu_q"][-1])
+    joint = device_plan == 1 and c8_attention.joint_launch(splits, tokens, args.heads, ratio, dc.meta["cu_q"],
+                                                           dc.meta["seq_lens"], cmp_rows=cmp_rows)
+    rows_kernel = ratio == 4 and device_plan == 1 and tokens * ((args.heads + 7) // 8) > c8_attention.CORES
+    floor = None
+    if not args.no_floor and args.heads == 8 and not joint and not rows_kernel:
+        streamed = tokens <= (4 if ratio == 4 else 1 if ratio == 128 else 0) * len(queries)
+        log(f"[bench] floor legs: gather of the launch's rows and a streaming read (non-temporal {streamed})")
+        floor = FloorLegs(dc, layers, device_plan, torch, streamed)
+        graphs["gather_floor"] = capture(stream, args.steps, lambda i: floor.launch("gather", i % layers, torch),
+                                         torch)
+        graphs["stream_read"] = capture(stream, args.steps, lambda i: floor.launch("stream", i % layers, torch),
+                                        torch)
+    wall0 = time.perf_counter()
+    medians, samples = timed_rounds(graphs, stream, args.steps, torch)
+    wall = time.perf_counter() - wall0
+    ms_per_step = medians["attention"] / 1e3
+    log(f"[bench] 9 rounds x {len(graphs)} graphs of {args.steps} launches in {wall * 1e3:.1f} ms wall; "
+        + ", ".join(f"{k} {v:.2f} us" for k, v in medians.items()))
     mean_bytes = sum(bytes_per_launch[i % layers] for i in range(args.steps)) / args.steps
     achieved = mean_bytes / (ms_per_step * 1e-3) / 1e9
+    floor_record = None
+    if floor is not None:
+        floor_record = {
+            "gather_us": medians["gather_floor"], "stream_read_us": medians["stream_read"],
+            "attention_us": medians["attention"], "bytes_per_launch": floor.bytes_per_launch,
+            "gather_gbs": floor.bytes_per_launch / (medians["gather_floor"] * 1e-6) / 1e9,
+            "stream_read_gbs": floor.bytes_per_launch / (medians["stream_read"] * 1e-6) / 1e9,
+            "gather_frac_of_peak_algorithmic": mean_bytes / (medians["gather_floor"] * 1e-6) / 1e9 / PEAK_HBM_GBS,
+            "note": "same 9 alternating rounds as the attention graph; gather = every row the launch's work items "
+                    "copy (tiles of 128 x 512 B, masked places included), with the launch's grid, item order, "
+                    "LDS DMA instruction and two-tile ring but no metadata round trips, compute or merge "
+                    "(csrc/gather_floor.hip); stream_read = the same byte count read contiguously by the "
+                    "same kernel"}
 
     # HBM bytes per launch measured with rocprofv3 FETCH_SIZE / WRITE_SIZE
     # (scaled by a plain copy's reading); the summary states the commands.
@@ -374,35 +548,48 @@ def main():
     live_seqs = args.live if args.live is not None else (8 if args.workload == "headline" else 0)
     padded = None
     if 0 < live_seqs < len(queries) and args.merge == 0:
+        import dataclasses
         cu_full, lens_full = dc.meta["cu_q"].copy(), dc.meta["seq_lens"].copy()
         cu = cu_full.copy()
         cu[live_seqs + 1:] = cu_full[live_seqs]
         lens = lens_full.copy()
         lens[live_seqs:] = 0
+        live_rows = int(cu[live_seqs])
         padded_plan = c8_attention.device_splits(splits, int(cu_full[-1]), args.heads, ratio, 1024, cu, lens,
                                                  cmp_rows=cmp_rows)
+        # The same layers' launches planned for the live sequences alone.
+        live_ops = []
+        for l in range(layers):
+            c = dc.cases[l]
+            live_case = dataclasses.replace(
+                c, q=c.q[:live_rows], cu_q=c.cu_q[:live_seqs + 1], seq_lens=c.seq_lens[:live_seqs],
+                ori_block_table=c.ori_block_table[:live_seqs],
+                cmp_block_table=c.cmp_block_table[:live_seqs] if c.cmp_block_table is not None else None,
+                cmp_indices=c.cmp_indices[:live_rows] if c.cmp_indices is not None else None)
+            live_ops.append(PreparedAttention(live_case, dc.ori_scales[l], dc.cmp_scales[l]))
+        with torch.cuda.stream(stream):
+            for i in range(layers):
+                live_ops[i].run()
+        torch.cuda.synchronize()
+        live_graph = capture(stream, args.steps, lambda i: live_ops[i % layers].run(), torch)
         dc.dev.cu_q.copy_(torch.from_numpy(cu))
         dc.dev.seq_lens.copy_(torch.from_numpy(lens))
         torch.cuda.synchronize()
-        with torch.cuda.stream(stream):
-            graph.replay()
-            torch.cuda.synchronize()
-            p0, p1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            p0.record(stream)
-            graph.replay()
-            p1.record(stream)
-            torch.cuda.synchronize()
+        pad_medians, _ = timed_rounds({"padded": graphs["attention"], "live_only": live_graph}, stream, args.steps,
+                                      torch)
         dc.dev.cu_q.copy_(torch.from_numpy(cu_full))
         dc.dev.seq_lens.copy_(torch.from_numpy(lens_full))
         torch.cuda.synchronize()
-        us = p0.elapsed_time(p1) / args.steps * 1e3
-        live_rows = int(cu[live_seqs])
+        us, live_us = pad_medians["padded"], pad_medians["live_only"]
         padded = {"capacity_sequences": len(queries), "live_sequences": live_seqs, "live_queries": live_rows,
                   "launch_splits": splits, "device_splits": padded_plan, "us_per_launch": us,
-                  "queries_per_s": live_rows / (us * 1e-6),
-                  "note": "the timed graph replayed with the sequences past the live ones at seq_len 0"}
+                  "queries_per_s": live_rows / (us * 1e-6), "live_only_us_per_launch": live_us,
+                  "live_only_splits": live_ops[0].splits, "padded_over_live_only": us / live_us,
+                  "note": "the timed graph replayed with the sequences past the live ones at seq_len 0, against a "
+                          "graph of the same layers' launches planned for the live sequences alone; medians of 9 "
+                          "alternating rounds"}
         log(f"[bench] padded graph: {live_seqs} of {len(queries)} sequences live, {padded_plan} partitions, "
-            f"{us:.2f} us per launch")
+            f"{us:.2f} us per launch; the live rows alone: {live_us:.2f} us ({live_ops[0].splits} partitions)")
 
     eager = eager_latency(ops[0], stream, torch)
     log(f"[bench] eager: kernel {eager['kernel_us_median']:.2f} us, call {eager['call_us_median']:.2f} us")
@@ -425,7 +612,8 @@ def main():
                        splits, int(dc.meta["cu_q"][-1]), args.heads, ratio, dc.meta["cu_q"], dc.meta["seq_lens"],
                        cmp_rows=cmp_rows)),
                    "lse": False, "merge": "fused" if args.merge == 0 else "separate launch",
-                   "timing": "one HIP graph replay of K launches, HIP events on its stream"},
+                   "timing": "median of 9 alternating rounds (reference protocol), each one replay of a graph of "
+                             "K launches between HIP events on its stream, after 3 untimed replays"},
         "latency_us_per_layer": ms_per_step * 1e3,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                      "frac": achieved / PEAK_HBM_GBS, "traffic": traffic, "traffic_source": traffic_source,
@@ -433,7 +621,10 @@ def main():
         "mfma": {"int8_ops_per_launch": int8_ops, "achieved_tops": int8_ops / (ms_per_step * 1e-3) / 1e12,
                  "peak_tops": 5000.0, "frac": int8_ops / (ms_per_step * 1e-3) / 1e12 / 5000.0},
         "eager_latency": eager,
+        "rounds_us_per_launch": samples["attention"],
     }
+    if floor_record:
+        record["floor"] = floor_record
     if padded:
         record["padded_graph"] = padded
     copy_calibration(args.copy_calibration, torch)
