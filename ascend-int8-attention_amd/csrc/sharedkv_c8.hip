@@ -574,10 +574,26 @@ c8_attention(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base
         plan = plan < tiles ? plan : tiles;
         plan = plan < room ? plan : room;
         plan = plan > S ? plan : S;
-        if (item >= (uint32_t)(live_rows * plan)) return;
-        const int32_t row = (int32_t)(item / (uint32_t)plan);
+        // Placement of the live work items: every XCD takes a contiguous
+        // eighth of the live rows (rows [x R / 8, (x + 1) R / 8) on XCD x,
+        // each with all its partitions), so that a padded launch spreads
+        // over the whole chip like an eager launch of its live rows, when
+        // every XCD has the work-groups for its share (the fullest XCD holds
+        // ceil(R / 8) rows; XCD 7 loses the grid's rounding work-groups);
+        // otherwise item i takes row i / plan on the launch's own order.
+        int32_t row;
+        const int32_t per_xcd = (int32_t)(G >> 3), usable = per_xcd - (int32_t)(G - items);
+        if ((live_rows + 7) / 8 * plan <= usable) {
+            const int32_t x = (int32_t)(blockIdx.x & 7u), j = (int32_t)(blockIdx.x >> 3);
+            row = x * live_rows / 8 + j / plan;
+            if (row >= (x + 1) * live_rows / 8) return;
+            part = j % plan;
+        } else {
+            if (item >= (uint32_t)(live_rows * plan)) return;
+            row = (int32_t)(item / (uint32_t)plan);
+            part = (int32_t)(item % (uint32_t)plan);
+        }
         S = plan;
-        part = (int32_t)(item % (uint32_t)plan);
         if (row != qrow) {
             // The work item moved to another row: load that row's Q and indices.
             qrow = row;
@@ -1397,7 +1413,12 @@ c8_merge(const SharedKVArgs p, uint32_t splits)
 // The same numerics as c8_attention with one partition (128-key tiles,
 // reference.py:210-323), laid out so that two work-groups share a CU: four
 // waves and one tile buffer each (80 KiB of LDS), each work-group taking rows
-// r, r + grid, ... in turn.  A row's tiles are a chain (QK -> tile maximum ->
+// r, r + grid, ... in turn.  When graph padding leaves fewer live rows than
+// the launch's capacity and the launch may merge (`fused`: partition states
+// and tickets supplied), the live rows are re-planned as c8_attention
+// re-plans them (the same rule, so the same partitions and numerics): each
+// work item is a (row, partition) pair, every XCD takes a contiguous eighth
+// of the live rows, and the last partition of a row folds the states.  A row's tiles are a chain (QK -> tile maximum ->
 // exponentials and P codes -> PV) through work-group barriers; with one row
 // per CU nothing fills those waits, with two rows per CU the other work-group
 // computes while this one waits for its barrier or its next tile.  Each wave
@@ -1430,15 +1451,16 @@ template <bool STREAM, bool ANYH>
 __global__ void __launch_bounds__(ROWS_THREADS, 2)
 c8_rows(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, const uint64_t cmp_indices,
         const uint32_t batch_arg, const uint32_t topk_arg, const uint32_t rows_arg, const uint32_t grid,
-        const uint32_t heads_arg, const SharedKVArgs p)
+        const uint32_t heads_arg, const SharedKVArgs p, const uint32_t fused)
 {
     __shared__ RowsShared s;
     const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, n = lane & 15;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // scalar: copy destinations on the SALU
     // XCD-aware order: consecutive rows stay on one XCD (their windows overlap).
     const uint32_t G = grid;
-    int32_t qrow = (int32_t)((blockIdx.x & 7u) * (G >> 3) + (blockIdx.x >> 3));
-    if (qrow >= (int32_t)rows_arg) return;
+    // (Work-groups past the rows still take part: a re-planned launch hands
+    // out its items per XCD.)
+    const int32_t first_row = (int32_t)((blockIdx.x & 7u) * (G >> 3) + (blockIdx.x >> 3));
     const __attribute__((address_space(1))) int32_t *cu = gptr<int32_t>(cu_q);
     const __attribute__((address_space(1))) int32_t *lens = gptr<int32_t>(seq_lens);
     const int batch_n = (int)batch_arg, topk = (int)topk_arg;
@@ -1459,8 +1481,40 @@ c8_rows(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, con
         *gptr<f32x4>(((tid >> 7) ? p.cmpScale : p.oriScale) + (uint64_t)((tid & 127) * 4) * 4);
     const int c0 = 128 * wave;   // this wave's PV output columns: c0 + 16 j + n
 
-    for (;; qrow += (int32_t)G) {
-        if (qrow >= (int32_t)rows_arg) return;
+    // ---- device plan of a padded launch (c8_attention's rule) ----
+    const int32_t rows_cap = (int32_t)rows_arg, live_rows = live_tokens * HG;
+    int32_t S = 1;
+    const bool replan = fused && live_rows > 0 && live_rows < rows_cap;
+    if (replan) {
+        if (tid == 0) s.misc[6] = 0;
+        __syncthreads();
+        for (int b = tid; b < live_batch; b += ROWS_THREADS) atomicMax(&s.misc[6], lens[b]);
+        __syncthreads();
+        const int longest = uni(s.misc[6]);
+        const int cnt = longest / 4 < topk ? longest / 4 : topk;
+        const int32_t tiles = 1 + (cnt + N - 1) / N;
+        int32_t plan = live_rows * PLAN_FEW <= PLAN_CUS ? PLAN_FEW : PLAN_MANY;
+        const int32_t fit = PLAN_CUS / live_rows > 1 ? PLAN_CUS / live_rows : 1;
+        const int32_t room = rows_cap / live_rows;
+        plan = plan < fit ? plan : fit;
+        plan = plan < tiles ? plan : tiles;
+        plan = plan < room ? plan : room;
+        S = plan > 1 ? plan : 1;
+        // Padding rows [live_rows, rows_cap) are zero (attention_impl.h:443-460).
+        for (int32_t pad = live_rows + first_row; pad < rows_cap; pad += (int32_t)G) {
+            const int32_t pt = ANYH ? pad / HG : pad, ph = ANYH ? HEADS * (pad % HG) : 0;
+            const int pl = ANYH ? (H - ph < HEADS ? H - ph : HEADS) : HEADS;
+            uint16_t *o = reinterpret_cast<uint16_t *>(p.out) + ((int64_t)pt * H + ph) * D;
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+                if (!ANYH || tid + ROWS_THREADS * i < pl * (D / 8))
+                    reinterpret_cast<v4i *>(o)[tid + ROWS_THREADS * i] = v4i{0, 0, 0, 0};
+            if (p.lse && tid < pl) reinterpret_cast<float *>(p.lse)[(int64_t)pt * H + ph + tid] = 0.0f;
+        }
+    }
+
+    // Work item (query row qrow, partition part of S).
+    auto run_item = [&](const int32_t qrow, const int32_t part) {
         const int t = ANYH ? qrow / HG : qrow;                   // token
         const int hbase = ANYH ? HEADS * (qrow % HG) : 0;        // first head of the row
         const int hlive = ANYH ? (H - hbase < HEADS ? H - hbase : HEADS) : HEADS;
@@ -1479,7 +1533,7 @@ c8_rows(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, con
         const __attribute__((address_space(1))) int32_t *row_ix = gptr<int32_t>(cmp_indices) + (int64_t)t * topk;
 #pragma unroll
         for (int e = 0; e < ROWS_IX; ++e) ix[e] = tid * ROWS_IX + e < topk ? row_ix[tid * ROWS_IX + e] : -1;
-        __syncthreads();   // every wave is done with the previous row's shared data
+        __syncthreads();   // every wave is done with the previous item's shared data
         if (tid == 0) s.misc[1] = -1;
         __syncthreads();
         for (int b = tid; b < live_batch; b += ROWS_THREADS) {
@@ -1496,12 +1550,13 @@ c8_rows(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, con
         // Padding rows of a captured graph (attention_impl.h:443-460) and rows
         // with a negative position (reference.py:104-105 rejects them) are zero.
         if (t >= live_tokens || batch < 0 || position < 0) {
+            if (part != 0) return;
 #pragma unroll
             for (int i = 0; i < 2; ++i)
                 if (!ANYH || tid + ROWS_THREADS * i < hlive * (D / 8))
                     reinterpret_cast<v4i *>(out_row)[tid + ROWS_THREADS * i] = v4i{0, 0, 0, 0};
             if (lse_row && tid < hlive) lse_row[tid] = 0.0f;
-            continue;
+            return;
         }
 
         // ---- selection (attention_impl.h:58-73, reference.py:228-253) ----
@@ -1553,6 +1608,11 @@ c8_rows(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, con
             for (int e = 0; e < ROWS_IX; ++e) ipos[e] = ok[e] ? tid * ROWS_IX + e : -1;
         }
         const int tiles = 1 + (list_len + N - 1) / N;   // window tile, then compressed tiles
+        // Tile k belongs to partition k % S (the window tile to partition 0);
+        // partitions that own no tile hold the initial state, which folds to
+        // nothing, and publish nothing.
+        if (part >= tiles) return;
+        const int folded = S < tiles ? S : tiles;
 
         // ---- row addresses of every tile (masked rows: the Q base, never used) ----
         for (int i = tid; i < tiles * N; i += ROWS_THREADS) s.addr[i] = p.q;
@@ -1568,7 +1628,7 @@ c8_rows(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, con
         // Staged in the tile buffer, then picked up in the MFMA A layout.
         v4i qa0[8], qa1[8];
         {
-            const int want = tiles > 1 ? 2 : 1;
+            const int want = (part == 0 ? S : part) < tiles ? 2 : 1;   // a compressed tile in this item
             const int qe0 = lane * 8;
 #pragma unroll
             for (int kind = 0; kind < 2; ++kind) {
@@ -1616,7 +1676,8 @@ c8_rows(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, con
 
         // ---- tiles (reference.py:280-316 with one partition) ----
         const __attribute__((address_space(1))) float *sinks = gptr<float>(p.sinks);
-        float mx[2], den[2] = {1.0f, 1.0f}, num[2][8];
+        const float den0 = part == 0 ? 1.0f : 0.0f;   // the sink's exp(sink - max) starts partition 0
+        float mx[2], den[2] = {den0, den0}, num[2][8];
         mx[0] = (!ANYH || 2 * g < hlive) ? sinks[hbase + 2 * g] : 0.0f;
         mx[1] = (!ANYH || 2 * g + 1 < hlive) ? sinks[hbase + 2 * g + 1] : 0.0f;
 #pragma unroll
@@ -1785,8 +1846,15 @@ c8_rows(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, con
             if (!STREAM) __builtin_amdgcn_s_setprio(0);
             lds_barrier();   // every wave is done with tile k and the P codes
         };
-        run_tile(0, qa0);
-        for (int k = 1; k < tiles; ++k) run_tile(k, qa1);
+        // The item's first tile (the window tile on partition 0) takes the Q
+        // codes of its kind; the rest are compressed tiles.
+        {
+            v4i qf[8];
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj) qf[jj] = part == 0 ? qa0[jj] : qa1[jj];
+            run_tile(part, qf);
+        }
+        for (int k = part + S; k < tiles; k += S) run_tile(k, qa1);
         if (held) {
 #pragma unroll
             for (int hh = 0; hh < 2; ++hh)
@@ -1798,16 +1866,56 @@ c8_rows(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, con
                     num[hh][j] = num[hh][j] * held_factor[hh] + pv;
                 }
         }
-        // ---- finalize (reference.py:317-323 with one partition) ----
+        if (folded == 1) {
+            // ---- finalize (reference.py:317-323 with one partition) ----
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                const int h = 2 * g + hh;
+                if (ANYH && h >= hlive) continue;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) out_row[h * D + c0 + 16 * j + n] = (uint16_t)pack_bf16(num[hh][j] / den[hh], 0.0f);
+                if (lse_row && wave == 0 && n == 0) lse_row[h] = mx[hh] + logf(den[hh]);
+            }
+            return;
+        }
+        // ---- publish this partition, the last one to finish folds the row
+        // (the protocol of c8_attention's fused merge) ----
+        const __amdgpu_buffer_rsrc_t states =
+            row_states(reinterpret_cast<float *>(p.partial) + (int64_t)qrow * S * HEADS * PART_FLOATS);
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
-            const int h = 2 * g + hh;
-            if (ANYH && h >= hlive) continue;
+            const int base = ((part * HEADS + 2 * g + hh) * PART_FLOATS) * 4;
 #pragma unroll
-            for (int j = 0; j < 8; ++j) out_row[h * D + c0 + 16 * j + n] = (uint16_t)pack_bf16(num[hh][j] / den[hh], 0.0f);
-            if (lse_row && wave == 0 && n == 0) lse_row[h] = mx[hh] + logf(den[hh]);
+            for (int j = 0; j < 8; ++j) state_store<SC1>(num[hh][j], states, base + (c0 + 16 * j + n) * 4);
+            if (wave == 0 && n == 0) {
+                state_store<SC1>(mx[hh], states, base + 512 * 4);
+                state_store<SC1>(den[hh], states, base + 513 * 4);
+            }
         }
-    }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        uint32_t *tickets = reinterpret_cast<uint32_t *>(p.workspace);
+        if (tid == 0) s.misc[5] = (int)__hip_atomic_fetch_add(&tickets[qrow], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __syncthreads();
+        if (s.misc[5] != folded - 1) return;
+        if (tid == 0) __hip_atomic_store(&tickets[qrow], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        // fold_row covers eight heads with 512 threads: heads 0-3, then 4-7
+        // (one copy of its code: the loop is kept).
+#pragma nounroll
+        for (int half = 0; half < 2; ++half)
+            fold_row<SC1>(states, folded, tid + ROWS_THREADS * half, out_row, lse_row, ANYH ? hlive : HEADS);
+    };
+
+    // Capacity plan: rows first_row, first_row + G, ...  Re-planned: the live
+    // items of this XCD, rows [x R / 8, (x + 1) R / 8) each as S partitions,
+    // over the XCD's work-groups in turn.
+    const int32_t x = (int32_t)(blockIdx.x & 7u);
+    const int32_t lo = replan ? x * live_rows / 8 : 0, hi = replan ? (x + 1) * live_rows / 8 : rows_cap;
+    const int32_t step = replan ? (int32_t)(G >> 3) : (int32_t)G;
+    for (int32_t j = replan ? (int32_t)(blockIdx.x >> 3) : first_row; lo + j / S < hi; j += step)
+        run_item(lo + j / S, j % S);
 }
 
 // ---- INT8 cache writer (cache_write.cpp:9-88): one wave per update row ----
@@ -1913,7 +2021,7 @@ void launch_variant(hipStream_t stream, const SharedKVArgs *a, const SharedKVDeb
         const uint32_t g2 = rows < 2u * (uint32_t)PLAN_CUS ? (rows + 7u) & ~7u : 2u * (uint32_t)PLAN_CUS;
         const auto rows_kernel = streamed ? &c8_rows<true, ANYH> : &c8_rows<false, ANYH>;
         hipLaunchKernelGGL(rows_kernel, dim3(g2), dim3(ROWS_THREADS), 0, stream, a->cuQ, a->seqLens, a->q, a->indices,
-                           a->batch, a->topk, rows, g2, a->heads, *a);
+                           a->batch, a->topk, rows, g2, a->heads, *a, fused);
         return;
     }
     decltype(&c8_attention<1, false, false, ANYH, false, false>) kernel =
@@ -1949,7 +2057,11 @@ int launch_attention(hipStream_t stream, const SharedKVArgs *a, const SharedKVDe
     const uint32_t rows = a->tokens * head_groups(a->heads);
     const uint32_t items = rows * splits;
     const uint32_t grid = (items + 7u) & ~7u;
-    const uint32_t fused = splits > 1 && g_merge_mode.load(std::memory_order_relaxed) == 0;
+    // Partition states may be merged inside the launch (merge mode 0) when
+    // the launch has several partitions, or has one and supplies partition
+    // states and tickets for the device re-plan of a padded launch.
+    const uint32_t fused = g_merge_mode.load(std::memory_order_relaxed) == 0 &&
+                           (splits > 1 || (a->partial && a->workspace && !DEBUG));
     // Debug dumps hold eight heads and one original tile (list places 0..127) per row.
     if (DEBUG && (a->heads != HEADS || (a->oriIndices && a->oriTopk > N))) return (int)hipErrorInvalidValue;
     const bool slots = a->oriIndices != 0;
@@ -2006,15 +2118,22 @@ int scratch_address(void **out)
 }
 
 uint64_t workspace_bytes(uint32_t rows) { return ((uint64_t)rows * 4 + 255) / 256 * 256; }
+// Partition states of a launch: rows x splits of them with several
+// partitions; with one partition, the states that the device re-plan of a
+// padded launch can reach (at most PLAN_CUS row partitions: the plan gives
+// live rows x partitions <= PLAN_CUS whenever it gives more than one).
 uint64_t partial_bytes(uint32_t rows, uint32_t splits)
 {
-    return splits > 1 ? (uint64_t)rows * splits * HEADS * PART_FLOATS * 4 : 0;
+    const uint64_t state = (uint64_t)HEADS * PART_FLOATS * 4;
+    if (splits > 1) return (uint64_t)rows * splits * state;
+    return rows > 1 ? (uint64_t)(rows < (uint32_t)PLAN_CUS ? rows : (uint32_t)PLAN_CUS) * state : 0;
 }
 
 // Byte offsets of a launch's tickets and partition states in the
 // allocation-free scratch array (constant: 0 and NOALLOC_TICKET_BYTES);
-// non-zero when the launch does not fit.  One-partition launches use
-// neither region and always fit.
+// non-zero when the launch does not fit.  One-partition launches always fit:
+// only their device re-plan merges, over at most PLAN_CUS row partitions
+// (tickets of at most PLAN_CUS rows, partial_bytes(rows, 1) of states).
 int noalloc_layout(uint64_t rows, uint32_t splits, uint64_t *tickets, uint64_t *states)
 {
     *tickets = 0;
@@ -2024,6 +2143,9 @@ int noalloc_layout(uint64_t rows, uint32_t splits, uint64_t *tickets, uint64_t *
     if (rows * 4 > NOALLOC_TICKET_BYTES || partial_bytes((uint32_t)rows, splits) > NOALLOC_STATE_BYTES) return 1;
     return 0;
 }
+static_assert(PLAN_CUS * 4 <= NOALLOC_TICKET_BYTES &&
+                  (uint64_t)PLAN_CUS * HEADS * PART_FLOATS * 4 <= NOALLOC_STATE_BYTES,
+              "a one-partition launch's re-plan fits the allocation-free scratch");
 
 }  // namespace
 

@@ -140,11 +140,13 @@ def device_splits(splits, tokens, heads, ratio, topk, cu_q, seq_lens, ori_topk=0
     rows are live (graph padding), the kernel hands idle work-groups to the
     live rows as more partitions: plan_splits(live rows, tile count of the
     longest live row), at most work-groups // live rows and never below
-    `splits`.  Only fused launches (splits > 1, merge in the same launch)
-    re-plan: the partition states need the partial buffer, which a
-    one-partition launch does not carry.  The kernel's numerics follow this
-    count (tile k folds into partition k % count), so checkers use it in
-    place of `splits`.
+    `splits`.  Only launches that merge in themselves re-plan (`fused`: the
+    library's merge mode 0, with several partitions or with one partition
+    and the re-plan's partition states supplied, which prepare() always
+    does); one-partition C4 launches of more rows than CUs (c8_rows) apply
+    the same rule with their rows as the work-groups.  The kernel's numerics
+    follow this count (tile k folds into partition k % count), so checkers
+    use it in place of `splits`.
 
     Joint-plan launches (joint_launch; `cmp_rows` = the compressed block
     table's rows per sequence, width x 32) run as one partition per row
@@ -155,9 +157,7 @@ def device_splits(splits, tokens, heads, ratio, topk, cu_q, seq_lens, ori_topk=0
     live_rows, rows = live_tokens * groups, tokens * groups
     if joint_launch(splits, tokens, heads, ratio, cu_q, seq_lens, ori_topk, fused, cmp_rows):
         return 1
-    if not fused or splits <= 1:
-        return splits
-    if live_rows == 0 or live_rows >= rows:
+    if not fused or live_rows == 0 or live_rows >= rows:
         return splits
     tiles = (ori_topk + TILE - 1) // TILE if ori_topk else 1
     if ratio == 4:
@@ -245,7 +245,13 @@ def workspace_bytes(rows, splits):
 
 
 def partial_shape(rows, splits):
-    return (rows, splits, HEADS, PARTIAL_FLOATS) if splits > 1 else (0,)
+    """FP32 partition states: [rows, splits, 8, 520] with several partitions;
+    with one, the room of the device re-plan of a padded launch (at most
+    CORES row partitions: live rows x partitions <= CORES whenever the plan
+    gives more than one), or nothing for a one-row launch."""
+    if splits > 1:
+        return (rows, splits, HEADS, PARTIAL_FLOATS)
+    return (min(rows, CORES), HEADS, PARTIAL_FLOATS) if rows > 1 else (0,)
 
 
 def prepare(entry, *, scratch_allocator=None, shared_storage=False):
@@ -258,7 +264,9 @@ def prepare(entry, *, scratch_allocator=None, shared_storage=False):
     zero again, so a workspace must not be shared by launches that can run
     concurrently (separate streams get separate scratch through
     scratch_allocator's (name, stream) key).
-    partial: FP32 [rows, splits, 8, 520] partition states (splits > 1).
+    partial: FP32 [rows, splits, 8, 520] partition states (splits > 1), or
+    with one partition the room of the device re-plan of a padded launch
+    (partial_shape).
     """
     if getattr(entry, "c8_dynamic", False) or not supported(entry):
         return entry
@@ -271,22 +279,23 @@ def prepare(entry, *, scratch_allocator=None, shared_storage=False):
     need_partial = 1
     for extent in shape:
         need_partial *= extent
+    has_partial = need_partial > 0 and shape != (0,)
     workspace, partial = entry.workspace, entry.partial
     if shared_storage:
         if workspace is None or workspace.numel() < need_ws or (
-                p.splits > 1 and (partial is None or partial.numel() < need_partial)):
+                has_partial and (partial is None or partial.numel() < need_partial)):
             raise ValueError("C8 shared controls require the full workspace and partial extents")
     else:
         if workspace is None or workspace.numel() < need_ws:
             workspace = allocate("workspace", (need_ws,), torch.uint8, device)
-        if p.splits > 1 and (partial is None or partial.numel() < need_partial):
+        if has_partial and (partial is None or partial.numel() < need_partial):
             partial = allocate("partial", shape, torch.float32, device)
     workspace[:need_ws].zero_()
 
     out = copy.copy(entry)
     out.args = type(p).from_buffer_copy(p)
     out.args.workspace = workspace.data_ptr()
-    out.args.partial = partial.data_ptr() if (partial is not None and p.splits > 1) else 0
+    out.args.partial = partial.data_ptr() if (partial is not None and has_partial) else 0
     out.workspace, out.partial = workspace, partial
     out.blocks = rows * p.splits
     out.argument_address = ctypes.addressof(out.args)

@@ -30,8 +30,9 @@ extern "C" {
  *   (INT32 [batch][width]), indices (INT32 [tokens][1][topk], ratio 4), cuQ
  *   (INT32 [batch+1]), seqLens (INT32 [batch]), sinks (FP32 [heads]), out
  *   (BF16 [tokens][heads][512]), lse (FP32 [tokens][heads] or 0), partial
- *   (FP32 [rows][splits][8][520] partition states when splits > 1, see
- *   sharedkv_c8_partial_bytes), splits (KV partitions), oriPages (pool size
+ *   (FP32 [rows][splits][8][520] partition states when splits > 1; with
+ *   one partition 0, or the re-plan room of sharedkv_c8_partial_bytes),
+ *   splits (KV partitions), oriPages (pool size
  *   of the window cache; rows on pages past it are masked), workspace (one
  *   uint32 merge ticket per row, sharedkv_c8_workspace_bytes; zero before the
  *   first launch, and each launch leaves it zero, so launches that may
@@ -103,7 +104,14 @@ int sharedkv_c8_attention_debug(void *stream, const SharedKVArgs *args, const Sh
 int launch_cache_write(uint32_t blocks, void *stream, const CacheWriteArgs *args);
 
 /* Scratch sizes in bytes for a launch with `rows` = tokens * ceil(heads / 8)
- * rows (the query token count at eight heads). */
+ * rows (the query token count at eight heads).  partial_bytes(rows, 1) is
+ * the partition-state room of a one-partition launch's device re-plan: when
+ * such a launch (merge mode 0) supplies non-zero `workspace` and `partial`
+ * of these sizes, graph padding that leaves fewer live rows than `rows`
+ * re-plans the live rows into several partitions merged in the launch, as
+ * launches with splits > 1 do (the reference device likewise plans splits
+ * from live rows, c4_wide.h:16-41); with partial = 0 it keeps one partition
+ * per row.  At most 256 row partitions: min(rows, 256) * 16640 bytes. */
 uint64_t sharedkv_c8_workspace_bytes(uint32_t rows, uint32_t splits);
 uint64_t sharedkv_c8_partial_bytes(uint32_t rows, uint32_t splits);
 
@@ -118,7 +126,8 @@ uint64_t sharedkv_c8_partial_bytes(uint32_t rows, uint32_t splits);
  * layout is fixed: tickets in its first 4096 bytes (1024 rows), partition
  * states from byte 4096 on, so launches of any sizes in any order never
  * find another launch's states where their tickets are.  One-partition
- * launches use neither region; a launch with splits > 1 whose
+ * launches use the regions only for their device re-plan of a padded
+ * launch (at most 256 rows' tickets and states); a launch with splits > 1 whose
  * partial_bytes(rows, splits) exceeds the state region (16 MiB - 4 KiB: 504
  * rows at two partitions) is rejected with hipErrorInvalidValue.  The
  * function calls no hipMalloc or hipFree.  Every call on one GPU uses that

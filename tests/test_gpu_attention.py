@@ -595,22 +595,24 @@ def test_graph_replay_with_changing_live_metadata():
         assert torch.equal(op.lse, eager.lse), i
 
 
-def test_graph_at_capacity_replayed_at_fewer_live_sequences():
+@pytest.mark.parametrize("cap", [64, 160])
+def test_graph_at_capacity_replayed_at_fewer_live_sequences(cap):
     """One launch captured at a capacity of 64 one-token C4 requests (3
-    partitions: 192 work-groups), replayed with 64, 8, 16, 32, 64 and 8 live
-    requests (graph padding: the rest seq_len 0).  The kernel re-plans from
-    the live metadata (the idle work-groups become partitions of the live
-    rows); every replay is bit-exact with the checker on that plan, padding
-    rows are zero, and eager work runs between replays."""
+    partitions: 192 work-groups) or 160 (one partition per row, with the
+    re-plan's partition states supplied), replayed with 64, 8, 16, 32, 64
+    and 8 live requests (graph padding: the rest seq_len 0).  The kernel
+    re-plans from the live metadata (the idle work-groups become partitions
+    of the live rows, placed on every XCD); every replay is bit-exact with
+    the checker on that plan, padding rows are zero, and eager work runs
+    between replays."""
     import torch
     from npu_sparse_attn_sharedkv_int8 import PreparedAttention, c8_attention
-    cap = 64
     rng = np.random.default_rng(5)
     lengths = [int(n) for n in rng.integers(2100, 3000, cap)]      # 6-7 tiles a row
     case = workloads.make_case(26, 4, [1] * cap, lengths, index_mode="uniform")
     dev, oscale, cscale, keep = to_device(case)
     op = PreparedAttention(dev, oscale, cscale, return_lse=True)
-    assert op.splits == 3
+    assert op.splits == (3 if cap == 64 else 1)
     stream = torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(stream):
@@ -626,7 +628,7 @@ def test_graph_at_capacity_replayed_at_fewer_live_sequences():
         cu = np.array(list(range(live + 1)) + [live] * (cap - live), np.int32)
         lens = np.array(lengths[:live] + [0] * (cap - live), np.int32)
         plan = c8_attention.device_splits(op.splits, cap, 8, 4, 1024, cu, lens)
-        assert plan == (3 if live == cap else 5)
+        assert plan == {64: {64: 3, 8: 5, 16: 5, 32: 5}, 160: {64: 2, 8: 5, 16: 5, 32: 5}}[cap][live], plan
         dev.cu_q.copy_(torch.from_numpy(cu))
         dev.seq_lens.copy_(torch.from_numpy(lens))
         op.out.fill_(float("nan"))
@@ -767,7 +769,8 @@ def test_persistent_graph_across_live_states():
     replayed twice per live state while the live batch and lengths change
     (4, 2, 1, 0 and 3 live requests).  Outputs and LSE are poisoned with NaN
     before each state; padding rows must come back zero and live rows
-    bit-exact with the checker."""
+    bit-exact with the checker on the device plan (one live request of 100
+    two-tile rows re-plans to two partitions merged in the launch)."""
     import torch
     from npu_sparse_attn_sharedkv_int8 import PreparedAttention
     full = workloads.make_case(91, 4, [100] * 4, [1600] * 4, index_mode="holes")
@@ -805,7 +808,68 @@ def test_persistent_graph_across_live_states():
         if not batch:
             continue
         sub = dict(full, q=q[:live], cu_q=cu[:batch + 1], seq_lens=lens[:batch])
-        ref, ref_lse, _ = run_oracle(sub, 1)
+        plan = effective_splits(dict(full, q=q, cu_q=cu, seq_lens=lens), op.splits)
+        assert plan == (2 if batch == 1 else 1), plan
+        ref, ref_lse, _ = run_oracle(sub, plan)
+        diff = out[:live] != ref
+        assert not diff.any(), f"{batch} live: {int(diff.sum())} BF16 mismatches"
+        np.testing.assert_allclose(lse[:live], ref_lse, rtol=0, atol=2e-6)
+    del graph
+
+
+def test_rows_graph_at_capacity_replayed_with_few_live_sequences():
+    """A decode launch of 256 requests x 2 tokens (512 one-partition rows:
+    c8_rows) captured once and replayed with 256, 16, 64, 3 and 256 live
+    requests.  With few live rows the kernel re-plans them into partitions
+    (c8_attention.device_splits: 4 for 32 rows of at most 4 tiles, 2 for
+    128 rows, 4 for 6 rows), spread
+    over every XCD and merged in the launch.  Outputs, LSE and partition
+    states are NaN-poisoned before each state and eager launches run between
+    replays; padding rows come back zero, live rows bit-exact with the
+    checker on the device plan, and the merge tickets return to zero."""
+    import torch
+    from npu_sparse_attn_sharedkv_int8 import PreparedAttention
+    cap = 256
+    rng = np.random.default_rng(33)
+    lengths = [int(n) for n in rng.integers(600, 1600, cap)]
+    full = workloads.make_case(93, 4, [2] * cap, lengths, index_mode="uniform")
+    dev, oscale, cscale, keep = to_device(full)
+    op = PreparedAttention(dev, oscale, cscale, return_lse=True)
+    assert op.splits == 1 and op.partial is not None and op.partial.shape == (256, 8, 520)
+    other = PreparedAttention(dev, oscale, cscale, return_lse=True, splits=2)
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        op.run()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            op.run()
+    torch.cuda.current_stream().wait_stream(stream)
+    for batch, want in ((cap, 1), (16, 4), (64, 2), (3, 4), (cap, 1)):
+        cu = np.array([2 * min(b, batch) for b in range(cap + 1)], np.int32)
+        lens = np.array(lengths[:batch] + [0] * (cap - batch), np.int32)
+        q = full["q"].copy()
+        q[2 * batch:] = 0x7FC0
+        dev.q.copy_(torch_bf16(q, "cuda"))
+        dev.cu_q.copy_(torch.from_numpy(cu))
+        dev.seq_lens.copy_(torch.from_numpy(lens))
+        op.out.fill_(float("nan"))
+        op.lse.fill_(float("nan"))
+        op.partial.fill_(float("nan"))
+        other.run()                                     # eager work between replays
+        torch.cuda.synchronize()
+        plan = effective_splits(dict(full, q=q, cu_q=cu, seq_lens=lens), op.splits)
+        assert plan == want, (batch, plan)
+        say(f"[rows graph] {batch} live requests, {plan} partition(s)")
+        graph.replay()
+        torch.cuda.synchronize()
+        out, lse = bits_of(op.out), op.lse.cpu().numpy()
+        live = 2 * batch
+        assert not out[live:].any() and not lse[live:].any(), "padding rows are not zero"
+        assert not op.workspace.any(), "merge tickets must return to zero"
+        sub = dict(full, q=q[:live], cu_q=cu[:batch + 1], seq_lens=lens[:batch])
+        ref, ref_lse, _ = run_oracle(sub, plan)
         diff = out[:live] != ref
         assert not diff.any(), f"{batch} live: {int(diff.sum())} BF16 mismatches"
         np.testing.assert_allclose(lse[:live], ref_lse, rtol=0, atol=2e-6)

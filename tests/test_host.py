@@ -96,7 +96,13 @@ def test_module_helpers_match_reference_names():
 
 def test_scratch_sizes():
     lib = runtime.library()
-    assert lib.sharedkv_c8_partial_bytes(64, 1) == 0
+    # One partition: the device re-plan's room, at most 256 row partitions
+    # (the host's partial_shape); nothing for a single row.
+    assert lib.sharedkv_c8_partial_bytes(64, 1) == 64 * 8 * 520 * 4
+    assert lib.sharedkv_c8_partial_bytes(4096, 1) == 256 * 8 * 520 * 4
+    assert lib.sharedkv_c8_partial_bytes(1, 1) == 0
+    for rows in (2, 64, 300, 4096):
+        assert lib.sharedkv_c8_partial_bytes(rows, 1) == 4 * int(np.prod(c8_attention.partial_shape(rows, 1)))
     assert lib.sharedkv_c8_partial_bytes(64, 8) == 64 * 8 * 8 * 520 * 4
     assert lib.sharedkv_c8_workspace_bytes(64, 8) >= 64 * 4
     assert lib.sharedkv_c8_workspace_bytes(1, 1) % 256 == 0
@@ -172,19 +178,27 @@ def test_device_plan_of_padded_launches():
     """The kernel's re-plan of a graph-padded launch (its host mirror):
     capacity 64 C4 rows at 3 partitions (192 work-groups) replayed with
     8/16/32/64 live requests of 9-tile rows runs what an eager launch of the
-    live rows would choose; one-partition and separate-merge launches keep
-    their plan."""
+    live rows would choose; separate-merge launches keep their plan, and a
+    one-partition launch re-plans within its rows (its work-groups)."""
     plan = c8_attention.device_splits
     cap = 64
     assert c8_attention.choose_splits(cap, 4, 1024) == 3
-    for live, want in ((8, 5), (16, 5), (32, 5), (51, 3), (64, 3)):
+    for live, want, one in ((8, 5, 5), (16, 5, 4), (32, 5, 2), (51, 3, 1), (64, 3, 1)):
         cu = list(range(live + 1)) + [cap] * (cap - live)
         lens = [20000] * live + [0] * (cap - live)
         assert plan(3, cap, 8, 4, 1024, cu, lens) == want, live
         assert plan(3, cap, 8, 4, 1024, cu, lens, fused=False) == 3
-        assert plan(1, cap, 8, 4, 1024, cu, lens) == 1
+        assert plan(1, cap, 8, 4, 1024, cu, lens) == one, live
+        assert plan(1, cap, 8, 4, 1024, cu, lens, fused=False) == 1
         # Eager's choice where the work-groups allow it (51 x 5 > 192).
         assert want == c8_attention.choose_splits(live, 4, 1024) or live == 51
+    # A one-partition C4 launch of 512 rows (c8_rows) replayed with 16 or 64
+    # live sequences of two tokens: the eager plan of the live rows.
+    for live, want in ((16, 5), (64, 2)):
+        cu = [2 * i for i in range(live + 1)] + [2 * live] * (256 - live)
+        lens = [30000] * live + [0] * (256 - live)
+        assert plan(1, 512, 8, 4, 1024, cu, lens) == want == c8_attention.choose_splits(2 * live, 4, 1024)
+    assert c8_attention.partial_shape(512, 1) == (256, 8, 520) and c8_attention.partial_shape(1, 1) == (0,)
     # Work-groups cap the plan: capacity 6 at 2 partitions, 5 live rows -> 2.
     assert plan(2, 6, 8, 4, 1024, [0, 5, 6], [9000, 0]) == 2
     # The longest live row bounds the plan by its tile count: C4 top-k rows
