@@ -46,6 +46,7 @@
 
 #include <atomic>
 #include <mutex>
+#include <type_traits>
 
 #include "sharedkv_hip.h"
 
@@ -71,6 +72,10 @@ constexpr int FOLD_SLOT = 514;         // partition 0, head 0: partitions to fol
 constexpr int WINDOW = 128;
 constexpr int BLOCK_ROWS = 32;
 constexpr uint32_t MAX_SPLITS = 16;
+// C4 launches of fewer query tokens go through the small-launch entry
+// (the reference host's rule, c8_attention.py:111-112 there: tokens < its
+// 24 cores).
+constexpr uint32_t SMALL_TOKENS = 24;
 static_assert(N == 128 && WINDOW == N && WAVES == 8, "one window tile of 128 keys; 8 waves x 16 keys");
 static_assert(MAX_LIST == 2 * THREADS, "two C4 index entries per thread");
 
@@ -482,13 +487,18 @@ c8_attention(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base
 
     // ---- live shape (attention_impl.h:121-137) ----
     // The last request with seq_len > 0 and cu_q >= 0 ends the live batch;
-    // its cu_q end bounds the live tokens.
+    // its cu_q end bounds the live tokens.  The longest of those requests
+    // bounds the rows' tile counts; kernels that choose joint rows from it
+    // take it in the same pass.
     if (tid == 0) { s.misc[0] = 0; s.misc[1] = -1; s.misc[2] = 0; s.misc[6] = 0; }
     __syncthreads();
     for (int b = tid; b < batch_n; b += THREADS) {
         const int len = b == tid ? my_len : lens[b];
         const int c1 = b == tid ? my_cu1 : cu[b + 1];
-        if (len > 0 && c1 >= 0) atomicMax(&s.misc[0], b + 1);
+        if (len > 0 && c1 >= 0) {
+            atomicMax(&s.misc[0], b + 1);
+            if (JOINT) atomicMax(&s.misc[6], len);
+        }
     }
     __syncthreads();
     const int live_batch = uni(s.misc[0]);
@@ -524,10 +534,13 @@ c8_attention(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base
     const int32_t live_rows = live_tokens * HG;
     // The longest live sequence bounds the rows' tile counts (one scan, only
     // where a plan needs it).
-    int longest = -1;
+    int longest = JOINT ? uni(s.misc[6]) : -1;
     auto longest_live = [&]() {
         if (longest < 0) {
-            for (int b = tid; b < live_batch; b += THREADS) atomicMax(&s.misc[6], b == tid ? my_len : lens[b]);
+            for (int b = tid; b < live_batch; b += THREADS) {
+                const int len = b == tid ? my_len : lens[b];
+                if (len > 0 && (b == tid ? my_cu1 : cu[b + 1]) >= 0) atomicMax(&s.misc[6], len);
+            }
             __syncthreads();
             longest = uni(s.misc[6]);
         }
@@ -614,8 +627,13 @@ c8_attention(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base
         }
     }
     // The work item (query row qrow, partition part) from its row request
-    // onwards.
-    auto run_row = [&]() {
+    // onwards.  joint_c4 (a compile-time flag): the launch is a joint-plan C4
+    // launch, whose rows take the joint route; C4 kernels with joint rows
+    // compiled in hold one specialized copy for such launches and one for
+    // tiled launches, so the tiled copy is the same code as in kernels
+    // without them.
+    auto run_row = [&](auto joint_c4) {
+        constexpr bool JC4 = decltype(joint_c4)::value;
         // Every metadata load has landed: said explicitly (vmcnt(0)) so that the
         // compiler's own wait tracking does not hold back the block-table reads
         // issued next for these registers.
@@ -741,7 +759,7 @@ c8_attention(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base
         // takes the joint route then too): its compressed tile is then all
         // masked.  The joint route rounds the PV dequantization differently from
         // the tiled one, so the row keeps it.
-        const bool joint4 = RATIO == 4 && joint_launch && m.count <= N;
+        const bool joint4 = RATIO == 4 && JC4 && m.count <= N;
         if (joint4 && m.position >= 0) m.total = 2;
         const int my_tiles = m.total > part ? (m.total - part + S - 1) / S : 0;   // tiles part, part + S, ...
         // A live row's window list holds at least its own position, so it has a
@@ -1045,7 +1063,9 @@ c8_attention(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base
             asm volatile("" : "+v"(lane_x));
             const int gx = lane_x >> 4, nx = lane_x & 15;
 
-            if (joint) {
+            // The joint-plan C4 copy holds only the joint route: every live
+            // row of such a launch is a joint row (count <= N).
+            if (JC4 || joint) {
                 // ---- joint row: both tiles resident (tile 0 = window in buffer
                 // 0, tile 1 = compressed rows in buffer 1) ----
                 vm_wait<0>();
@@ -1386,7 +1406,12 @@ c8_attention(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
         fold_row<SC1>(states, folded, tid, out_row, lse_row, ANYH ? hlive : HEADS);
     };
-    run_row();
+    if constexpr (RATIO == 4 && JOINT) {
+        if (joint_launch) run_row(std::integral_constant<bool, true>{});
+        else run_row(std::integral_constant<bool, false>{});
+    } else {
+        run_row(std::integral_constant<bool, false>{});
+    }
 }
 
 // Partition merge as a second launch (merge mode 1): one 512-thread group
@@ -1488,7 +1513,8 @@ c8_rows(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, con
     if (replan) {
         if (tid == 0) s.misc[6] = 0;
         __syncthreads();
-        for (int b = tid; b < live_batch; b += ROWS_THREADS) atomicMax(&s.misc[6], lens[b]);
+        for (int b = tid; b < live_batch; b += ROWS_THREADS)
+            if (lens[b] > 0 && cu[b + 1] >= 0) atomicMax(&s.misc[6], lens[b]);
         __syncthreads();
         const int longest = uni(s.misc[6]);
         const int cnt = longest / 4 < topk ? longest / 4 : topk;
@@ -2000,17 +2026,21 @@ std::atomic<int> g_merge_mode{0};
 
 template <bool DEBUG, bool ANYH>
 void launch_variant(hipStream_t stream, const SharedKVArgs *a, const SharedKVDebug &dbg, bool slots, uint32_t grid,
-                    uint32_t splits, uint32_t rows, uint32_t fused)
+                    uint32_t splits, uint32_t rows, uint32_t fused, bool small_entry)
 {
     // Decode-shaped launches stream their KV rows with the non-temporal
     // policy; window-only (ratio 1) launches keep the default.
     const uint32_t per_slot = a->ratio == 4 ? STREAM_TOKENS_C4 : a->ratio == 128 ? STREAM_TOKENS_C128 : 0;
     const bool streamed = !DEBUG && (uint64_t)a->tokens <= (uint64_t)per_slot * a->batch;
-    // Joint rows: C128 kernels always carry them; C4 kernels only when the
-    // launch's compressed block table names at most one tile of rows per
-    // sequence (C4 joint rows cost the tiled C4 path about 3 % where they
-    // are compiled in, so only such launches get them).
-    const bool joint4 = !DEBUG && !slots && a->heads <= HEADS && (uint64_t)a->cmpTableWidth * BLOCK_ROWS <= (uint64_t)N;
+    // Joint rows: C128 kernels always carry them.  C4 kernels carry them
+    // (and take them when every live row is short) for launches through the
+    // small-launch entry, as the reference's sparse_small entry chooses its
+    // narrow route from live lengths (c4_small.cpp:10-19), and for launches
+    // whose compressed block table names at most one tile of rows per
+    // sequence.  Other C4 launches run kernels without them: compiled in,
+    // they cost tiled C4 launches about 1 %.
+    const bool joint4 = !DEBUG && !slots && a->heads <= HEADS &&
+                        (small_entry || (uint64_t)a->cmpTableWidth * BLOCK_ROWS <= (uint64_t)N);
     // One-partition C4 launches of more rows than CUs (prefill, large decode
     // batches) run two four-wave work-groups per CU taking rows in turn
     // (c8_rows).  C128 and window-only launches keep one work-group per row.
@@ -2048,7 +2078,7 @@ void launch_variant(hipStream_t stream, const SharedKVArgs *a, const SharedKVDeb
 }
 
 template <bool DEBUG>
-int launch_attention(hipStream_t stream, const SharedKVArgs *a, const SharedKVDebug *debug)
+int launch_attention(hipStream_t stream, const SharedKVArgs *a, const SharedKVDebug *debug, bool small_entry = false)
 {
     if (check_attention(a)) return (int)hipErrorInvalidValue;
     if (a->tokens == 0) return (int)hipSuccess;
@@ -2066,9 +2096,9 @@ int launch_attention(hipStream_t stream, const SharedKVArgs *a, const SharedKVDe
     if (DEBUG && (a->heads != HEADS || (a->oriIndices && a->oriTopk > N))) return (int)hipErrorInvalidValue;
     const bool slots = a->oriIndices != 0;
     if (!DEBUG && a->heads != HEADS)
-        launch_variant<false, true>(stream, a, dbg, slots, grid, splits, rows, fused);
+        launch_variant<false, true>(stream, a, dbg, slots, grid, splits, rows, fused, small_entry);
     else
-        launch_variant<DEBUG, false>(stream, a, dbg, slots, grid, splits, rows, fused);
+        launch_variant<DEBUG, false>(stream, a, dbg, slots, grid, splits, rows, fused, small_entry);
     if (splits > 1 && !fused)
         hipLaunchKernelGGL(c8_merge, dim3(rows), dim3(THREADS), 0, stream, *a, splits);
     return (int)hipGetLastError();
@@ -2160,7 +2190,9 @@ int launch_sharedkv_c8_sparse(uint32_t blocks, void *stream, const SharedKVArgs 
 
 int launch_sharedkv_c8_sparse_small(uint32_t blocks, void *stream, const SharedKVArgs *args)
 {
-    return launch_sharedkv_c8_sparse(blocks, stream, args);
+    if (!blocks) return (int)hipSuccess;
+    if (!args || args->ratio != 4) return (int)hipErrorInvalidValue;
+    return launch_attention<false>(static_cast<hipStream_t>(stream), args, nullptr, true);
 }
 
 int launch_sharedkv_c8_dense(uint32_t blocks, void *stream, const SharedKVArgs *args)
@@ -2218,7 +2250,10 @@ int launch_sharedkv_c8_noalloc(uint32_t blocks, void *stream, const SharedKVArgs
     SharedKVArgs a = *args;
     a.workspace = (uint64_t)(uintptr_t)base + tickets;
     a.partial = (uint64_t)(uintptr_t)base + states;
-    return launch_attention<false>(static_cast<hipStream_t>(stream), &a, nullptr);
+    // The entry the package routes the launch to: C4 launches of fewer than
+    // SMALL_TOKENS tokens as launch_sharedkv_c8_sparse_small.
+    return launch_attention<false>(static_cast<hipStream_t>(stream), &a, nullptr,
+                                   a.ratio == 4 && a.tokens < SMALL_TOKENS);
 }
 
 uint64_t sharedkv_c8_noalloc_scratch_bytes(void) { return NOALLOC_SCRATCH_BYTES; }

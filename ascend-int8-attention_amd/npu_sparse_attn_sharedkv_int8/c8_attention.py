@@ -42,6 +42,7 @@ MAX_SPLITS = 16
 WINDOW = 128
 BLOCK = 32
 MAX_TOPK = 1024
+SMALL_TOKENS = 24          # C4 launches of fewer tokens go through the small-launch entry
 SPLITS_FEW_ROWS = 5        # when rows x 5 work-groups fit one wave on the CUs
 SPLITS_MANY_ROWS = 3
 PARTIAL_FLOATS = 520       # per (token, partition, head): 512 numerator, max, denominator, pad
@@ -101,17 +102,15 @@ def live_shape(cu_q, seq_lens, tokens):
     """(live tokens, longest live sequence) of a launch's metadata, as the
     kernel reads them (attention_impl.h:121-137): the last request with
     seq_len > 0 and cu_q[b + 1] >= 0 ends the live batch, its cu_q end
-    (clamped to the launch's tokens) bounds the live tokens."""
+    (clamped to the launch's tokens) bounds the live tokens; the longest
+    live sequence is the longest request that passes the same test."""
     cu_q = [int(x) for x in cu_q]
     seq_lens = [int(x) for x in seq_lens]
-    live_batch = 0
-    for b, length in enumerate(seq_lens):
-        if length > 0 and cu_q[b + 1] >= 0:
-            live_batch = b + 1
-    if not live_batch:
+    live = [b for b, length in enumerate(seq_lens) if length > 0 and cu_q[b + 1] >= 0]
+    if not live:
         return 0, 0
-    end = cu_q[live_batch]
-    return max(0, min(end, tokens)), max([0] + seq_lens[:live_batch])
+    end = cu_q[live[-1] + 1]
+    return max(0, min(end, tokens)), max(seq_lens[b] for b in live)
 
 
 def keyless_tokens(cu_q, seq_lens, tokens):
@@ -132,7 +131,8 @@ def keyless_tokens(cu_q, seq_lens, tokens):
     return keyless
 
 
-def device_splits(splits, tokens, heads, ratio, topk, cu_q, seq_lens, ori_topk=0, fused=True, cmp_rows=None):
+def device_splits(splits, tokens, heads, ratio, topk, cu_q, seq_lens, ori_topk=0, fused=True, cmp_rows=None,
+                  small=None):
     """The KV partitions the kernel runs a launch with, from its live metadata.
 
     A launch planned for `tokens` query tokens (graph capacity) at `splits`
@@ -155,7 +155,7 @@ def device_splits(splits, tokens, heads, ratio, topk, cu_q, seq_lens, ori_topk=0
     live_tokens, longest = live_shape(cu_q, seq_lens, tokens)
     groups = head_groups(heads)
     live_rows, rows = live_tokens * groups, tokens * groups
-    if joint_launch(splits, tokens, heads, ratio, cu_q, seq_lens, ori_topk, fused, cmp_rows):
+    if joint_launch(splits, tokens, heads, ratio, cu_q, seq_lens, ori_topk, fused, cmp_rows, small):
         return 1
     if not fused or live_rows == 0 or live_rows >= rows:
         return splits
@@ -167,19 +167,23 @@ def device_splits(splits, tokens, heads, ratio, topk, cu_q, seq_lens, ori_topk=0
     return max(splits, min(plan_splits(live_rows, tiles), rows * splits // live_rows))
 
 
-def joint_launch(splits, tokens, heads, ratio, cu_q, seq_lens, ori_topk=0, fused=True, cmp_rows=None):
+def joint_launch(splits, tokens, heads, ratio, cu_q, seq_lens, ori_topk=0, fused=True, cmp_rows=None, small=None):
     """Whether the kernel runs a launch as a joint-plan launch: joint_plan
     holds, every live row fits one window tile and one compressed tile
     (longest live sequence // ratio <= 128), and the launch is fused or of
-    one partition; for C4 also the compressed block table names at most 128
-    rows per sequence (`cmp_rows` = table width x 32; the library compiles
-    C4 joint rows only into the kernels it launches for such tables, since
-    they slow the tiled C4 path elsewhere).  Such a launch runs one
-    partition per row.  Its C128 rows with compressed rows, and all its C4
-    rows, are joint rows; C4 launches that are not joint-plan launches have
-    none (reference.py:246 switches every C4 row of a joint_sparse plan to
-    the dense multiplicity list)."""
-    if ratio == 4 and (cmp_rows is None or cmp_rows > TILE):
+    one partition.  C4 launches need kernels with joint rows compiled in:
+    those of the small-launch entry (`small`; by default the package's
+    routing, fewer than SMALL_TOKENS tokens: launch_sharedkv_c8_sparse_small,
+    which like the reference's small entry chooses from live lengths,
+    c4_small.cpp:10-19), or whose compressed block table names at most 128
+    rows per sequence (`cmp_rows` = table width x 32).  Such a launch runs
+    one partition per row.  Its C128 rows with compressed rows, and all its
+    C4 rows, are joint rows; C4 launches that are not joint-plan launches
+    have none (reference.py:246 switches every C4 row of a joint_sparse plan
+    to the dense multiplicity list)."""
+    if small is None:
+        small = tokens < SMALL_TOKENS
+    if ratio == 4 and not small and (cmp_rows is None or cmp_rows > TILE):
         return False
     live_tokens, longest = live_shape(cu_q, seq_lens, tokens)
     return (joint_plan(ratio, heads, ori_topk > 0) and (fused or splits == 1) and live_tokens > 0
@@ -299,7 +303,7 @@ def prepare(entry, *, scratch_allocator=None, shared_storage=False):
     out.workspace, out.partial = workspace, partial
     out.blocks = rows * p.splits
     out.argument_address = ctypes.addressof(out.args)
-    small = p.ratio == 4 and p.tokens < 24
+    small = p.ratio == 4 and p.tokens < SMALL_TOKENS
     out.variant = VARIANT_SPARSE_SMALL if small else (VARIANT_SPARSE if p.ratio == 4 else VARIANT_DENSE)
     out.native = native_launcher()
     if out.native.attention_args_size != ctypes.sizeof(type(p)):

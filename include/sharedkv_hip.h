@@ -87,7 +87,14 @@ typedef struct SharedKVDebug {
  * pass 2^31 - 8 work-groups is rejected with hipErrorInvalidValue. */
 int launch_sharedkv_c8_sparse(uint32_t blocks, void *stream, const SharedKVArgs *args);
 
-/* Small-capacity C4 entry (c4_small.cpp:21-22); same kernel family here. */
+/* Small-capacity C4 entry (c4_small.cpp:21-22), for launches of fewer than
+ * 24 query tokens.  The same kernels, except that they also carry the joint
+ * route (reference.py:246-267 with joint_sparse) and take it when every live
+ * row is short (longest live sequence / 4 <= 128), whatever the block
+ * table's width, as the reference's small entry chooses its narrow route
+ * from live lengths (c4_small.cpp:10-19).  Through launch_sharedkv_c8_sparse
+ * only launches whose compressed block table names at most 128 rows per
+ * sequence take it (compiled in, the route costs tiled launches ~1 %). */
 int launch_sharedkv_c8_sparse_small(uint32_t blocks, void *stream, const SharedKVArgs *args);
 
 /* C128 attention: SWA128 window plus every compressed row (c128.cpp:107-108).
@@ -118,7 +125,9 @@ uint64_t sharedkv_c8_partial_bytes(uint32_t rows, uint32_t splits);
 /* Allocation-free attention launch.  No counterpart in the reference: it is
  * for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
- * launch as launch_sharedkv_c8_sparse / _dense (ratio from args->ratio);
+ * launch as the entry the package routes it to: launch_sharedkv_c8_dense
+ * (ratio 1 or 128), launch_sharedkv_c8_sparse_small (ratio 4, fewer than 24
+ * tokens) or launch_sharedkv_c8_sparse (other ratio-4 launches);
  * args->workspace and args->partial are ignored: the merge tickets and
  * partition states live in a library-owned array of
  * sharedkv_c8_noalloc_scratch_bytes() (16 MiB) per GPU, located on the first

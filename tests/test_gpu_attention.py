@@ -272,6 +272,38 @@ def test_joint_c4_rows(mode, heads):
         compare(long_case, out, lse, splits, tag=f"{mode} with a long row, splits {splits}")
 
 
+@pytest.mark.parametrize("mode", ["dups", "mixed", "holes"])
+def test_joint_c4_rows_with_a_serving_width_table(mode):
+    """Short C4 rows behind a block table as wide as a serving table (1055
+    pages: every sequence of a 135 000-token model) take the joint route when
+    the launch comes through the small-launch entry (fewer than 24 tokens,
+    the package's routing), which like the reference's small entry chooses
+    from live lengths (c4_small.cpp:10-19): bit-exact with the checker's
+    joint_sparse plan and different from the tiled plan.  Short rows of a
+    24-token launch (the sparse entry) behind the same table stay tiled."""
+    import oracle.oracle as ora
+    from npu_sparse_attn_sharedkv_int8 import c8_attention
+
+    def widen(case):
+        narrow = case["cmp"].table
+        wide = np.concatenate([narrow, np.tile(narrow[:, :1], (1, 1055 - narrow.shape[1]))], axis=1)
+        case["cmp"].table = np.ascontiguousarray(wide)
+        return case
+
+    case = widen(workloads.make_case(73, 4, [1, 2, 1, 1, 3, 1], [300, 515, 100, 40, 200, 2], index_mode=mode))
+    say(f"[joint c4, serving-width table] {mode}")
+    out, lse, op = run_hip(case, splits=1)
+    assert op.variant == c8_attention.VARIANT_SPARSE_SMALL and op.args.cmpTableWidth == 1055
+    assert joint_flags(case, 1) == (False, True) and op.device_splits() == 1
+    compare(case, out, lse, 1, tag=f"{mode} wide table")
+    tiled, _, _ = ora.tiled_attention(workloads.oracle_case(case), tile=128, splits=1, return_lse=True)
+    assert (out != tiled).any()
+    case = widen(workloads.make_case(74, 4, [4] * 6, [300, 515, 100, 40, 200, 20], index_mode=mode))
+    out, lse, op = run_hip(case, splits=1)
+    assert op.variant == c8_attention.VARIANT_SPARSE and joint_flags(case, 1) == (False, False)
+    compare(case, out, lse, 1, tag=f"{mode} wide table, 24 tokens")
+
+
 @pytest.mark.parametrize("heads", [8, 12])
 def test_persistent_rows(heads):
     """One-partition C4 launches of more rows than CUs run c8_rows: two

@@ -233,12 +233,20 @@ def test_device_plan_of_joint_launches():
     assert plan(5, 4, 8, 128, 0, short, [16511] * 4) == 1 and plan(5, 4, 8, 128, 0, short, [16512] * 4) == 5
     assert plan(5, 4, 16, 128, 0, short, [4096] * 4) == 5                      # no residual codes
     assert plan(5, 4, 8, 128, 0, short, [4096] * 4, ori_topk=128) == 5         # explicit slots
-    # C4: also a compressed block table of at most 128 rows per sequence.
+    # C4: a launch through the small-launch entry (fewer than 24 tokens, the
+    # package's routing) follows live lengths whatever the table width, like
+    # the reference's c4_small.cpp:10-19; other launches also need a
+    # compressed block table of at most 128 rows per sequence.
     assert plan(5, 4, 8, 4, 1024, short, [4096] * 4, cmp_rows=1024) == 5      # long C4 rows keep the plan
     assert plan(5, 4, 8, 4, 1024, short, [515] * 4, cmp_rows=128) == 1
     assert plan(5, 4, 8, 4, 1024, short, [516] * 4, cmp_rows=160) == 5
-    assert plan(5, 4, 8, 4, 1024, short, [515] * 4, cmp_rows=160) == 5        # wide table: tiled kernel
-    assert plan(5, 4, 8, 4, 1024, short, [515] * 4) == 5                      # table unknown
+    assert plan(5, 4, 8, 4, 1024, short, [515] * 4, cmp_rows=160) == 1        # small entry: live lengths
+    assert plan(5, 4, 8, 4, 1024, short, [515] * 4, cmp_rows=33760) == 1      # a serving-width table (1055 pages)
+    assert plan(5, 4, 8, 4, 1024, short, [515] * 4, cmp_rows=160, small=False) == 5   # sparse entry, wide table
+    assert plan(5, 4, 8, 4, 1024, short, [515] * 4, small=False) == 5         # table unknown
+    wide_cu = list(range(25)) + [24] * 8
+    assert plan(2, 32, 8, 4, 1024, wide_cu, [515] * 24 + [0] * 8, cmp_rows=33760) == 2   # 32 tokens: sparse entry
+    assert plan(2, 32, 8, 4, 1024, wide_cu, [515] * 24 + [0] * 8, cmp_rows=128) == 1
     assert plan(5, 4, 8, 4, 1024, short, [515] * 4, ori_topk=128, cmp_rows=128) == 5   # explicit slots
     assert plan(5, 4, 8, 1, 0, short, [100] * 4) == 5                          # window only: no joint rows
     assert plan(3, 64, 8, 128, 0, list(range(9)) + [8] * 56, [4096] * 8 + [0] * 56) == 1   # padded
