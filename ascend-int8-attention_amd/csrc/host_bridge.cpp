@@ -15,6 +15,7 @@
 namespace {
 
 constexpr long VARIANT_SPARSE = 20, VARIANT_DENSE = 21, VARIANT_SPARSE_SMALL = 22;   // c8_launch.cpp:14-17
+constexpr long VARIANT_DENSE_PAIRED = 23;   // the query-grouped plan (launch_sharedkv_c8_dense_paired)
 
 bool read_u64(PyObject *o, uint64_t *out)
 {
@@ -44,7 +45,8 @@ PyObject *attention(PyObject *, PyObject *const *args, Py_ssize_t nargs)
     int (*launch)(uint32_t, void *, const SharedKVArgs *) =
         variant == VARIANT_SPARSE ? launch_sharedkv_c8_sparse
         : variant == VARIANT_DENSE ? launch_sharedkv_c8_dense
-        : variant == VARIANT_SPARSE_SMALL ? launch_sharedkv_c8_sparse_small : nullptr;
+        : variant == VARIANT_SPARSE_SMALL ? launch_sharedkv_c8_sparse_small
+        : variant == VARIANT_DENSE_PAIRED ? launch_sharedkv_c8_dense_paired : nullptr;
     if (!launch) {
         PyErr_SetString(PyExc_ValueError, "Invalid C8 variant");   // c8_launch.cpp:17
         return nullptr;

@@ -1944,6 +1944,478 @@ c8_rows(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, con
         run_item(lo + j / S, j % S);
 }
 
+// ---- c8_pairs: query-grouped plans (two query tokens per group) ----
+// reference.py:224-323 with query_group 2 (the reference device's C128
+// "paired" plan, c128.cpp:17-23): the tokens 2 j and 2 j + 1 of a request
+// form a group that shares one window list (positions max(0, p0 + 1 - 128)
+// .. p1, up to 129 rows) and, for C128, one compressed list (rows below
+// (p1 + 1) / 128); each token masks what it may not see (its own window,
+// its own compressed count) and keeps its own online softmax.  128-key
+// tiles numbered across both kinds, tile k on partition k % S, no joint
+// rows.  One work-group of 8 waves per (group, partition): the group's
+// tiles are fetched once into a two-tile LDS ring, waves 0-3 compute token
+// 0 and waves 4-7 token 1, each wave taking 32 keys in QK and 128 output
+// columns in PV (the per-row layout of c8_rows).  Work items are
+// (token, partition); items of the second token of a group exit (the
+// group's first token takes both), items of padding or keyless tokens
+// zero-fill them.  At most eight heads (residual codes on).
+struct alignas(16) PairShared {
+    int32_t redmax[2][HEADS][4];   // per token: per-wave tile maxima (fkey)
+    float redsum[2][HEADS][4];     // per token: per-wave weight sums of its two 16-key blocks
+    float asc[2][2][HEADS];        // [token][kind][head]: alpha * softmax_scale
+    int32_t misc[8];
+    float scale[2][D];             // channel scales of the window / compressed cache
+    int8_t p[2][16 * PROW];        // P codes per token [MFMA row][key]
+    int32_t code[CODE_TILES * N];  // row codes of the resident tiles: page * 32 + row, -1 masked
+    uint64_t addr[CODE_TILES * N]; // HBM address of each resident row (masked rows: the Q base)
+    int8_t tile[2][N * D];         // the DMA ring; Q code staging before tile 1
+};
+static_assert(2 * 2 * 16 * QSTAGE <= N * D, "both tokens' Q codes fit one tile buffer");
+static_assert(sizeof(PairShared) <= 160 * 1024, "one work-group per CU");
+
+template <int RATIO, bool STREAM>
+__global__ void __launch_bounds__(THREADS, 1)
+c8_pairs(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, const uint32_t batch_arg,
+         const uint32_t heads_arg, const uint32_t splits, const uint32_t rows_arg, const uint32_t grid,
+         const SharedKVArgs p, const uint32_t fused)
+{
+    static_assert(RATIO == 1 || RATIO == 128, "grouped plans: window-only and C128 launches");
+    __shared__ PairShared s;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, n = lane & 15;
+    const int tok = wave >> 2, tw = wave & 3;   // token of the group, wave within the token
+    const uint32_t G = grid;
+    const uint32_t item = (blockIdx.x & 7u) * (G >> 3) + (blockIdx.x >> 3);
+    if (item >= rows_arg * splits) return;
+    const int S = (int)splits;
+    const int t = (int)(item / splits), part = (int)(item % splits);
+    const int H = (int)heads_arg;               // 1..8
+    const __attribute__((address_space(1))) int32_t *cu = gptr<int32_t>(cu_q);
+    const __attribute__((address_space(1))) int32_t *lens = gptr<int32_t>(seq_lens);
+    const int batch_n = (int)batch_arg;
+    const int mine_b = tid < batch_n ? tid : 0;
+    const int my_cu0 = cu[mine_b], my_cu1 = cu[mine_b + 1], my_len = lens[mine_b];
+    // Q of both tokens (t and t + 1, which exists when t leads a pair):
+    // wave (tok, tw) holds heads tw and tw + 4 of token t + tok, 8 channels
+    // per lane.  Rows past the launch read row t instead (never used).
+    const int tq = t + tok < (int)rows_arg ? t + tok : t;
+    v4i qv[2];
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh)
+        qv[hh] = tw + 4 * hh < H ? *gptr<v4i>(q_base + (((uint64_t)tq * H + tw + 4 * hh) * D + lane * 8) * 2)
+                                 : v4i{0, 0, 0, 0};
+
+    // ---- live shape (attention_impl.h:121-137) and the request of token t ----
+    if (tid == 0) { s.misc[0] = 0; s.misc[1] = -1; s.misc[2] = 0; }
+    __syncthreads();
+    for (int b = tid; b < batch_n; b += THREADS) {
+        const int len = b == tid ? my_len : lens[b];
+        const int c1 = b == tid ? my_cu1 : cu[b + 1];
+        if (len > 0 && c1 >= 0) atomicMax(&s.misc[0], b + 1);
+    }
+    __syncthreads();
+    const int live_batch = uni(s.misc[0]);
+    for (int b = tid; b < live_batch; b += THREADS) {
+        const int c0 = b == tid ? my_cu0 : cu[b];
+        const int c1 = b == tid ? my_cu1 : cu[b + 1];
+        if (c0 <= t && t < c1) {
+            s.misc[1] = b;
+            s.misc[3] = b == tid ? my_len : lens[b];
+            s.misc[4] = c1;
+            s.misc[5] = c0;
+        }
+        if (b == live_batch - 1) s.misc[2] = c1;
+    }
+    __syncthreads();
+    const int end = live_batch ? uni(s.misc[2]) : 0;
+    const int live_tokens = end <= 0 ? 0 : (end < (int)p.tokens ? end : (int)p.tokens);
+    const int batch = uni(s.misc[1]);
+    uint16_t *out_base = reinterpret_cast<uint16_t *>(p.out);
+    float *lse_base = p.lse ? reinterpret_cast<float *>(p.lse) : nullptr;
+    auto zero_token = [&](int tz) {   // output and LSE rows of token tz
+        if (tid < H * (D / 8)) reinterpret_cast<v4i *>(out_base + (int64_t)tz * H * D)[tid] = v4i{0, 0, 0, 0};
+        if (lse_base && tid < H) lse_base[(int64_t)tz * H + tid] = 0.0f;
+    };
+    // Padding tokens (attention_impl.h:443-460) and tokens of no live request.
+    // With a separate merge launch (merge mode 1), partition 0 also marks
+    // the tokens it finalizes or zero-fills as having nothing to fold.
+    auto no_fold = [&](int tz) {
+        if (S > 1 && !fused && tid == 0)
+            reinterpret_cast<float *>(p.partial)[(int64_t)tz * S * HEADS * PART_FLOATS + FOLD_SLOT] = 0.0f;
+    };
+    if (t >= live_tokens || batch < 0) {
+        if (part == 0) {
+            zero_token(t);
+            no_fold(t);
+        }
+        return;
+    }
+    const int c0r = uni(s.misc[5]), c1r = uni(s.misc[4]), len = uni(s.misc[3]);
+    if ((t - c0r) & 1) return;                        // the group's first token takes it
+    const int gs = t + 1 < c1r && t + 1 < live_tokens ? 2 : 1;   // tokens in the group
+    const int p0 = len - c1r + t, plast = p0 + gs - 1;
+    if (p0 < 0) {                                     // negative positions (reference.py:104-105): zero
+        if (part == 0) {
+            for (int k = 0; k < gs; ++k) {
+                zero_token(t + k);
+                no_fold(t + k);
+            }
+        }
+        return;
+    }
+    // ---- the group's lists (reference.py:229-253) ----
+    const int lo0 = p0 + 1 - WINDOW > 0 ? p0 + 1 - WINDOW : 0;
+    const int ori_count = plast + 1 - lo0;            // window rows max(0, p0 + 1 - 128) .. plast
+    const int t0w = (ori_count + N - 1) / N;
+    const int list_len = RATIO == 128 ? (plast + 1) / 128 : 0;
+    const int total = t0w + (list_len + N - 1) / N;
+    const int folded = S < total ? S : total;
+    if (part >= folded) return;
+    const int my_tiles = (total - part + S - 1) / S;
+    // Each token's own window and compressed count.
+    const int ptok = p0 + (tok < gs ? tok : 0);
+    const int own_lo = ptok + 1 - WINDOW > 0 ? ptok + 1 - WINDOW : 0;
+    const int own_count = RATIO == 128 ? (ptok + 1) / 128 : 0;
+    const bool tok_live = tok < gs;
+
+    const __attribute__((address_space(1))) int32_t *otab = gptr<int32_t>(p.oriTable) + (int64_t)batch * p.oriTableWidth;
+    const __attribute__((address_space(1))) int32_t *ctab =
+        RATIO == 128 ? gptr<int32_t>(p.cmpTable) + (int64_t)batch * p.cmpTableWidth : otab;
+    const __attribute__((address_space(1))) float *sinks = gptr<float>(p.sinks);
+    const float sink0 = 2 * g < H ? sinks[2 * g] : 0.0f;
+    const float sink1 = 2 * g + 1 < H ? sinks[2 * g + 1] : 0.0f;
+    const f32x2 scale_pair = *gptr<f32x2>(((tid >> 8) && RATIO != 1 ? p.cmpScale : p.oriScale) +
+                                          (uint64_t)((tid & 255) * 2) * 4);
+    const int c0 = 128 * tw;   // this wave's PV output columns: c0 + 16 j + n
+
+    float mx[2] = {sink0, sink1}, den[2], num[2][8];
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+        den[hh] = part == 0 ? 1.0f : 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) num[hh][j] = 0.0f;
+    }
+
+    // LDS DMA of resident tile i into ring buffer buf, instructions [r0, r0 + count)
+    // of this wave (the layout c8_attention's issue_rows writes).
+    auto issue_rows = [&](int i, int buf, int r0, int count) {
+        const int h = lane >> 5, c = lane & 31;
+        typedef uint64_t u64x2 __attribute__((ext_vector_type(2)));
+        const u64x2 *rows = reinterpret_cast<const u64x2 *>(s.addr + i * N + 16 * wave + 8 * h + r0);
+        u64x2 ra[DMA_PER_TILE / 2];
+#pragma unroll
+        for (int r = 0; r < DMA_PER_TILE / 2; ++r)
+            if (2 * r < count) ra[r] = rows[r];
+        const uint32_t dst = (uint32_t)(uintptr_t)(lds_i8 *)(s.tile[buf]) + 16 * wave * D;
+        const int hx = (h ^ wave) & 1;
+#pragma unroll
+        for (int k = 0; k < DMA_PER_TILE; ++k) {
+            if (k >= count) break;
+            const int r = r0 + k;
+            const int chunk = c ^ r ^ (hx << 3);
+            dma16<STREAM>(ra[k >> 1][k & 1] + (uint32_t)(chunk << 4), (uint32_t)uni((int)(dst + 2 * r * D)));
+        }
+    };
+    constexpr int DMA_STEP = DMA_PER_TILE / 4;
+
+    v4i qa0[8], qa1[8];
+    for (int first = 0; first < my_tiles; first += CODE_TILES) {
+        const int ntiles = my_tiles - first < CODE_TILES ? my_tiles - first : CODE_TILES;
+        // ---- row codes of partition tiles [first, first + ntiles) ----
+        for (int i = tid; i < ntiles * N; i += THREADS) {
+            s.code[i] = -1;
+            s.addr[i] = p.q;
+        }
+        constexpr int PER = CODE_TILES * N / THREADS;
+        int tpage[PER], tidx[PER];
+#pragma unroll
+        for (int e = 0; e < PER; ++e) {
+            const int i = tid + e * THREADS;
+            tidx[e] = -1;
+            tpage[e] = -1;
+            if (i >= ntiles * N) continue;
+            const int k = part + S * (first + i / N), r = i % N;
+            if (k < t0w) {
+                const int j = k * N + r;      // place in the group's window list
+                const int idx = lo0 + j;
+                if (j < ori_count && idx / BLOCK_ROWS < (int)p.oriTableWidth) {
+                    tidx[e] = idx;
+                    tpage[e] = otab[idx / BLOCK_ROWS];
+                }
+            } else if (RATIO == 128) {
+                const int idx = (k - t0w) * N + r;
+                if (idx < list_len && idx / BLOCK_ROWS < (int)p.cmpTableWidth) {
+                    tidx[e] = idx;
+                    tpage[e] = ctab[idx / BLOCK_ROWS];
+                }
+            }
+        }
+        if (first == 0) *reinterpret_cast<f32x2 *>(&s.scale[tid >> 8][(tid & 255) * 2]) = scale_pair;
+        lds_barrier();                        // the -1 fill is complete before the writes below
+#pragma unroll
+        for (int e = 0; e < PER; ++e) {
+            if (tidx[e] < 0) continue;
+            const int i = tid + e * THREADS;
+            const bool window = part + S * (first + i / N) < t0w;
+            const bool ok = tpage[e] >= 0 && (!window || (uint32_t)tpage[e] < p.oriPages);
+            if (ok) {
+                s.code[i] = tpage[e] * BLOCK_ROWS + tidx[e] % BLOCK_ROWS;
+                s.addr[i] = (window ? p.ori : p.cmp) + (uint64_t)tpage[e] * (window ? p.oriStride : p.cmpStride) +
+                            (uint64_t)((tidx[e] % BLOCK_ROWS) * D);
+            }
+        }
+        lds_barrier();                        // codes visible
+
+        issue_rows(0, 0, 0, DMA_PER_TILE);
+        if (first == 0) {
+            // ---- Q folding and residual split per token and kind (reference.py:274-279),
+            // staged in tile buffer 1, then picked up in the MFMA A layout ----
+            // Window tiles are tiles 0 .. t0w - 1 (t0w <= 2): this partition
+            // holds one when its first tile is one; a compressed one when its
+            // last tile is one.
+            const bool want[2] = {part < t0w, part + S * (my_tiles - 1) >= t0w};
+            int lx = lane;
+            asm volatile("" : "+v"(lx));
+            const int qe0 = lx * 8;
+#pragma unroll
+            for (int kind = 0; kind < 2; ++kind) {
+                if (!want[kind]) continue;
+                const float *scale = s.scale[kind] + qe0;
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    const int h = tw + 4 * hh;
+                    const uint32_t qw[4] = {(uint32_t)qv[hh].x, (uint32_t)qv[hh].y, (uint32_t)qv[hh].z, (uint32_t)qv[hh].w};
+                    float f[8];
+                    float amax = 0.0f;
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        f[e] = bf16_to_f32((qw[e >> 1] >> (16 * (e & 1))) & 0xffffu) * scale[e];
+                        amax = fmaxf(amax, fabsf(f[e]));
+                    }
+                    amax = wave_max(amax);
+                    float alpha = amax * (float)(1.0 / 127.0);
+                    alpha = alpha < 1e-12f ? 1e-12f : alpha;
+                    const float inv = 1.0f / alpha;
+                    uint32_t hiw[2] = {0, 0}, low[2] = {0, 0};
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) {
+                        const float x = clamp127(f[e] * inv);
+                        const float hi = __builtin_rintf(x);
+                        const float lo_ = __builtin_rintf((x - hi) * 127.0f);
+                        hiw[e >> 2] |= ((uint32_t)(int32_t)hi & 0xffu) << (8 * (e & 3));
+                        low[e >> 2] |= ((uint32_t)(int32_t)lo_ & 0xffu) << (8 * (e & 3));
+                    }
+                    int8_t *stage = s.tile[1] + (tok * 2 + kind) * 16 * QSTAGE;
+                    *reinterpret_cast<u32x2 *>(stage + row_of(h, 0) * QSTAGE + qe0) = u32x2{hiw[0], hiw[1]};
+                    *reinterpret_cast<u32x2 *>(stage + row_of(h, 1) * QSTAGE + qe0) = u32x2{low[0], low[1]};
+                    if (lane == 0) s.asc[tok][kind][h] = alpha * p.softmaxScale;
+                }
+            }
+            lds_barrier();
+            const int8_t *st0 = s.tile[1] + (tok * 2) * 16 * QSTAGE, *st1 = st0 + 16 * QSTAGE;
+#pragma unroll
+            for (int jj = 0; jj < 8; ++jj) {
+                qa0[jj] = want[0] ? *reinterpret_cast<const v4i *>(st0 + n * QSTAGE + 64 * jj + 16 * g) : v4i{0, 0, 0, 0};
+                qa1[jj] = want[1] ? *reinterpret_cast<const v4i *>(st1 + n * QSTAGE + 64 * jj + 16 * g) : v4i{0, 0, 0, 0};
+            }
+            lds_barrier();                    // every wave holds its Q codes: buffer 1 is free
+        }
+        if (ntiles > 1) issue_rows(1, 1, 0, DMA_PER_TILE);
+
+        for (int i = 0; i < ntiles; ++i) {
+            const int k = part + S * (first + i);
+            const int kind = k >= t0w ? 1 : 0;
+            const int buf = i & 1;
+            if (i == 0 && ntiles > 1) vm_wait<DMA_PER_TILE>();
+            else vm_wait<0>();
+            lds_barrier();   // tile i has landed for every wave; every wave is done with tile i - 1
+            const bool stream_next = i >= 1 && i + 1 < ntiles;
+            if (stream_next) issue_rows(i + 1, buf ^ 1, 0, DMA_STEP);
+            const int8_t *tb = s.tile[buf];
+
+            // ---- QK: S[16 rows][32 keys of this wave] (reference.py:286-289) ----
+            v4i sacc[2] = {v4i{0, 0, 0, 0}, v4i{0, 0, 0, 0}};
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                const int sl = slot_of(32 * tw + 16 * kb + n);
+#pragma unroll
+                for (int jq = 0; jq < 2; ++jq) {   // 256 channels at a time
+                    v4i b[4];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) b[j] = *reinterpret_cast<const v4i *>(tb + tile_offset(sl, 4 * (4 * jq + j) + g));
+                    if (kind) {
+#pragma unroll
+                        for (int j = 0; j < 4; ++j)
+                            sacc[kb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(qa1[4 * jq + j], b[j], sacc[kb], 0, 0, 0);
+                    } else {
+#pragma unroll
+                        for (int j = 0; j < 4; ++j)
+                            sacc[kb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(qa0[4 * jq + j], b[j], sacc[kb], 0, 0, 0);
+                    }
+                }
+            }
+            if (stream_next) issue_rows(i + 1, buf ^ 1, DMA_STEP, DMA_STEP);
+            // ---- logits with this token's masks, tile maximum (reference.py:288-303) ----
+            float lg[2][2];
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+                const int key = 32 * tw + 16 * kb + n;
+                const int idx = kind ? (k - t0w) * N + key : lo0 + k * N + key;
+                const bool mine = kind ? idx < own_count : (idx >= own_lo && idx <= ptok);
+                const bool valid = tok_live && mine && s.code[i * N + key] >= 0;
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    float dots = (float)sacc[kb][2 * hh];
+                    dots = dots + (float)sacc[kb][2 * hh + 1] * (float)(1.0 / 127.0);
+                    const float l = dots * s.asc[tok][kind][2 * g + hh];
+                    lg[kb][hh] = valid ? l : -1e30f;
+                }
+            }
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                const int kmax = row16_max_key(max(fkey(lg[0][hh]), fkey(lg[1][hh])));
+                if (n == 0) s.redmax[tok][2 * g + hh][tw] = kmax;
+            }
+            lds_barrier();
+            if (stream_next) issue_rows(i + 1, buf ^ 1, 2 * DMA_STEP, DMA_STEP);
+            float mnew[2], factor[2];
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                const v4i a = *reinterpret_cast<const v4i *>(&s.redmax[tok][2 * g + hh][0]);
+                mnew[hh] = fkey_value(max(max(fkey(mx[hh]), a.x), max(max(a.y, a.z), a.w)));
+            }
+            {
+                const bool odd = n & 1;   // exp(max_old - max_new), one exponential per lane pair
+                const float mine = sk_expf_nonpos(odd ? mx[1] - mnew[1] : mx[0] - mnew[0]);
+                const float other = dpp<DPP_XOR1>(mine);
+                factor[0] = odd ? other : mine;
+                factor[1] = odd ? mine : other;
+            }
+            // ---- weights, pairwise tile sum, P codes (reference.py:304-312) ----
+            int8_t *pt = s.p[tok];
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                float blk[2];
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb) {
+                    const int key = 32 * tw + 16 * kb + n;
+                    const float w = sk_expf_nonpos(lg[kb][hh] - mnew[hh]);
+                    const float x = w * 127.0f;
+                    const float ph = __builtin_rintf(x);
+                    const float pl = __builtin_rintf((x - ph) * 127.0f);
+                    pt[row_of(2 * g + hh, 0) * PROW + key] = (int8_t)(int32_t)ph;
+                    pt[row_of(2 * g + hh, 1) * PROW + key] = (int8_t)(int32_t)pl;
+                    blk[kb] = row16_tree_sum(w);   // one 16-key block
+                }
+                if (n == 0) s.redsum[tok][2 * g + hh][tw] = blk[0] + blk[1];   // blocks 2 tw and 2 tw + 1
+            }
+            lds_barrier();
+            if (stream_next) issue_rows(i + 1, buf ^ 1, 3 * DMA_STEP, DMA_STEP);
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+                const f32x4 a = *reinterpret_cast<const f32x4 *>(&s.redsum[tok][2 * g + hh][0]);
+                const float tile_sum = (a.x + a.y) + (a.z + a.w);   // pairwise over the eight blocks
+                den[hh] = den[hh] * factor[hh] + tile_sum;
+            }
+            // ---- PV: [16 rows][this wave's 128 columns] (reference.py:310-316),
+            // in two halves of 64 columns, each followed by its FP32 epilogue
+            // (reference.py:313-316): the registers of a deferred epilogue do
+            // not fit beside both kinds' Q codes of the wave's token ----
+            const lds_i8 *vbase = (const lds_i8 *)(tb);
+#pragma unroll
+            for (int jh = 0; jh < 2; ++jh) {
+                v4i vacc[4];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) vacc[j] = v4i{0, 0, 0, 0};
+#pragma unroll
+                for (int kb = 0; kb < 2; ++kb) {
+                    const v4i pa = *reinterpret_cast<const v4i *>(pt + n * PROW + 64 * kb + 16 * g);
+                    const int sl_lo = slot_of(64 * kb + 16 * g + (n >> 1));
+                    const int sl_hi = slot_of(64 * kb + 16 * g + 8 + (n >> 1));
+                    v2i b0[4], b1[4];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const int chunk = 8 * tw + 4 * jh + j;
+                        b0[j] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i *)(vbase + tile_offset(sl_lo, chunk) + 8 * (n & 1)));
+                        b1[j] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i *)(vbase + tile_offset(sl_hi, chunk) + 8 * (n & 1)));
+                    }
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const v4i vb = {b0[j].x, b0[j].y, b1[j].x, b1[j].y};
+                        vacc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(pa, vb, vacc[j], 0, 0, 0);
+                    }
+                }
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        float dots = (float)vacc[j][2 * hh];
+                        dots = dots + (float)vacc[j][2 * hh + 1] * (float)(1.0 / 127.0);
+                        const float pv = dots * s.scale[kind][c0 + 16 * (4 * jh + j) + n] * (float)(1.0 / 127.0);
+                        num[hh][4 * jh + j] = num[hh][4 * jh + j] * factor[hh] + pv;
+                    }
+            }
+            mx[0] = mnew[0];
+            mx[1] = mnew[1];
+        }
+        if (first + CODE_TILES < my_tiles) __syncthreads();   // s.code and the tile buffers are rebuilt next
+    }
+    const int tt = t + tok;   // this wave's token
+    uint16_t *out_row = out_base + (int64_t)tt * H * D;
+    if (folded == 1) {
+        // ---- finalize (reference.py:317-323 with one partition) ----
+        if (part == 0 && tok == 0)
+            for (int k = 0; k < gs; ++k) no_fold(t + k);
+        if (!tok_live) return;
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            const int h = 2 * g + hh;
+            if (h >= H) continue;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) out_row[h * D + c0 + 16 * j + n] = (uint16_t)pack_bf16(num[hh][j] / den[hh], 0.0f);
+            if (lse_base && tw == 0 && n == 0) lse_base[(int64_t)tt * H + h] = mx[hh] + logf(den[hh]);
+        }
+        return;
+    }
+    // ---- publish this partition's state of each token, the last partition
+    // of the group to finish folds both (c8_attention's fused merge) ----
+    if (tok_live) {
+        const __amdgpu_buffer_rsrc_t states =
+            row_states(reinterpret_cast<float *>(p.partial) + (int64_t)tt * S * HEADS * PART_FLOATS);
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+            const int base = ((part * HEADS + 2 * g + hh) * PART_FLOATS) * 4;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) state_store<SC1>(num[hh][j], states, base + (c0 + 16 * j + n) * 4);
+            if (tw == 0 && n == 0) {
+                state_store<SC1>(mx[hh], states, base + 512 * 4);
+                state_store<SC1>(den[hh], states, base + 513 * 4);
+            }
+        }
+    }
+    if (!fused) {
+        if (part == 0 && tid == 0)
+            for (int k = 0; k < gs; ++k)
+                state_store<SC1>((float)folded,
+                                 row_states(reinterpret_cast<float *>(p.partial) + (int64_t)(t + k) * S * HEADS * PART_FLOATS),
+                                 FOLD_SLOT * 4);
+        return;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    uint32_t *tickets = reinterpret_cast<uint32_t *>(p.workspace);
+    if (tid == 0) s.misc[6] = (int)__hip_atomic_fetch_add(&tickets[t], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (s.misc[6] != folded - 1) return;
+    if (tid == 0) __hip_atomic_store(&tickets[t], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+#pragma nounroll
+    for (int k = 0; k < gs; ++k)
+        fold_row<SC1>(row_states(reinterpret_cast<float *>(p.partial) + (int64_t)(t + k) * S * HEADS * PART_FLOATS),
+                      folded, tid, out_base + (int64_t)(t + k) * H * D, lse_base ? lse_base + (int64_t)(t + k) * H : nullptr,
+                      H);
+}
+
 // ---- INT8 cache writer (cache_write.cpp:9-88): one wave per update row ----
 template <typename Index, bool Paired>
 __global__ void __launch_bounds__(256)
@@ -2104,6 +2576,28 @@ int launch_attention(hipStream_t stream, const SharedKVArgs *a, const SharedKVDe
     return (int)hipGetLastError();
 }
 
+// Query-grouped launch (two tokens per group, c8_pairs): ratio 1 or 128, at
+// most eight heads, no explicit original slots.  The partition plan is the
+// launch's (`splits`); graph padding is zero-filled but not re-planned.
+int launch_paired(hipStream_t stream, const SharedKVArgs *a)
+{
+    if (check_attention(a)) return (int)hipErrorInvalidValue;
+    if ((a->ratio != 1 && a->ratio != 128) || a->heads > HEADS || a->oriIndices) return (int)hipErrorInvalidValue;
+    if (a->tokens == 0) return (int)hipSuccess;
+    const uint32_t splits = a->splits, rows = a->tokens;
+    const uint32_t grid = (rows * splits + 7u) & ~7u;
+    const uint32_t fused = splits > 1 && g_merge_mode.load(std::memory_order_relaxed) == 0;
+    const bool streamed = a->ratio == 128 && a->tokens <= STREAM_TOKENS_C128 * a->batch;
+    const auto kernel = a->ratio == 1 ? &c8_pairs<1, false>
+                        : streamed    ? &c8_pairs<128, true>
+                                      : &c8_pairs<128, false>;
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(THREADS), 0, stream, a->cuQ, a->seqLens, a->q, a->batch, a->heads,
+                       splits, rows, grid, *a, fused);
+    if (splits > 1 && !fused)
+        hipLaunchKernelGGL(c8_merge, dim3(rows), dim3(THREADS), 0, stream, *a, splits);
+    return (int)hipGetLastError();
+}
+
 // ---- scratch of the allocation-free entry point ----
 // One array per GPU with a fixed layout: the merge tickets (one uint32 per
 // row) in the first NOALLOC_TICKET_BYTES, the partition states from there to
@@ -2200,6 +2694,13 @@ int launch_sharedkv_c8_dense(uint32_t blocks, void *stream, const SharedKVArgs *
     if (!blocks) return (int)hipSuccess;
     if (!args || (args->ratio != 128 && args->ratio != 1)) return (int)hipErrorInvalidValue;
     return launch_attention<false>(static_cast<hipStream_t>(stream), args, nullptr);
+}
+
+int launch_sharedkv_c8_dense_paired(uint32_t blocks, void *stream, const SharedKVArgs *args)
+{
+    if (!blocks) return (int)hipSuccess;
+    if (!args) return (int)hipErrorInvalidValue;
+    return launch_paired(static_cast<hipStream_t>(stream), args);
 }
 
 int sharedkv_c8_attention_debug(void *stream, const SharedKVArgs *args, const SharedKVDebug *debug)

@@ -104,15 +104,17 @@ class PreparedAttention:
             raise ValueError("Invalid FP32 LSE[T,H] output buffer")
 
         # Tuning knobs of the Ascend planner.  Only the ones that change this
-        # build's numerics (tile_size, splits) are honoured; the rest are
-        # validated for type and recorded.  adaptive_splits has nothing left
-        # to switch: the kernel always adapts the partition count to the live
-        # rows of a padded launch (c8_attention.device_splits).  query_group
-        # is validated and not applied: every query row runs its own key list,
-        # and self.query_group = 1 tells callers which plan ran.  The
-        # reference's C8 path likewise runs its kernel's own plan whatever
-        # query_group asks (c8_attention.py:74-113; its tests rebuild the
-        # oracle plan from the device's choice, attention_cases.py:56-111).
+        # build's numerics (tile_size, splits, query_group) are honoured; the
+        # rest are validated for type and recorded.  adaptive_splits has
+        # nothing left to switch: the kernel always adapts the partition count
+        # to the live rows of a padded launch (c8_attention.device_splits).
+        # query_group 2 on a C128 or window-only launch of at most eight heads
+        # without explicit slots runs the paired plan (reference.py:224-323
+        # with query_group 2; launch_sharedkv_c8_dense_paired); any other
+        # request runs the ungrouped plan, and self.query_group tells callers
+        # which plan ran (the reference's C8 path likewise runs its kernel's
+        # own plan, c8_attention.py:74-113; its tests rebuild the oracle plan
+        # from the device's choice, attention_cases.py:56-111).
         if tile_size is not None and tile_size != c8_attention.TILE:
             raise ValueError(f"This build tiles keys in groups of {c8_attention.TILE}; tile_size must be None or "
                              f"{c8_attention.TILE}")
@@ -121,7 +123,9 @@ class PreparedAttention:
         if splits is not None and (not isinstance(splits, int) or not 1 <= splits <= c8_attention.MAX_SPLITS):
             raise ValueError(f"Expected 1..{c8_attention.MAX_SPLITS} KV partitions")
         self.tile_size = c8_attention.TILE
-        self.query_group = 1
+        paired = (query_group == 2 and case.ratio in (1, 128) and heads <= c8_attention.HEADS
+                  and case.ori_indices is None)
+        self.query_group = 2 if paired else 1
         self.adaptive_splits = bool(adaptive_splits)
         self.trim_cube_tails = bool(trim_cube_tails)
         self.dynamic_c4 = self.dynamic_c128 = self.dynamic_grouped_c128 = False
@@ -135,9 +139,14 @@ class PreparedAttention:
             self.args = None
             return
         ori_topk = case.ori_indices.shape[-1] if case.ori_indices is not None else 0
-        self.splits = splits if splits is not None else c8_attention.choose_splits(
-            tokens * c8_attention.head_groups(heads), case.ratio,
-            case.cmp_indices.shape[-1] if case.ratio == 4 else 0, max_seq_len, ori_topk)
+        if splits is not None:
+            self.splits = splits
+        elif paired:
+            self.splits = c8_attention.choose_paired_splits(tokens, case.ratio, max_seq_len)
+        else:
+            self.splits = c8_attention.choose_splits(
+                tokens * c8_attention.head_groups(heads), case.ratio,
+                case.cmp_indices.shape[-1] if case.ratio == 4 else 0, max_seq_len, ori_topk)
 
         ptr = lambda t: t.data_ptr() if t is not None else 0  # noqa: E731
         cmp = case.cmp if case.ratio != 1 else None
@@ -165,6 +174,8 @@ class PreparedAttention:
                              "block32 pages, top-k <= 1024, at most 1024 explicit original slots)")
         prepared = c8_attention.prepare(self, scratch_allocator=scratch_allocator)
         self.__dict__.update(prepared.__dict__)
+        if paired:
+            self.variant = c8_attention.VARIANT_DENSE_PAIRED
 
     def _rebind_same_geometry(self, case, *, output=None, lse_output=None):
         """Serving fast path: same geometry, new tensors (attention.py:233-247)."""
@@ -188,8 +199,8 @@ class PreparedAttention:
         (default: the case's, read back to the host); equals .splits unless
         graph padding leaves rows idle.  merge_mode is the library's
         (sharedkv_c8_set_merge_mode): 1 keeps the launch plan."""
-        if not self.blocks:
-            return self.splits
+        if not self.blocks or self.query_group != 1:
+            return self.splits          # the paired plan keeps the launch's partitions
         c = self.case
         cu_q = c.cu_q.cpu().tolist() if cu_q is None else cu_q
         seq_lens = c.seq_lens.cpu().tolist() if seq_lens is None else seq_lens

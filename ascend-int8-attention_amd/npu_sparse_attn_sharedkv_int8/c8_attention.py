@@ -48,6 +48,7 @@ SPLITS_MANY_ROWS = 3
 PARTIAL_FLOATS = 520       # per (token, partition, head): 512 numerator, max, denominator, pad
 
 VARIANT_SPARSE, VARIANT_DENSE, VARIANT_SPARSE_SMALL = 20, 21, 22
+VARIANT_DENSE_PAIRED = 23      # the query-grouped (two tokens per group) plan
 
 # A workspace of this size serves any launch of up to WORKSPACE_ROWS rows (one
 # uint32 merge ticket per row), for callers that size one shared workspace up
@@ -96,6 +97,15 @@ def choose_splits(tokens, ratio, topk, max_seq_len=None, ori_topk=0):
     if tokens <= 0:
         return 1
     return plan_splits(tokens, max_tiles(ratio, topk, max_seq_len, ori_topk))
+
+
+def choose_paired_splits(tokens, ratio, max_seq_len=None):
+    """KV partitions of a paired launch (query_group 2): the plan of its
+    groups (at most ceil(tokens / 2) of them), whose window list can take a
+    second tile (up to 129 rows)."""
+    if tokens <= 0:
+        return 1
+    return plan_splits((tokens + 1) // 2, max_tiles(ratio, 0, max_seq_len) + 1)
 
 
 def live_shape(cu_q, seq_lens, tokens):

@@ -20,7 +20,8 @@ from types import SimpleNamespace
 from ._paths import native_path
 
 VARIANT_SPARSE, VARIANT_DENSE, VARIANT_SPARSE_SMALL = 20, 21, 22
-ATTENTION_VARIANT_COUNT = 23
+VARIANT_DENSE_PAIRED = 23          # the query-grouped plan (launch_sharedkv_c8_dense_paired)
+ATTENTION_VARIANT_COUNT = 24
 
 
 class SharedKVArgs(ctypes.Structure):
@@ -48,6 +49,7 @@ class SharedKVDebug(ctypes.Structure):
 
 
 EXPORTS = ("launch_sharedkv_c8_sparse", "launch_sharedkv_c8_dense", "launch_sharedkv_c8_sparse_small",
+           "launch_sharedkv_c8_dense_paired",
            "launch_sharedkv_c8_noalloc", "sharedkv_c8_attention_debug", "launch_cache_write",
            "sharedkv_c8_workspace_bytes", "sharedkv_c8_partial_bytes", "sharedkv_c8_noalloc_scratch_bytes",
            "sharedkv_c8_noalloc_layout", "sharedkv_c8_set_merge_mode", "sharedkv_attention_args_size", "sharedkv_cache_args_size",
@@ -67,7 +69,7 @@ def library():
     import torch  # noqa: F401  (binds the library to torch's HIP runtime)
     lib = ctypes.CDLL(str(native_path()))
     for name in ("launch_sharedkv_c8_sparse", "launch_sharedkv_c8_dense", "launch_sharedkv_c8_sparse_small",
-                 "launch_sharedkv_c8_noalloc"):
+                 "launch_sharedkv_c8_dense_paired", "launch_sharedkv_c8_noalloc"):
         fn = getattr(lib, name)
         fn.argtypes = [ctypes.c_uint32, ctypes.c_void_p, ctypes.c_void_p]
         fn.restype = ctypes.c_int
@@ -135,7 +137,8 @@ class _Host:
         self.bridge = None if use_ctypes else bridge()
         self._launchers = {VARIANT_SPARSE: lib.launch_sharedkv_c8_sparse,
                            VARIANT_DENSE: lib.launch_sharedkv_c8_dense,
-                           VARIANT_SPARSE_SMALL: lib.launch_sharedkv_c8_sparse_small}
+                           VARIANT_SPARSE_SMALL: lib.launch_sharedkv_c8_sparse_small,
+                           VARIANT_DENSE_PAIRED: lib.launch_sharedkv_c8_dense_paired}
 
     def attention(self, address, blocks, variant, device):
         """Launch on the current stream of `device` (c8_launch.cpp:20-25)."""

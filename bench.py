@@ -323,7 +323,7 @@ def host_cores():
     return max(1, min(share, affinity))
 
 
-def cpu_baseline(dc, layers, splits, seconds, cmp_rows):
+def cpu_baseline(dc, layers, splits, seconds, cmp_rows, query_group=1):
     """Time the C restatement on whole launches of the same workload until
     about `seconds` of wall time have passed (bounded sample), on every host
     core of the job's share and then on one thread (half the time)."""
@@ -332,7 +332,7 @@ def cpu_baseline(dc, layers, splits, seconds, cmp_rows):
     from tests import workloads
     hosts = [workloads.oracle_case(dc.host(layer)) for layer in range(min(layers, 2))]
     m = dc.meta
-    joint_dense = c8_attention.joint_plan(m["ratio"], dc.heads, False) and m["ratio"] == 128
+    joint_dense = c8_attention.joint_plan(m["ratio"], dc.heads, False) and m["ratio"] == 128 and query_group == 1
     joint_sparse = m["ratio"] == 4 and splits == 1 and c8_attention.joint_launch(
         splits, int(m["cu_q"][-1]), dc.heads, 4, m["cu_q"], m["seq_lens"], cmp_rows=cmp_rows)
 
@@ -341,7 +341,8 @@ def cpu_baseline(dc, layers, splits, seconds, cmp_rows):
         start = time.perf_counter()
         while time.perf_counter() - start < budget:
             ora.tiled_attention(hosts[launches % len(hosts)], tile=128, splits=splits, return_lse=False,
-                                joint_dense=joint_dense, joint_sparse=joint_sparse, threads=threads)
+                                joint_dense=joint_dense, joint_sparse=joint_sparse, threads=threads,
+                                query_group=query_group)
             queries += int(dc.meta["cu_q"][-1])
             launches += 1
         elapsed = time.perf_counter() - start
@@ -439,6 +440,8 @@ def main():
     ap.add_argument("--page-stride", type=int, default=None, help="override the workload's page stride (bytes)")
     ap.add_argument("--merge", type=int, default=0, help="0: fused partition merge, 1: separate merge launch")
     ap.add_argument("--heads", type=int, default=8, help="query heads per token (the metric is quoted at 8)")
+    ap.add_argument("--query-group", type=int, default=None, choices=[1, 2],
+                    help="2: the paired plan (two query tokens share each tile) for C128 / window-only launches")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-floor", action="store_true", help="skip the gather-floor and streaming-read legs")
@@ -483,16 +486,19 @@ def main():
     torch.cuda.synchronize()
     log(f"[bench] generated in {time.perf_counter() - t0:.1f} s: ori pages {dc.ori.pages}, "
         f"cmp pages {dc.cmp.pages if dc.cmp else 0}")
-    ops = [PreparedAttention(dc.cases[l], dc.ori_scales[l], dc.cmp_scales[l], splits=args.splits)
+    ops = [PreparedAttention(dc.cases[l], dc.ori_scales[l], dc.cmp_scales[l], splits=args.splits,
+                             query_group=args.query_group)
            for l in range(layers)]
     splits = ops[0].splits
+    group = ops[0].query_group
     from npu_sparse_attn_sharedkv_int8 import c8_attention
     # The partitions the kernel runs: the device re-plans joint C128 launches
-    # (and padded ones, below) from the live metadata.
+    # (and padded ones, below) from the live metadata; the paired plan keeps
+    # the launch's.
     cmp_rows = ops[0].args.cmpTableWidth * c8_attention.BLOCK
-    device_plan = c8_attention.device_splits(splits, int(dc.meta["cu_q"][-1]), args.heads, ratio, 1024,
-                                             dc.meta["cu_q"], dc.meta["seq_lens"], fused=args.merge == 0,
-                                             cmp_rows=cmp_rows)
+    device_plan = splits if group != 1 else c8_attention.device_splits(
+        splits, int(dc.meta["cu_q"][-1]), args.heads, ratio, 1024, dc.meta["cu_q"], dc.meta["seq_lens"],
+        fused=args.merge == 0, cmp_rows=cmp_rows)
     live_queries = int(sum(queries))
     bytes_per_launch = [dc.algorithmic_bytes(l) for l in range(layers)]
 
@@ -504,11 +510,11 @@ def main():
     torch.cuda.synchronize()
     graphs = {"attention": capture(stream, args.steps, lambda i: ops[i % layers].run(), torch)}
     tokens = int(dc.meta["cu_q"][-1])
-    joint = device_plan == 1 and c8_attention.joint_launch(splits, tokens, args.heads, ratio, dc.meta["cu_q"],
-                                                           dc.meta["seq_lens"], cmp_rows=cmp_rows)
+    joint = group == 1 and device_plan == 1 and c8_attention.joint_launch(
+        splits, tokens, args.heads, ratio, dc.meta["cu_q"], dc.meta["seq_lens"], cmp_rows=cmp_rows)
     rows_kernel = ratio == 4 and device_plan == 1 and tokens * ((args.heads + 7) // 8) > c8_attention.CORES
     floor = None
-    if not args.no_floor and args.heads == 8 and not joint and not rows_kernel:
+    if not args.no_floor and args.heads == 8 and not joint and not rows_kernel and group == 1:
         streamed = tokens <= (4 if ratio == 4 else 1 if ratio == 128 else 0) * len(queries)
         log(f"[bench] floor legs: gather of the launch's rows and a streaming read (non-temporal {streamed})")
         floor = FloorLegs(dc, layers, device_plan, torch, streamed)
@@ -547,7 +553,7 @@ def main():
     # live rows as extra partitions (c8_attention.device_splits).
     live_seqs = args.live if args.live is not None else (8 if args.workload == "headline" else 0)
     padded = None
-    if 0 < live_seqs < len(queries) and args.merge == 0:
+    if 0 < live_seqs < len(queries) and args.merge == 0 and group == 1:
         import dataclasses
         cu_full, lens_full = dc.meta["cu_q"].copy(), dc.meta["seq_lens"].copy()
         cu = cu_full.copy()
@@ -599,7 +605,8 @@ def main():
     keys = dc.selected_keys(0)
     int8_ops = keys * 16 * 512 * 2 * 2 * ((args.heads + 7) // 8)   # per group of eight heads
     metric = (METRIC if args.workload == "headline" and args.heads == 8 else
-              f"INT8 sharedKV attention queries/s + HBM GB/s, {args.workload}, {args.heads} heads")
+              f"INT8 sharedKV attention queries/s + HBM GB/s, {args.workload}, {args.heads} heads"
+              + (", paired plan" if group == 2 else ""))
     record = {
         "metric": metric, "value": live_queries / (ms_per_step * 1e-3), "unit": "queries/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms_per_step, "higher_is_better": True,
@@ -608,9 +615,7 @@ def main():
                    "dim": 512, "ratio": ratio, "topk": 1024 if ratio == 4 else 0, "window": 128,
                    "page_stride": stride, "layers_rotated": layers, "tile": 128, "splits": splits,
                    "device_splits": device_plan,
-                   "joint_rows": bool(device_plan == 1 and c8_attention.joint_launch(
-                       splits, int(dc.meta["cu_q"][-1]), args.heads, ratio, dc.meta["cu_q"], dc.meta["seq_lens"],
-                       cmp_rows=cmp_rows)),
+                   "joint_rows": bool(joint), "query_group": group,
                    "lse": False, "merge": "fused" if args.merge == 0 else "separate launch",
                    "timing": "median of 9 alternating rounds (reference protocol), each one replay of a graph of "
                              "K launches between HIP events on its stream, after 3 untimed replays"},
@@ -630,7 +635,7 @@ def main():
     copy_calibration(args.copy_calibration, torch)
     if not args.no_cpu:
         log(f"[bench] CPU baseline ({args.cpu_seconds:.0f} s sample)")
-        record["cpu_baseline"] = cpu_baseline(dc, layers, device_plan, args.cpu_seconds, cmp_rows)
+        record["cpu_baseline"] = cpu_baseline(dc, layers, device_plan, args.cpu_seconds, cmp_rows, group)
     print(json.dumps(record), flush=True)
 
 

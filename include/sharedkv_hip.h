@@ -101,6 +101,18 @@ int launch_sharedkv_c8_sparse_small(uint32_t blocks, void *stream, const SharedK
  * Also serves ratio 1 (window only; the reference's legacy R1 plan). */
 int launch_sharedkv_c8_dense(uint32_t blocks, void *stream, const SharedKVArgs *args);
 
+/* Query-grouped C128 / window-only attention: the reference device's paired
+ * plan (c128.cpp:17-23, numerics reference.py:224-323 with query_group 2),
+ * here chosen by the caller (PreparedAttention(query_group=2)); the
+ * reference's launcher picks it inside launch_sharedkv_c8_dense.  Tokens
+ * 2j and 2j + 1 of each request form a group sharing one window list (up to
+ * 129 rows) and one compressed list, each masking what it may not see;
+ * 128-key tiles, tile k on partition k % splits, no joint rows.  ratio 1 or
+ * 128, heads <= 8, no explicit original slots (else hipErrorInvalidValue).
+ * Scratch as for the other launches at rows = tokens; graph padding rows
+ * are zero-filled and the launch keeps its partition plan. */
+int launch_sharedkv_c8_dense_paired(uint32_t blocks, void *stream, const SharedKVArgs *args);
+
 /* Same launch as the three above (ratio taken from args->ratio), with the
  * integer dumps written to `debug`.  Test entry; slower. */
 int sharedkv_c8_attention_debug(void *stream, const SharedKVArgs *args, const SharedKVDebug *debug);

@@ -368,10 +368,11 @@ def test_against_reference_vectors(name):
         ori_indices=torch.from_numpy(z["ori_indices"]).to(dev) if "ori_indices" in z.files else None)
     live = int(z["cu_q"][-1])
 
-    def launch(splits):
+    def launch(splits, query_group=None):
         op = PreparedAttention(case, torch.from_numpy(z["ori_scale"]).to(dev),
                                torch.from_numpy(z["cmp_scale"]).to(dev) if ratio != 1 else None, splits=splits,
-                               return_lse=True)
+                               return_lse=True, query_group=query_group)
+        assert op.query_group == (query_group or 1)
         op.run()
         torch.cuda.synchronize()
         return bits_of(op.out)[:live], op.lse.cpu().numpy()[:live]
@@ -402,12 +403,15 @@ def test_against_reference_vectors(name):
         # `splits`: 128-key tiles, ungrouped, and joint rows (C128
         # joint_dense, C4 joint_sparse) exactly when the HIP plan takes them
         # (one partition, at most eight heads, no explicit slots).
+        # The paired plan (query_group 2, launch_sharedkv_c8_dense_paired)
+        # covers the stored 128-key, non-joint C128 and window-only G2 plans.
         joint_here = splits == 1 and c8_attention.joint_plan(ratio, z["q"].shape[1], "ori_indices" in z.files)
         stored_joint = bool(jd) if ratio == 128 else bool(js) if ratio == 4 else False
-        if tile != 128 or dense or group != 1 or stored_joint != joint_here:
+        paired = group == 2 and ratio in (1, 128) and not jd and z["q"].shape[1] <= 8
+        if tile != 128 or dense or not (group == 1 and stored_joint == joint_here or paired):
             continue
-        say(f"[reference vectors] {name} plan {i}: splits={splits}")
-        got, got_lse = launch(splits)
+        say(f"[reference vectors] {name} plan {i}: splits={splits}, query group {group}")
+        got, got_lse = launch(splits, query_group=2 if paired else None)
         assert (got == want).mean() >= 0.999, (name, i)
         np.testing.assert_allclose(got_lse, z[f"lse_{i}"][:live], rtol=0, atol=1e-5)
 
