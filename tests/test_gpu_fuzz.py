@@ -1,9 +1,12 @@
 """Seeded random launches against the CPU checker: mixed ratios, head counts,
 explicit original slots, C4 index modes, short contexts (joint rows),
 prefill-like chunks of 260-400 tokens (c8_rows: work-groups taking rows in
-turn), graph-capacity padding rows, KV partitions (1-8) and both merge placements,
-all bit-exact (BF16 outputs) with the checker on the launch's own plan and LSE
-within 2e-6."""
+turn), graph-capacity padding rows (a few, or enough that the device
+re-plans the live rows, c8_rows capacities included), compressed block
+tables as wide as a serving table, the paired plan (query_group 2 on C128
+and window-only launches), KV partitions (1-8) and both merge placements,
+all bit-exact (BF16 outputs) with the checker on the launch's own plan and
+LSE within 2e-6."""
 import os
 import sys
 
@@ -11,7 +14,7 @@ import numpy as np
 import pytest
 
 from tests import workloads
-from tests.device_cases import run_hip, run_oracle
+from tests.device_cases import joint_flags, run_hip, run_oracle
 
 pytestmark = pytest.mark.gpu
 
@@ -51,7 +54,21 @@ def random_case(seed):
     ori_topk = 256 if need <= 256 else 384
     case = workloads.make_case(seed, ratio, queries, lengths, topk=topk, heads=heads, index_mode=mode,
                                ori_slots=slot_mode, ori_topk=ori_topk)
+    # Graph capacity: a few padding rows, or (one launch in eight) enough that
+    # the device re-plans the live rows of a one-partition or c8_rows launch.
     pad = int(rng.integers(1, 4)) if rng.random() < 0.3 else 0
+    if not prefill and rng.random() < 0.125:
+        pad = int(rng.integers(20, 300))
+    # One C4 launch in six behind a serving-width compressed block table.
+    wide = ratio == 4 and rng.random() < 1 / 6
+    if wide:
+        narrow = case["cmp"].table
+        extra = int(rng.integers(1, 1055)) - narrow.shape[1]
+        if extra > 0:
+            case["cmp"].table = np.ascontiguousarray(
+                np.concatenate([narrow, np.tile(narrow[:, :1], (1, extra))], axis=1))
+    # One C128 / window-only launch in four asks for the paired plan.
+    group = 2 if ratio in (1, 128) and heads <= 8 and not slot_mode and rng.random() < 0.25 else None
     if pad:
         # Graph capacity: a synthetic request of `pad` NaN query rows with
         # seq_len 0 after the live ones (zero-filled by the kernel).
@@ -68,7 +85,8 @@ def random_case(seed):
                 case[key] = np.concatenate([case[key], filler])
     return case, (None if splits is None else int(splits)), merge, dict(
         ratio=ratio, queries=queries, lengths=lengths, heads=heads, mode=mode, slots=slot_mode, topk=topk,
-        pad=pad, joint=bool(ratio != 1 and max(lengths) // ratio <= 128 and heads <= 8 and not slot_mode))
+        pad=pad, wide=case["cmp"].table.shape[1] if wide else 0, group=group,
+        joint=bool(ratio != 1 and max(lengths) // ratio <= 128 and heads <= 8 and not slot_mode))
 
 
 @pytest.mark.parametrize("seed", range(CASES))
@@ -79,15 +97,17 @@ def test_random_launch_matches_checker(seed):
     lib = library()
     try:
         assert lib.sharedkv_c8_set_merge_mode(merge) == 0
-        out, lse, op = run_hip(case, splits=splits)
+        out, lse, op = run_hip(case, splits=splits, query_group=desc["group"])
     finally:
         lib.sharedkv_c8_set_merge_mode(0)
+    assert op.query_group == (desc["group"] or 1)
     plan = op.device_splits(merge_mode=merge)     # the kernel's re-plan under padding
+    joint = joint_flags(case, op.splits, merge)   # judged on the launch as the kernel saw it
     live = int(case["cu_q"][-1]) - desc["pad"]
     if desc["pad"]:
         assert not out[live:].any() and not lse[live:].any(), "padding rows are not zero"
         case = dict(case, q=case["q"][:live], cu_q=case["cu_q"][:-1], seq_lens=case["seq_lens"][:-1])
-    ref, ref_lse, _ = run_oracle(case, plan)
+    ref, ref_lse, _ = run_oracle(case, plan, joint=joint, query_group=op.query_group)
     diff = out[:live] != ref[:live]
     assert not diff.any(), f"seed {seed}: {int(diff.sum())} BF16 mismatches of {diff.size}"
     np.testing.assert_allclose(lse[:live], ref_lse[:live], rtol=0, atol=2e-6)
