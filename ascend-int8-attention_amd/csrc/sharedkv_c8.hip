@@ -34,10 +34,10 @@
 //   partials   with S > 1 partitions, FP32 [num, max, den] go to `partial`;
 //              the last partition of a row to finish (a ticket per row in
 //              `workspace`) folds them, or c8_merge does in a second launch
-// One-partition C4 launches of more rows than CUs (prefill, large decode
-// batches; any head count) run c8_rows instead: two four-wave work-groups per
-// CU with one tile buffer each, each taking rows in turn, so that one row's
-// tile chain fills the other's waits.
+// One-partition C4 and window-only launches of more rows than CUs (prefill,
+// large decode batches; any head count, no explicit slots) run c8_rows instead:
+// two four-wave work-groups per CU with one tile buffer each, each taking
+// rows in turn, so that one row's tile chain fills the other's waits.
 // Integer partials are exact, so any assignment of keys to lanes gives the
 // reference's integers; the FP32 sequence below is kept in the reference's
 // order with contraction disabled.
@@ -1434,20 +1434,28 @@ c8_merge(const SharedKVArgs p, uint32_t splits)
                 H - hbase < HEADS ? H - hbase : HEADS);
 }
 
-// ---- c8_rows: one-partition C4 launches of many query rows ----
+// ---- c8_rows: one-partition launches of many query rows ----
 // The same numerics as c8_attention with one partition (128-key tiles,
 // reference.py:210-323), laid out so that two work-groups share a CU: four
 // waves and one tile buffer each (80 KiB of LDS), each work-group taking rows
-// r, r + grid, ... in turn.  When graph padding leaves fewer live rows than
-// the launch's capacity and the launch may merge (`fused`: partition states
-// and tickets supplied), the live rows are re-planned as c8_attention
-// re-plans them (the same rule, so the same partitions and numerics): each
-// work item is a (row, partition) pair, every XCD takes a contiguous eighth
-// of the live rows, and the last partition of a row folds the states.  A row's tiles are a chain (QK -> tile maximum ->
-// exponentials and P codes -> PV) through work-group barriers; with one row
-// per CU nothing fills those waits, with two rows per CU the other work-group
-// computes while this one waits for its barrier or its next tile.  Each wave
-// takes 32 keys in QK (two 16-key blocks) and 128 output columns in PV.
+// r, r + grid, ... in turn.
+// When graph padding leaves fewer live rows than the launch's capacity and
+// the launch may merge (`fused`: partition states and tickets supplied), the
+// live rows are re-planned as c8_attention re-plans them (the same rule, so
+// the same partitions and numerics): each work item is a (row, partition)
+// pair, every XCD takes a contiguous eighth of the live rows, and the last
+// partition of a row folds the states.  A row's tiles are a chain (QK -> tile
+// maximum -> exponentials and P codes -> PV) through work-group barriers;
+// with one row per CU nothing fills those waits, with two rows per CU the
+// other work-group computes while this one waits for its barrier or its next
+// tile.  Each wave takes 32 keys in QK (two 16-key blocks) and 128 output
+// columns in PV.
+// RATIO 4: the window tile and up to eight compressed tiles, every row's HBM
+// address resident in LDS.  RATIO 1: the window tile alone.  (C128 launches
+// keep c8_attention: its two-tile ring keeps two tiles of a row in flight,
+// where this kernel's single buffer exposes one copy round trip per tile; on
+// C128 rows of three tiles and on joint rows that costs more than the second
+// work-group per CU gains.)
 // No explicit original slots.  STREAM: non-temporal KV copies (decode-shaped
 // launches).  ANYH: 1..128 heads, a row being one group of eight heads of a
 // token (residual codes off above eight heads, reference.py:221-222), as in
@@ -1472,12 +1480,13 @@ struct alignas(16) RowsShared {
 };
 static_assert(sizeof(RowsShared) <= 80 * 1024, "two work-groups per CU");
 
-template <bool STREAM, bool ANYH>
+template <int RATIO, bool STREAM, bool ANYH>
 __global__ void __launch_bounds__(ROWS_THREADS, 2)
 c8_rows(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, const uint64_t cmp_indices,
         const uint32_t batch_arg, const uint32_t topk_arg, const uint32_t rows_arg, const uint32_t grid,
         const uint32_t heads_arg, const SharedKVArgs p, const uint32_t fused)
 {
+    static_assert(RATIO == 1 || RATIO == 4, "window-only and C4 launches");
     __shared__ RowsShared s;
     const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, n = lane & 15;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // scalar: copy destinations on the SALU
@@ -1488,7 +1497,7 @@ c8_rows(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, con
     const int32_t first_row = (int32_t)((blockIdx.x & 7u) * (G >> 3) + (blockIdx.x >> 3));
     const __attribute__((address_space(1))) int32_t *cu = gptr<int32_t>(cu_q);
     const __attribute__((address_space(1))) int32_t *lens = gptr<int32_t>(seq_lens);
-    const int batch_n = (int)batch_arg, topk = (int)topk_arg;
+    const int batch_n = (int)batch_arg, topk = RATIO == 4 ? (int)topk_arg : 0;
 
     // ---- live shape (attention_impl.h:121-137), once per work-group ----
     if (tid == 0) s.misc[0] = 0;
@@ -1502,8 +1511,10 @@ c8_rows(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, con
     const int H = ANYH ? (int)heads_arg : HEADS;                 // heads of a query token
     const int HG = ANYH ? (H + HEADS - 1) / HEADS : 1;           // groups of eight
     const bool resid = !ANYH || H <= HEADS;
-    *reinterpret_cast<f32x4 *>(&s.scale[tid >> 7][(tid & 127) * 4]) =
-        *gptr<f32x4>(((tid >> 7) ? p.cmpScale : p.oriScale) + (uint64_t)((tid & 127) * 4) * 4);
+    // Channel scales: the window's, and the compressed cache's (none without one).
+    if (RATIO != 1 || tid < ROWS_THREADS / 2)
+        *reinterpret_cast<f32x4 *>(&s.scale[tid >> 7][(tid & 127) * 4]) =
+            *gptr<f32x4>(((tid >> 7) ? p.cmpScale : p.oriScale) + (uint64_t)((tid & 127) * 4) * 4);
     const int c0 = 128 * wave;   // this wave's PV output columns: c0 + 16 j + n
 
     // ---- device plan of a padded launch (c8_attention's rule) ----
@@ -1517,8 +1528,11 @@ c8_rows(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, con
             if (lens[b] > 0 && cu[b + 1] >= 0) atomicMax(&s.misc[6], lens[b]);
         __syncthreads();
         const int longest = uni(s.misc[6]);
-        const int cnt = longest / 4 < topk ? longest / 4 : topk;
-        const int32_t tiles = 1 + (cnt + N - 1) / N;
+        int32_t tiles = 1;
+        if (RATIO == 4) {
+            const int cnt = longest / 4 < topk ? longest / 4 : topk;
+            tiles += (cnt + N - 1) / N;
+        }
         int32_t plan = live_rows * PLAN_FEW <= PLAN_CUS ? PLAN_FEW : PLAN_MANY;
         const int32_t fit = PLAN_CUS / live_rows > 1 ? PLAN_CUS / live_rows : 1;
         const int32_t room = rows_cap / live_rows;
@@ -1556,9 +1570,11 @@ c8_rows(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, con
                          ? *gptr<v4i>(q_base + (((uint64_t)t * H + hbase + wave + 4 * hh) * D + lane * 8) * 2)
                          : v4i{0, 0, 0, 0};   // padding heads of the last group: zero Q, never written
         int ix[ROWS_IX];
-        const __attribute__((address_space(1))) int32_t *row_ix = gptr<int32_t>(cmp_indices) + (int64_t)t * topk;
+        if (RATIO == 4) {
+            const __attribute__((address_space(1))) int32_t *row_ix = gptr<int32_t>(cmp_indices) + (int64_t)t * topk;
 #pragma unroll
-        for (int e = 0; e < ROWS_IX; ++e) ix[e] = tid * ROWS_IX + e < topk ? row_ix[tid * ROWS_IX + e] : -1;
+            for (int e = 0; e < ROWS_IX; ++e) ix[e] = tid * ROWS_IX + e < topk ? row_ix[tid * ROWS_IX + e] : -1;
+        }
         __syncthreads();   // every wave is done with the previous item's shared data
         if (tid == 0) s.misc[1] = -1;
         __syncthreads();
@@ -1588,7 +1604,7 @@ c8_rows(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, con
         // ---- selection (attention_impl.h:58-73, reference.py:228-253) ----
         const int first_ori = position + 1 > WINDOW ? position + 1 - WINDOW : 0;
         const int ori_count = position + 1 - first_ori;
-        const int count = (position + 1) / 4;
+        const int count = RATIO == 4 ? (position + 1) / 4 : 0;
         const __attribute__((address_space(1))) int32_t *otab = gptr<int32_t>(p.oriTable) + (int64_t)batch * p.oriTableWidth;
         const __attribute__((address_space(1))) int32_t *ctab = gptr<int32_t>(p.cmpTable) + (int64_t)batch * p.cmpTableWidth;
         int wpage = -1, widx = -1, cpage[ROWS_IX];
@@ -1599,39 +1615,42 @@ c8_rows(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, con
                 wpage = otab[idx / BLOCK_ROWS];
             }
         }
-        bool ok[ROWS_IX];
-#pragma unroll
-        for (int e = 0; e < ROWS_IX; ++e) {
-            ok[e] = ix[e] >= 0 && ix[e] < count;
-            cpage[e] = ok[e] && ix[e] / BLOCK_ROWS < (int)p.cmpTableWidth ? ctab[ix[e] / BLOCK_ROWS] : -1;
-        }
-        // List place of each entry: compacted (count < topk <= 1024,
-        // reference.py:250) or in place with holes masked.
         int ipos[ROWS_IX];
-        int list_len = topk;
-        if (count < topk) {
-            uint64_t v[ROWS_IX];
-            int below = 0, mine = 0;
+        int list_len = 0;
+        bool ok[ROWS_IX];
+        if (RATIO == 4) {
 #pragma unroll
             for (int e = 0; e < ROWS_IX; ++e) {
-                v[e] = __ballot(ok[e]);
-                below += (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(v[e] >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)v[e], 0u));
-                mine += __popcll(v[e]);
+                ok[e] = ix[e] >= 0 && ix[e] < count;
+                cpage[e] = ok[e] && ix[e] / BLOCK_ROWS < (int)p.cmpTableWidth ? ctab[ix[e] / BLOCK_ROWS] : -1;
             }
-            if (lane == 0) s.scan[wave] = mine;
-            lds_barrier();
-            int at = below, total = 0;
+            // List place of each entry: compacted (count < topk <= 1024,
+            // reference.py:250) or in place with holes masked.
+            list_len = topk;
+            if (count < topk) {
+                uint64_t v[ROWS_IX];
+                int below = 0, mine = 0;
 #pragma unroll
-            for (int w = 0; w < ROWS_WAVES; ++w) {
-                at += w < wave ? s.scan[w] : 0;
-                total += s.scan[w];
+                for (int e = 0; e < ROWS_IX; ++e) {
+                    v[e] = __ballot(ok[e]);
+                    below += (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(v[e] >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)v[e], 0u));
+                    mine += __popcll(v[e]);
+                }
+                if (lane == 0) s.scan[wave] = mine;
+                lds_barrier();
+                int at = below, total = 0;
+#pragma unroll
+                for (int w = 0; w < ROWS_WAVES; ++w) {
+                    at += w < wave ? s.scan[w] : 0;
+                    total += s.scan[w];
+                }
+#pragma unroll
+                for (int e = 0; e < ROWS_IX; ++e) ipos[e] = ok[e] ? at++ : -1;
+                list_len = uni(total);
+            } else {
+#pragma unroll
+                for (int e = 0; e < ROWS_IX; ++e) ipos[e] = ok[e] ? tid * ROWS_IX + e : -1;
             }
-#pragma unroll
-            for (int e = 0; e < ROWS_IX; ++e) ipos[e] = ok[e] ? at++ : -1;
-            list_len = uni(total);
-        } else {
-#pragma unroll
-            for (int e = 0; e < ROWS_IX; ++e) ipos[e] = ok[e] ? tid * ROWS_IX + e : -1;
         }
         const int tiles = 1 + (list_len + N - 1) / N;   // window tile, then compressed tiles
         // Tile k belongs to partition k % S (the window tile to partition 0);
@@ -1640,15 +1659,17 @@ c8_rows(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, con
         if (part >= tiles) return;
         const int folded = S < tiles ? S : tiles;
 
-        // ---- row addresses of every tile (masked rows: the Q base, never used) ----
+        // ---- row addresses (masked rows: the Q base, never used) ----
         for (int i = tid; i < tiles * N; i += ROWS_THREADS) s.addr[i] = p.q;
         lds_barrier();
         if (widx >= 0 && wpage >= 0 && (uint32_t)wpage < p.oriPages)
             s.addr[tid] = p.ori + (uint64_t)wpage * p.oriStride + (uint64_t)((widx % BLOCK_ROWS) * D);
+        if (RATIO == 4) {
 #pragma unroll
-        for (int e = 0; e < ROWS_IX; ++e)
-            if (ipos[e] >= 0 && cpage[e] >= 0)
-                s.addr[N + ipos[e]] = p.cmp + (uint64_t)cpage[e] * p.cmpStride + (uint64_t)((ix[e] % BLOCK_ROWS) * D);
+            for (int e = 0; e < ROWS_IX; ++e)
+                if (ipos[e] >= 0 && cpage[e] >= 0)
+                    s.addr[N + ipos[e]] = p.cmp + (uint64_t)cpage[e] * p.cmpStride + (uint64_t)((ix[e] % BLOCK_ROWS) * D);
+        }
 
         // ---- Q folding and residual split per kind (reference.py:274-279) ----
         // Staged in the tile buffer, then picked up in the MFMA A layout.
@@ -2513,15 +2534,22 @@ void launch_variant(hipStream_t stream, const SharedKVArgs *a, const SharedKVDeb
     // they cost tiled C4 launches about 1 %.
     const bool joint4 = !DEBUG && !slots && a->heads <= HEADS &&
                         (small_entry || (uint64_t)a->cmpTableWidth * BLOCK_ROWS <= (uint64_t)N);
-    // One-partition C4 launches of more rows than CUs (prefill, large decode
-    // batches) run two four-wave work-groups per CU taking rows in turn
-    // (c8_rows).  C128 and window-only launches keep one work-group per row.
-    const bool persist = !DEBUG && !slots && a->ratio == 4 && !joint4 && splits == 1 && rows > (uint32_t)PLAN_CUS;
+    // One-partition C4 and window-only launches of more rows than CUs
+    // (prefill, large decode batches) without explicit slots run two
+    // four-wave work-groups per CU taking rows in turn (c8_rows).  C128
+    // launches keep one work-group per row: their rows are three or fewer
+    // tiles in a prefill chunk, or joint rows, and c8_attention's two-tile
+    // ring measured faster on them (C128 prefill chunk 80 against 85 us,
+    // joint rows 63 against 110, decode of 512 rows 51 against 72).
+    const bool persist = !DEBUG && !slots && splits == 1 && rows > (uint32_t)PLAN_CUS &&
+                         (a->ratio == 1 || (a->ratio == 4 && !joint4));
     if (persist) {
         // Two four-wave work-groups per CU (c8_rows), at most one per row, so
         // that every XCD gets its share of the rows.
         const uint32_t g2 = rows < 2u * (uint32_t)PLAN_CUS ? (rows + 7u) & ~7u : 2u * (uint32_t)PLAN_CUS;
-        const auto rows_kernel = streamed ? &c8_rows<true, ANYH> : &c8_rows<false, ANYH>;
+        const auto rows_kernel = a->ratio == 1 ? &c8_rows<1, false, ANYH>
+                                 : streamed    ? &c8_rows<4, true, ANYH>
+                                               : &c8_rows<4, false, ANYH>;
         hipLaunchKernelGGL(rows_kernel, dim3(g2), dim3(ROWS_THREADS), 0, stream, a->cuQ, a->seqLens, a->q, a->indices,
                            a->batch, a->topk, rows, g2, a->heads, *a, fused);
         return;

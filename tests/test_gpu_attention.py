@@ -336,6 +336,109 @@ def test_persistent_rows(heads):
     compare(live_case, out[:live], lse[:live], 1, rows=rows, tag=f"persistent heads {heads}")
 
 
+@pytest.mark.parametrize("ratio,lengths,heads", [
+    (128, [20000, 40, 1], 8),    # tiled rows of 151-156 compressed rows, short rows, a keyless row
+    (128, [16990, 300, 1], 8),   # rows of 128 compressed rows (joint) and of 129-132 (tiled) in one chunk
+    (128, [3000, 140, 1], 8),    # joint rows (1-23 compressed rows) and window-only rows (position < 127)
+    (128, [20000, 40, 1], 12),   # two rows per token, no residual codes: tiled
+    (1, [3000, 40, 1], 8),       # window-only cache
+])
+def test_persistent_dense_rows(ratio, lengths, heads):
+    """One-partition C128 and window-only launches of more rows than CUs:
+    window-only launches run c8_rows (two four-wave work-groups per CU taking
+    rows in turn), C128 launches one work-group per row, rows of 1-128
+    compressed rows being joint rows.  Bit-exact with the checker's plan for
+    the launch (joint_dense per row at one partition), with graph-padding
+    rows and a keyless row as in the C4 case."""
+    from npu_sparse_attn_sharedkv_int8 import c8_attention
+    case = workloads.make_case(82, ratio, [600, 5, 2], lengths, heads=heads)
+    pad = 12
+    live = int(case["cu_q"][-1])
+    case["q"] = np.concatenate([case["q"], np.full((pad, heads, 512), 0x7FC0, np.uint16)])
+    case["cu_q"] = np.concatenate([case["cu_q"], [live + pad]]).astype(np.int32)
+    case["seq_lens"] = np.concatenate([case["seq_lens"], [0]]).astype(np.int32)
+    case["ori"].table = np.concatenate([case["ori"].table, case["ori"].table[:1]])
+    if case["cmp"] is not None:
+        case["cmp"].table = np.concatenate([case["cmp"].table, case["cmp"].table[:1]])
+    rows = (live + pad) * ((heads + 7) // 8)
+    say(f"[persistent dense] ratio {ratio}, lengths {lengths}, heads {heads}: {rows} rows")
+    out, lse, op = run_hip(case, splits=1)
+    assert op.splits == 1 and op.device_splits() == 1 and rows > c8_attention.CORES
+    assert not out[live:].any() and not lse[live:].any(), "padding rows are not zero"
+    keyless = live - 2                                   # position -1
+    assert not out[keyless].any() and not lse[keyless].any()
+    live_case = dict(case, q=case["q"][:live], cu_q=case["cu_q"][:-1], seq_lens=case["seq_lens"][:-1])
+    compare(live_case, out[:live], lse[:live], 1, rows=[r for r in range(live) if r != keyless],
+            tag=f"persistent dense ratio {ratio} heads {heads}")
+    if ratio == 128 and heads == 8 and lengths[0] == 16990:
+        # Both routes of the straddling chunk are taken: the tiled plan of
+        # the same launch differs on the joint rows only.
+        import oracle.oracle as ora
+        chunk = query_subcase(live_case, list(range(600)))
+        tiled, _, _ = ora.tiled_attention(workloads.oracle_case(chunk), tile=128, splits=1, return_lse=True)
+        first = [t for t in range(600) if (16990 - 600 + t + 1) // 128 <= 128]
+        rest = [t for t in range(600) if t not in first]
+        assert first and rest and (out[first] != tiled[first]).any()
+        assert not (out[rest] != tiled[rest]).any()
+
+
+def test_rows_graph_c128_replayed_with_few_live_sequences():
+    """A C128 decode launch of 256 requests x 2 tokens (512 one-partition
+    rows) captured once and replayed with 256, 16, 64 and 3 live requests of
+    16.6-30 K tokens (re-planned into partitions merged in the launch, spread
+    over every XCD), then with 16 live requests of at most 16 511 tokens (a
+    joint-plan launch: one partition per row, every row joint).  Outputs, LSE and partition states
+    are NaN-poisoned before each state; padding rows come back zero, live
+    rows bit-exact with the checker on the device plan."""
+    import torch
+    from npu_sparse_attn_sharedkv_int8 import PreparedAttention
+    cap = 256
+    rng = np.random.default_rng(34)
+    long_lengths = [int(n) for n in rng.integers(16600, 30000, cap)]
+    short_lengths = [int(n) for n in rng.integers(200, 16511, cap)]
+    full = workloads.make_case(94, 128, [2] * cap, long_lengths)
+    dev, oscale, cscale, keep = to_device(full)
+    op = PreparedAttention(dev, oscale, cscale, return_lse=True)
+    assert op.splits == 1 and op.partial is not None
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        op.run()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=stream):
+            op.run()
+    torch.cuda.current_stream().wait_stream(stream)
+    for batch, lengths in ((cap, long_lengths), (16, long_lengths), (64, long_lengths), (3, long_lengths),
+                           (16, short_lengths)):
+        cu = np.array([2 * min(b, batch) for b in range(cap + 1)], np.int32)
+        lens = np.array(lengths[:batch] + [0] * (cap - batch), np.int32)
+        q = full["q"].copy()
+        q[2 * batch:] = 0x7FC0
+        dev.q.copy_(torch_bf16(q, "cuda"))
+        dev.cu_q.copy_(torch.from_numpy(cu))
+        dev.seq_lens.copy_(torch.from_numpy(lens))
+        op.out.fill_(float("nan"))
+        op.lse.fill_(float("nan"))
+        op.partial.fill_(float("nan"))
+        torch.cuda.synchronize()
+        plan = effective_splits(dict(full, q=q, cu_q=cu, seq_lens=lens), op.splits)
+        assert (plan > 1) == (batch < cap and lengths is long_lengths), (batch, plan)
+        say(f"[rows graph c128] {batch} live requests, {plan} partition(s)")
+        graph.replay()
+        torch.cuda.synchronize()
+        out, lse = bits_of(op.out), op.lse.cpu().numpy()
+        live = 2 * batch
+        assert not out[live:].any() and not lse[live:].any(), "padding rows are not zero"
+        assert not op.workspace.any(), "merge tickets must return to zero"
+        sub = dict(full, q=q[:live], cu_q=cu[:batch + 1], seq_lens=lens[:batch])
+        ref, ref_lse, _ = run_oracle(sub, plan)
+        diff = out[:live] != ref
+        assert not diff.any(), f"{batch} live: {int(diff.sum())} BF16 mismatches"
+        np.testing.assert_allclose(lse[:live], ref_lse, rtol=0, atol=2e-6)
+    del graph
+
+
 @pytest.mark.parametrize("name", GOLDEN_NAMES)
 def test_against_reference_vectors(name):
     """HIP output vs reference.py's own tiled_quantized_reference output on
