@@ -1563,17 +1563,21 @@ c8_rows(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, con
         // Q (heads wave and wave + 4, channels 8 lane ..) and the row's index
         // entries 4 tid .. 4 tid + 3, requested with the request search (the
         // other work-group of the CU computes meanwhile).
+        // Q, the indices and the output are read or written once: non-temporal,
+        // so they do not displace the KV rows the launch's rows share in L2.
         v4i qv[2];
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh)
             qv[hh] = !ANYH || wave + 4 * hh < hlive
-                         ? *gptr<v4i>(q_base + (((uint64_t)t * H + hbase + wave + 4 * hh) * D + lane * 8) * 2)
+                         ? __builtin_nontemporal_load(
+                               gptr<v4i>(q_base + (((uint64_t)t * H + hbase + wave + 4 * hh) * D + lane * 8) * 2))
                          : v4i{0, 0, 0, 0};   // padding heads of the last group: zero Q, never written
         int ix[ROWS_IX];
         if (RATIO == 4) {
             const __attribute__((address_space(1))) int32_t *row_ix = gptr<int32_t>(cmp_indices) + (int64_t)t * topk;
 #pragma unroll
-            for (int e = 0; e < ROWS_IX; ++e) ix[e] = tid * ROWS_IX + e < topk ? row_ix[tid * ROWS_IX + e] : -1;
+            for (int e = 0; e < ROWS_IX; ++e)
+                ix[e] = tid * ROWS_IX + e < topk ? __builtin_nontemporal_load(row_ix + tid * ROWS_IX + e) : -1;
         }
         __syncthreads();   // every wave is done with the previous item's shared data
         if (tid == 0) s.misc[1] = -1;
@@ -1920,7 +1924,8 @@ c8_rows(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, con
                 const int h = 2 * g + hh;
                 if (ANYH && h >= hlive) continue;
 #pragma unroll
-                for (int j = 0; j < 8; ++j) out_row[h * D + c0 + 16 * j + n] = (uint16_t)pack_bf16(num[hh][j] / den[hh], 0.0f);
+                for (int j = 0; j < 8; ++j)
+                    __builtin_nontemporal_store((uint16_t)pack_bf16(num[hh][j] / den[hh], 0.0f), out_row + h * D + c0 + 16 * j + n);
                 if (lse_row && wave == 0 && n == 0) lse_row[h] = mx[hh] + logf(den[hh]);
             }
             return;
