@@ -342,6 +342,7 @@ def test_persistent_rows(heads):
     (128, [3000, 140, 1], 8),    # joint rows (1-23 compressed rows) and window-only rows (position < 127)
     (128, [20000, 40, 1], 12),   # two rows per token, no residual codes: tiled
     (1, [3000, 40, 1], 8),       # window-only cache
+    (1, [3000, 40, 1], 12),      # window-only, two rows per token (c8_rows head groups)
 ])
 def test_persistent_dense_rows(ratio, lengths, heads):
     """One-partition C128 and window-only launches of more rows than CUs:
