@@ -16,6 +16,7 @@ namespace {
 
 constexpr long VARIANT_SPARSE = 20, VARIANT_DENSE = 21, VARIANT_SPARSE_SMALL = 22;   // c8_launch.cpp:14-17
 constexpr long VARIANT_DENSE_PAIRED = 23;   // the query-grouped plan (launch_sharedkv_c8_dense_paired)
+constexpr long VARIANT_DENSE_PACKED = 24;   // groups of four (launch_sharedkv_c8_dense_packed)
 
 bool read_u64(PyObject *o, uint64_t *out)
 {
@@ -46,7 +47,8 @@ PyObject *attention(PyObject *, PyObject *const *args, Py_ssize_t nargs)
         variant == VARIANT_SPARSE ? launch_sharedkv_c8_sparse
         : variant == VARIANT_DENSE ? launch_sharedkv_c8_dense
         : variant == VARIANT_SPARSE_SMALL ? launch_sharedkv_c8_sparse_small
-        : variant == VARIANT_DENSE_PAIRED ? launch_sharedkv_c8_dense_paired : nullptr;
+        : variant == VARIANT_DENSE_PAIRED ? launch_sharedkv_c8_dense_paired
+        : variant == VARIANT_DENSE_PACKED ? launch_sharedkv_c8_dense_packed : nullptr;
     if (!launch) {
         PyErr_SetString(PyExc_ValueError, "Invalid C8 variant");   // c8_launch.cpp:17
         return nullptr;

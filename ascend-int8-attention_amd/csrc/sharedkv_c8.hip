@@ -281,6 +281,7 @@ struct alignas(16) Shared {
     int8_t tile[2][N * D];          // two K/V tiles (the DMA ring); Q code staging before the first tile
 };
 static_assert(2 * 16 * QSTAGE <= N * D, "Q staging fits in one tile buffer");
+static_assert(offsetof(Shared, tile) % 16 == 0, "16-byte LDS DMA rows and tile reads");
 
 struct Row {
     int32_t batch, position, first_ori, ori_count, count, list_len, t0, total;
@@ -1479,6 +1480,7 @@ struct alignas(16) RowsShared {
     int8_t tile[N * D];                  // the tile buffer; Q code staging before the first tile
 };
 static_assert(sizeof(RowsShared) <= 80 * 1024, "two work-groups per CU");
+static_assert(offsetof(RowsShared, tile) % 16 == 0, "16-byte LDS DMA rows and tile reads");
 
 template <int RATIO, bool STREAM, bool ANYH>
 __global__ void __launch_bounds__(ROWS_THREADS, 2)
@@ -1970,43 +1972,60 @@ c8_rows(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, con
         run_item(lo + j / S, j % S);
 }
 
-// ---- c8_pairs: query-grouped plans (two query tokens per group) ----
-// reference.py:224-323 with query_group 2 (the reference device's C128
-// "paired" plan, c128.cpp:17-23): the tokens 2 j and 2 j + 1 of a request
-// form a group that shares one window list (positions max(0, p0 + 1 - 128)
-// .. p1, up to 129 rows) and, for C128, one compressed list (rows below
-// (p1 + 1) / 128); each token masks what it may not see (its own window,
-// its own compressed count) and keeps its own online softmax.  128-key
-// tiles numbered across both kinds, tile k on partition k % S, no joint
-// rows.  One work-group of 8 waves per (group, partition): the group's
-// tiles are fetched once into a two-tile LDS ring, waves 0-3 compute token
-// 0 and waves 4-7 token 1, each wave taking 32 keys in QK and 128 output
-// columns in PV (the per-row layout of c8_rows).  Work items are
-// (token, partition); items of the second token of a group exit (the
-// group's first token takes both), items of padding or keyless tokens
+// ---- c8_pairs: query-grouped plans (groups of two or four query tokens) ----
+// reference.py:224-323 with query_group G = 2 or 4 (the reference device's
+// C128 "paired" and "packed" plans, c128.cpp:17-27): the tokens G j ..
+// G j + G - 1 of a request form a group that shares one window list
+// (positions max(0, p_first + 1 - 128) .. p_last, up to 127 + G rows) and,
+// for C128, one compressed list (rows below (p_last + 1) / 128); each token
+// masks what it may not see (its own window, its own compressed count) and
+// keeps its own online softmax.  128-key tiles numbered across both kinds,
+// tile k on partition k % S, no joint rows.  One work-group of 8 waves per
+// (sub-pair, partition), a sub-pair being tokens 2 i and 2 i + 1 of the
+// request within one group (a group of four has two): the group's tiles are
+// fetched into a two-tile LDS ring, waves 0-3 compute the sub-pair's first
+// token and waves 4-7 its second, each wave taking 32 keys in QK and 128
+// output columns in PV (the per-row layout of c8_rows).  Work items are
+// (token, partition); items of the second token of a sub-pair exit (the
+// sub-pair's first token takes both), items of padding or keyless tokens
 // zero-fill them.  At most eight heads (residual codes on).
+// C4 groups (reference.py:242-253 with query_group > 1) list every
+// compressed row below (p_last + 1) / 4 once; each token weighs row r by its
+// multiplicity m_r among its own valid top-k entries (log(m_r) added to the
+// logit, rows with m_r = 0 masked).  The multiplicities of the resident
+// tiles are counted in LDS per code chunk (both tokens' counts packed in one
+// word), and only rows that one of the two tokens lists are fetched.
+template <int RATIO>
 struct alignas(16) PairShared {
+    static constexpr int CT = RATIO == 4 ? 8 : CODE_TILES;   // tiles whose row codes are resident at once
     int32_t redmax[2][HEADS][4];   // per token: per-wave tile maxima (fkey)
     float redsum[2][HEADS][4];     // per token: per-wave weight sums of its two 16-key blocks
     float asc[2][2][HEADS];        // [token][kind][head]: alpha * softmax_scale
     int32_t misc[8];
     float scale[2][D];             // channel scales of the window / compressed cache
     int8_t p[2][16 * PROW];        // P codes per token [MFMA row][key]
-    int32_t code[CODE_TILES * N];  // row codes of the resident tiles: page * 32 + row, -1 masked
-    uint64_t addr[CODE_TILES * N]; // HBM address of each resident row (masked rows: the Q base)
-    int8_t tile[2][N * D];         // the DMA ring; Q code staging before tile 1
+    int32_t code[CT * N];          // row codes of the resident tiles: page * 32 + row, -1 masked
+    uint64_t addr[CT * N];         // HBM address of each resident row (masked rows: the Q base)
+    uint32_t mult[RATIO == 4 ? CT * N : 1];   // C4: multiplicity of each resident row, token 0 | token 1 << 16
+    float logt[RATIO == 4 ? MAX_LIST + 4 : 1];   // C4: log(m) for multiplicities m = 0 .. MAX_LIST
+    alignas(16) int8_t tile[2][N * D];   // the DMA ring; Q code staging before tile 1
 };
 static_assert(2 * 2 * 16 * QSTAGE <= N * D, "both tokens' Q codes fit one tile buffer");
-static_assert(sizeof(PairShared) <= 160 * 1024, "one work-group per CU");
+static_assert(sizeof(PairShared<128>) <= 160 * 1024 && sizeof(PairShared<4>) <= 160 * 1024, "one work-group per CU");
+static_assert(2 * MAX_LIST == 4 * THREADS, "four index entries per thread: two tokens' top-k lists");
+static_assert(PairShared<4>::CT * N % THREADS == 0 && PairShared<128>::CT * N % THREADS == 0, "whole code rounds");
+static_assert(offsetof(PairShared<4>, tile) % 16 == 0 && offsetof(PairShared<128>, tile) % 16 == 0,
+              "16-byte LDS DMA rows and tile reads");
 
 template <int RATIO, bool STREAM>
 __global__ void __launch_bounds__(THREADS, 1)
 c8_pairs(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, const uint32_t batch_arg,
          const uint32_t heads_arg, const uint32_t splits, const uint32_t rows_arg, const uint32_t grid,
-         const SharedKVArgs p, const uint32_t fused)
+         const SharedKVArgs p, const uint32_t fused, const uint32_t group)
 {
-    static_assert(RATIO == 1 || RATIO == 128, "grouped plans: window-only and C128 launches");
-    __shared__ PairShared s;
+    static_assert(RATIO == 1 || RATIO == 4 || RATIO == 128, "grouped plans: window-only, C4 and C128 launches");
+    __shared__ PairShared<RATIO> s;
+    constexpr int CT = PairShared<RATIO>::CT;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, n = lane & 15;
     const int tok = wave >> 2, tw = wave & 3;   // token of the group, wave within the token
     const uint32_t G = grid;
@@ -2076,10 +2095,17 @@ c8_pairs(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, co
         return;
     }
     const int c0r = uni(s.misc[5]), c1r = uni(s.misc[4]), len = uni(s.misc[3]);
-    if ((t - c0r) & 1) return;                        // the group's first token takes it
-    const int gs = t + 1 < c1r && t + 1 < live_tokens ? 2 : 1;   // tokens in the group
-    const int p0 = len - c1r + t, plast = p0 + gs - 1;
-    if (p0 < 0) {                                     // negative positions (reference.py:104-105): zero
+    // Sub-pairs start at even offsets in the request (groups hold an even
+    // number of tokens, so no sub-pair straddles two groups).
+    if ((t - c0r) & 1) return;                        // the sub-pair's first token takes it
+    const int gfirst = c0r + (t - c0r) / (int)group * (int)group;
+    int gend = gfirst + (int)group;                   // one past the group's last token
+    gend = gend < c1r ? gend : c1r;
+    gend = gend < live_tokens ? gend : live_tokens;
+    const int gs = t + 1 < gend ? 2 : 1;              // tokens in the sub-pair
+    const int p0 = len - c1r + t;                     // position of the sub-pair's first token
+    const int pfirst = len - c1r + gfirst, plast = len - c1r + gend - 1;
+    if (pfirst < 0) {                                 // negative positions (reference.py:104-105): zero
         if (part == 0) {
             for (int k = 0; k < gs; ++k) {
                 zero_token(t + k);
@@ -2089,10 +2115,10 @@ c8_pairs(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, co
         return;
     }
     // ---- the group's lists (reference.py:229-253) ----
-    const int lo0 = p0 + 1 - WINDOW > 0 ? p0 + 1 - WINDOW : 0;
-    const int ori_count = plast + 1 - lo0;            // window rows max(0, p0 + 1 - 128) .. plast
+    const int lo0 = pfirst + 1 - WINDOW > 0 ? pfirst + 1 - WINDOW : 0;
+    const int ori_count = plast + 1 - lo0;            // window rows max(0, pfirst + 1 - 128) .. plast
     const int t0w = (ori_count + N - 1) / N;
-    const int list_len = RATIO == 128 ? (plast + 1) / 128 : 0;
+    const int list_len = RATIO == 1 ? 0 : (plast + 1) / RATIO;   // C4: the group's dense list
     const int total = t0w + (list_len + N - 1) / N;
     const int folded = S < total ? S : total;
     if (part >= folded) return;
@@ -2100,12 +2126,17 @@ c8_pairs(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, co
     // Each token's own window and compressed count.
     const int ptok = p0 + (tok < gs ? tok : 0);
     const int own_lo = ptok + 1 - WINDOW > 0 ? ptok + 1 - WINDOW : 0;
-    const int own_count = RATIO == 128 ? (ptok + 1) / 128 : 0;
+    const int own_count = RATIO == 1 ? 0 : (ptok + 1) / RATIO;
     const bool tok_live = tok < gs;
+    if (RATIO == 4) {
+        // log(m) of every multiplicity a top-k list can give (reference.py:300-301,
+        // exact: see the oracle's log_count), read back per key.
+        for (int m = tid; m <= MAX_LIST; m += THREADS) s.logt[m] = m > 1 ? (float)log((double)m) : 0.0f;
+    }
 
     const __attribute__((address_space(1))) int32_t *otab = gptr<int32_t>(p.oriTable) + (int64_t)batch * p.oriTableWidth;
     const __attribute__((address_space(1))) int32_t *ctab =
-        RATIO == 128 ? gptr<int32_t>(p.cmpTable) + (int64_t)batch * p.cmpTableWidth : otab;
+        RATIO != 1 ? gptr<int32_t>(p.cmpTable) + (int64_t)batch * p.cmpTableWidth : otab;
     const __attribute__((address_space(1))) float *sinks = gptr<float>(p.sinks);
     const float sink0 = 2 * g < H ? sinks[2 * g] : 0.0f;
     const float sink1 = 2 * g + 1 < H ? sinks[2 * g + 1] : 0.0f;
@@ -2144,14 +2175,43 @@ c8_pairs(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, co
     constexpr int DMA_STEP = DMA_PER_TILE / 4;
 
     v4i qa0[8], qa1[8];
-    for (int first = 0; first < my_tiles; first += CODE_TILES) {
-        const int ntiles = my_tiles - first < CODE_TILES ? my_tiles - first : CODE_TILES;
+    for (int first = 0; first < my_tiles; first += CT) {
+        const int ntiles = my_tiles - first < CT ? my_tiles - first : CT;
         // ---- row codes of partition tiles [first, first + ntiles) ----
         for (int i = tid; i < ntiles * N; i += THREADS) {
             s.code[i] = -1;
             s.addr[i] = p.q;
+            if (RATIO == 4) s.mult[i] = 0;
         }
-        constexpr int PER = CODE_TILES * N / THREADS;
+        if (RATIO == 4) {
+            // Multiplicities of the resident compressed rows, from the top-k
+            // entries of both tokens (threads 0-255 the first token's, 256-511
+            // the second's, four entries each) that are valid for their token
+            // (reference.py:243-245: 0 <= index < count).  List place idx is
+            // tile t0w + idx / N, on this partition when that tile is
+            // part + S * l, resident when first <= l < first + ntiles.
+            const int u = tid >> 8;
+            const int ucount = (p0 + u + 1) / 4;
+            const __attribute__((address_space(1))) int32_t *row_ix =
+                gptr<int32_t>(p.indices) + (int64_t)(t + (u < gs ? u : 0)) * p.topk;
+            int cix[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int j = (tid & 255) + 256 * e;
+                cix[e] = u < gs && j < (int)p.topk ? row_ix[j] : -1;
+            }
+            lds_barrier();                    // the zero fill is complete
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                if (cix[e] < 0 || cix[e] >= ucount) continue;
+                const int k = t0w + cix[e] / N;
+                if (k % S != part) continue;
+                const int l = k / S - first;
+                if (l >= 0 && l < ntiles) atomicAdd(&s.mult[l * N + cix[e] % N], u ? 65536u : 1u);
+            }
+            lds_barrier();
+        }
+        constexpr int PER = CT * N / THREADS;
         int tpage[PER], tidx[PER];
 #pragma unroll
         for (int e = 0; e < PER; ++e) {
@@ -2167,9 +2227,10 @@ c8_pairs(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, co
                     tidx[e] = idx;
                     tpage[e] = otab[idx / BLOCK_ROWS];
                 }
-            } else if (RATIO == 128) {
+            } else if (RATIO != 1) {
                 const int idx = (k - t0w) * N + r;
-                if (idx < list_len && idx / BLOCK_ROWS < (int)p.cmpTableWidth) {
+                // C4: rows that neither token lists are not fetched.
+                if (idx < list_len && idx / BLOCK_ROWS < (int)p.cmpTableWidth && (RATIO != 4 || s.mult[i])) {
                     tidx[e] = idx;
                     tpage[e] = ctab[idx / BLOCK_ROWS];
                 }
@@ -2195,7 +2256,8 @@ c8_pairs(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, co
         if (first == 0) {
             // ---- Q folding and residual split per token and kind (reference.py:274-279),
             // staged in tile buffer 1, then picked up in the MFMA A layout ----
-            // Window tiles are tiles 0 .. t0w - 1 (t0w <= 2): this partition
+            // Window tiles are tiles 0 .. t0w - 1 (t0w <= 2, the window list
+            // holding at most 131 rows): this partition
             // holds one when its first tile is one; a compressed one when its
             // last tile is one.
             const bool want[2] = {part < t0w, part + S * (my_tiles - 1) >= t0w};
@@ -2286,13 +2348,19 @@ c8_pairs(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, co
             for (int kb = 0; kb < 2; ++kb) {
                 const int key = 32 * tw + 16 * kb + n;
                 const int idx = kind ? (k - t0w) * N + key : lo0 + k * N + key;
-                const bool mine = kind ? idx < own_count : (idx >= own_lo && idx <= ptok);
+                // C4: this token's multiplicity of the row; log(m) joins
+                // the logit (reference.py:300-301).
+                const int times = RATIO == 4 && kind ? (int)((s.mult[i * N + key] >> (16 * tok)) & 0xffffu) : 0;
+                const bool mine = RATIO == 4 && kind ? times > 0
+                                  : kind ? idx < own_count : (idx >= own_lo && idx <= ptok);
                 const bool valid = tok_live && mine && s.code[i * N + key] >= 0;
+                const float bias = RATIO == 4 && kind ? s.logt[times] : 0.0f;
 #pragma unroll
                 for (int hh = 0; hh < 2; ++hh) {
                     float dots = (float)sacc[kb][2 * hh];
                     dots = dots + (float)sacc[kb][2 * hh + 1] * (float)(1.0 / 127.0);
-                    const float l = dots * s.asc[tok][kind][2 * g + hh];
+                    float l = dots * s.asc[tok][kind][2 * g + hh];
+                    if (RATIO == 4 && kind) l = l + bias;
                     lg[kb][hh] = valid ? l : -1e30f;
                 }
             }
@@ -2383,7 +2451,7 @@ c8_pairs(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, co
             mx[0] = mnew[0];
             mx[1] = mnew[1];
         }
-        if (first + CODE_TILES < my_tiles) __syncthreads();   // s.code and the tile buffers are rebuilt next
+        if (first + CT < my_tiles) __syncthreads();   // s.code and the tile buffers are rebuilt next
     }
     const int tt = t + tok;   // this wave's token
     uint16_t *out_row = out_base + (int64_t)tt * H * D;
@@ -2392,12 +2460,15 @@ c8_pairs(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, co
         if (part == 0 && tok == 0)
             for (int k = 0; k < gs; ++k) no_fold(t + k);
         if (!tok_live) return;
+        int lx = lane;                    // head and column from a fresh lane copy (nothing held across the loop)
+        asm volatile("" : "+v"(lx));
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
-            const int h = 2 * g + hh;
+            const int h = 2 * (lx >> 4) + hh;
             if (h >= H) continue;
 #pragma unroll
-            for (int j = 0; j < 8; ++j) out_row[h * D + c0 + 16 * j + n] = (uint16_t)pack_bf16(num[hh][j] / den[hh], 0.0f);
+            for (int j = 0; j < 8; ++j)
+                out_row[h * D + c0 + 16 * j + (lx & 15)] = (uint16_t)pack_bf16(num[hh][j] / den[hh], 0.0f);
             if (lse_base && tw == 0 && n == 0) lse_base[(int64_t)tt * H + h] = mx[hh] + logf(den[hh]);
         }
         return;
@@ -2407,12 +2478,14 @@ c8_pairs(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, co
     if (tok_live) {
         const __amdgpu_buffer_rsrc_t states =
             row_states(reinterpret_cast<float *>(p.partial) + (int64_t)tt * S * HEADS * PART_FLOATS);
+        int lx = lane;                    // head and column from a fresh lane copy (nothing held across the loop)
+        asm volatile("" : "+v"(lx));
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
-            const int base = ((part * HEADS + 2 * g + hh) * PART_FLOATS) * 4;
+            const int base = ((part * HEADS + 2 * (lx >> 4) + hh) * PART_FLOATS) * 4;
 #pragma unroll
-            for (int j = 0; j < 8; ++j) state_store<SC1>(num[hh][j], states, base + (c0 + 16 * j + n) * 4);
-            if (tw == 0 && n == 0) {
+            for (int j = 0; j < 8; ++j) state_store<SC1>(num[hh][j], states, base + (c0 + 16 * j + (lx & 15)) * 4);
+            if (tw == 0 && (lx & 15) == 0) {
                 state_store<SC1>(mx[hh], states, base + 512 * 4);
                 state_store<SC1>(den[hh], states, base + 513 * 4);
             }
@@ -2609,23 +2682,26 @@ int launch_attention(hipStream_t stream, const SharedKVArgs *a, const SharedKVDe
     return (int)hipGetLastError();
 }
 
-// Query-grouped launch (two tokens per group, c8_pairs): ratio 1 or 128, at
-// most eight heads, no explicit original slots.  The partition plan is the
-// launch's (`splits`); graph padding is zero-filled but not re-planned.
-int launch_paired(hipStream_t stream, const SharedKVArgs *a)
+// Query-grouped launch (groups of `group` = 2 or 4 tokens, c8_pairs): any
+// ratio, at most eight heads, no explicit original slots.  The partition
+// plan is the launch's (`splits`); graph padding is zero-filled but not
+// re-planned.
+int launch_paired(hipStream_t stream, const SharedKVArgs *a, uint32_t group)
 {
     if (check_attention(a)) return (int)hipErrorInvalidValue;
-    if ((a->ratio != 1 && a->ratio != 128) || a->heads > HEADS || a->oriIndices) return (int)hipErrorInvalidValue;
+    if (a->heads > HEADS || a->oriIndices) return (int)hipErrorInvalidValue;
+    if (group != 2 && group != 4) return (int)hipErrorInvalidValue;
     if (a->tokens == 0) return (int)hipSuccess;
     const uint32_t splits = a->splits, rows = a->tokens;
     const uint32_t grid = (rows * splits + 7u) & ~7u;
     const uint32_t fused = splits > 1 && g_merge_mode.load(std::memory_order_relaxed) == 0;
     const bool streamed = a->ratio == 128 && a->tokens <= STREAM_TOKENS_C128 * a->batch;
     const auto kernel = a->ratio == 1 ? &c8_pairs<1, false>
+                        : a->ratio == 4 ? &c8_pairs<4, false>
                         : streamed    ? &c8_pairs<128, true>
                                       : &c8_pairs<128, false>;
     hipLaunchKernelGGL(kernel, dim3(grid), dim3(THREADS), 0, stream, a->cuQ, a->seqLens, a->q, a->batch, a->heads,
-                       splits, rows, grid, *a, fused);
+                       splits, rows, grid, *a, fused, group);
     if (splits > 1 && !fused)
         hipLaunchKernelGGL(c8_merge, dim3(rows), dim3(THREADS), 0, stream, *a, splits);
     return (int)hipGetLastError();
@@ -2733,7 +2809,14 @@ int launch_sharedkv_c8_dense_paired(uint32_t blocks, void *stream, const SharedK
 {
     if (!blocks) return (int)hipSuccess;
     if (!args) return (int)hipErrorInvalidValue;
-    return launch_paired(static_cast<hipStream_t>(stream), args);
+    return launch_paired(static_cast<hipStream_t>(stream), args, 2);
+}
+
+int launch_sharedkv_c8_dense_packed(uint32_t blocks, void *stream, const SharedKVArgs *args)
+{
+    if (!blocks) return (int)hipSuccess;
+    if (!args) return (int)hipErrorInvalidValue;
+    return launch_paired(static_cast<hipStream_t>(stream), args, 4);
 }
 
 int sharedkv_c8_attention_debug(void *stream, const SharedKVArgs *args, const SharedKVDebug *debug)

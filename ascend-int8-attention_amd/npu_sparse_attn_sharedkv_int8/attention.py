@@ -108,13 +108,16 @@ class PreparedAttention:
         # rest are validated for type and recorded.  adaptive_splits has
         # nothing left to switch: the kernel always adapts the partition count
         # to the live rows of a padded launch (c8_attention.device_splits).
-        # query_group 2 on a C128 or window-only launch of at most eight heads
-        # without explicit slots runs the paired plan (reference.py:224-323
-        # with query_group 2; launch_sharedkv_c8_dense_paired); any other
-        # request runs the ungrouped plan, and self.query_group tells callers
-        # which plan ran (the reference's C8 path likewise runs its kernel's
-        # own plan, c8_attention.py:74-113; its tests rebuild the oracle plan
-        # from the device's choice, attention_cases.py:56-111).
+        # query_group 2 or 4 on a launch of at most eight heads without
+        # explicit slots runs the grouped plan (reference.py:224-323 with
+        # that query_group; launch_sharedkv_c8_dense_paired / _packed).  C4
+        # groups take the dense multiplicity list of reference.py:246-249 at
+        # any sequence length (the reference's operator accepts grouped C4
+        # only under max_seq_len <= 1024, attention.py:88-98 there).  Any
+        # other request runs the ungrouped plan, and self.query_group tells
+        # callers which plan ran (the reference's C8 path likewise runs its
+        # kernel's own plan, c8_attention.py:74-113; its tests rebuild the
+        # oracle plan from the device's choice, attention_cases.py:56-111).
         if tile_size is not None and tile_size != c8_attention.TILE:
             raise ValueError(f"This build tiles keys in groups of {c8_attention.TILE}; tile_size must be None or "
                              f"{c8_attention.TILE}")
@@ -123,9 +126,8 @@ class PreparedAttention:
         if splits is not None and (not isinstance(splits, int) or not 1 <= splits <= c8_attention.MAX_SPLITS):
             raise ValueError(f"Expected 1..{c8_attention.MAX_SPLITS} KV partitions")
         self.tile_size = c8_attention.TILE
-        paired = (query_group == 2 and case.ratio in (1, 128) and heads <= c8_attention.HEADS
-                  and case.ori_indices is None)
-        self.query_group = 2 if paired else 1
+        paired = query_group in (2, 4) and heads <= c8_attention.HEADS and case.ori_indices is None
+        self.query_group = query_group if paired else 1
         self.adaptive_splits = bool(adaptive_splits)
         self.trim_cube_tails = bool(trim_cube_tails)
         self.dynamic_c4 = self.dynamic_c128 = self.dynamic_grouped_c128 = False
@@ -175,7 +177,8 @@ class PreparedAttention:
         prepared = c8_attention.prepare(self, scratch_allocator=scratch_allocator)
         self.__dict__.update(prepared.__dict__)
         if paired:
-            self.variant = c8_attention.VARIANT_DENSE_PAIRED
+            self.variant = (c8_attention.VARIANT_DENSE_PAIRED if query_group == 2
+                            else c8_attention.VARIANT_DENSE_PACKED)
 
     def _rebind_same_geometry(self, case, *, output=None, lse_output=None):
         """Serving fast path: same geometry, new tensors (attention.py:233-247)."""

@@ -49,6 +49,7 @@ PARTIAL_FLOATS = 520       # per (token, partition, head): 512 numerator, max, d
 
 VARIANT_SPARSE, VARIANT_DENSE, VARIANT_SPARSE_SMALL = 20, 21, 22
 VARIANT_DENSE_PAIRED = 23      # the query-grouped (two tokens per group) plan
+VARIANT_DENSE_PACKED = 24      # the same in groups of four tokens
 
 # A workspace of this size serves any launch of up to WORKSPACE_ROWS rows (one
 # uint32 merge ticket per row), for callers that size one shared workspace up
@@ -100,12 +101,18 @@ def choose_splits(tokens, ratio, topk, max_seq_len=None, ori_topk=0):
 
 
 def choose_paired_splits(tokens, ratio, max_seq_len=None):
-    """KV partitions of a paired launch (query_group 2): the plan of its
-    groups (at most ceil(tokens / 2) of them), whose window list can take a
-    second tile (up to 129 rows)."""
+    """KV partitions of a query-grouped launch (query_group 2 or 4): the plan
+    of its work-groups (one per pair of tokens, at most ceil(tokens / 2) of
+    them), whose window list can take a second tile (up to 129 or 131
+    rows).  A C4 group lists every compressed row below its last position
+    / 4 (max_seq_len // 4 rows at most)."""
     if tokens <= 0:
         return 1
-    return plan_splits((tokens + 1) // 2, max_tiles(ratio, 0, max_seq_len) + 1)
+    if ratio == 4:
+        tiles = MAX_SPLITS if max_seq_len is None else 2 + (max(0, int(max_seq_len)) // 4 + TILE - 1) // TILE
+    else:
+        tiles = max_tiles(ratio, 0, max_seq_len) + 1
+    return plan_splits((tokens + 1) // 2, tiles)
 
 
 def live_shape(cu_q, seq_lens, tokens):

@@ -21,7 +21,8 @@ from ._paths import native_path
 
 VARIANT_SPARSE, VARIANT_DENSE, VARIANT_SPARSE_SMALL = 20, 21, 22
 VARIANT_DENSE_PAIRED = 23          # the query-grouped plan (launch_sharedkv_c8_dense_paired)
-ATTENTION_VARIANT_COUNT = 24
+VARIANT_DENSE_PACKED = 24          # groups of four (launch_sharedkv_c8_dense_packed)
+ATTENTION_VARIANT_COUNT = 25
 
 
 class SharedKVArgs(ctypes.Structure):
@@ -49,7 +50,7 @@ class SharedKVDebug(ctypes.Structure):
 
 
 EXPORTS = ("launch_sharedkv_c8_sparse", "launch_sharedkv_c8_dense", "launch_sharedkv_c8_sparse_small",
-           "launch_sharedkv_c8_dense_paired",
+           "launch_sharedkv_c8_dense_paired", "launch_sharedkv_c8_dense_packed",
            "launch_sharedkv_c8_noalloc", "sharedkv_c8_attention_debug", "launch_cache_write",
            "sharedkv_c8_workspace_bytes", "sharedkv_c8_partial_bytes", "sharedkv_c8_noalloc_scratch_bytes",
            "sharedkv_c8_noalloc_layout", "sharedkv_c8_set_merge_mode", "sharedkv_attention_args_size", "sharedkv_cache_args_size",
@@ -69,7 +70,7 @@ def library():
     import torch  # noqa: F401  (binds the library to torch's HIP runtime)
     lib = ctypes.CDLL(str(native_path()))
     for name in ("launch_sharedkv_c8_sparse", "launch_sharedkv_c8_dense", "launch_sharedkv_c8_sparse_small",
-                 "launch_sharedkv_c8_dense_paired", "launch_sharedkv_c8_noalloc"):
+                 "launch_sharedkv_c8_dense_paired", "launch_sharedkv_c8_dense_packed", "launch_sharedkv_c8_noalloc"):
         fn = getattr(lib, name)
         fn.argtypes = [ctypes.c_uint32, ctypes.c_void_p, ctypes.c_void_p]
         fn.restype = ctypes.c_int
@@ -138,7 +139,8 @@ class _Host:
         self._launchers = {VARIANT_SPARSE: lib.launch_sharedkv_c8_sparse,
                            VARIANT_DENSE: lib.launch_sharedkv_c8_dense,
                            VARIANT_SPARSE_SMALL: lib.launch_sharedkv_c8_sparse_small,
-                           VARIANT_DENSE_PAIRED: lib.launch_sharedkv_c8_dense_paired}
+                           VARIANT_DENSE_PAIRED: lib.launch_sharedkv_c8_dense_paired,
+                           VARIANT_DENSE_PACKED: lib.launch_sharedkv_c8_dense_packed}
 
     def attention(self, address, blocks, variant, device):
         """Launch on the current stream of `device` (c8_launch.cpp:20-25)."""

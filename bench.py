@@ -440,8 +440,9 @@ def main():
     ap.add_argument("--page-stride", type=int, default=None, help="override the workload's page stride (bytes)")
     ap.add_argument("--merge", type=int, default=0, help="0: fused partition merge, 1: separate merge launch")
     ap.add_argument("--heads", type=int, default=8, help="query heads per token (the metric is quoted at 8)")
-    ap.add_argument("--query-group", type=int, default=None, choices=[1, 2],
-                    help="2: the paired plan (two query tokens share each tile) for C128 / window-only launches")
+    ap.add_argument("--query-group", type=int, default=None, choices=[1, 2, 4],
+                    help="2 or 4: the query-grouped plan (groups of 2 or 4 query tokens share one window and one "
+                         "compressed list) for C128 / window-only launches")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-floor", action="store_true", help="skip the gather-floor and streaming-read legs")

@@ -113,6 +113,16 @@ int launch_sharedkv_c8_dense(uint32_t blocks, void *stream, const SharedKVArgs *
  * are zero-filled and the launch keeps its partition plan. */
 int launch_sharedkv_c8_dense_paired(uint32_t blocks, void *stream, const SharedKVArgs *args);
 
+/* Query-grouped C128 / window-only attention in groups of four: the
+ * reference device's packed plan (c128.cpp:24-27, numerics
+ * reference.py:224-323 with query_group 4), chosen by the caller
+ * (PreparedAttention(query_group=4)).  Tokens 4j .. 4j + 3 of each request
+ * form a group sharing one window list (up to 131 rows) and one compressed
+ * list (rows below (p_last + 1) / 128), each masking what it may not see;
+ * otherwise as launch_sharedkv_c8_dense_paired (same limits, scratch and
+ * padding behaviour). */
+int launch_sharedkv_c8_dense_packed(uint32_t blocks, void *stream, const SharedKVArgs *args);
+
 /* Same launch as the three above (ratio taken from args->ratio), with the
  * integer dumps written to `debug`.  Test entry; slower. */
 int sharedkv_c8_attention_debug(void *stream, const SharedKVArgs *args, const SharedKVDebug *debug);

@@ -449,9 +449,13 @@ def test_against_reference_vectors(name):
     joint row, paired query groups).  The HIP launch runs its own plan
     (128-key tiles, one partition); every stored output is within the
     BASELINE tolerance of it (BF16 mean-abs 2e-3, max-abs 2e-2 or one BF16
-    ulp of the reference value, whichever is larger; LSE within 2e-3).  Where a stored plan is a 128-key ungrouped, non-joint plan the
-    HIP launch also runs that plan's partitions and equals reference.py bit
-    for bit except rare one-ulp exp flips (at most 0.1 %), LSE within 1e-5.
+    ulp of the reference value, whichever is larger; LSE within 2e-3).
+    Where a stored plan is a 128-key plan the HIP launch can run (ungrouped
+    with the same joint rows, or query groups of 2 or 4 through the grouped
+    entries: c4_prefill G2 and G4, c4_pairs, c4_raw_holes, c128_mixed and
+    c1_group G2) the HIP launch also runs that plan's partitions and equals
+    reference.py bit for bit except rare one-ulp exp flips (at most 0.1 %),
+    LSE within 1e-5.
     Above eight heads (no residual codes) only the same-plan check applies."""
     import torch
     from npu_sparse_attn_sharedkv_int8 import PreparedAttention, SharedKVCase, c8_attention
@@ -507,15 +511,15 @@ def test_against_reference_vectors(name):
         # `splits`: 128-key tiles, ungrouped, and joint rows (C128
         # joint_dense, C4 joint_sparse) exactly when the HIP plan takes them
         # (one partition, at most eight heads, no explicit slots).
-        # The paired plan (query_group 2, launch_sharedkv_c8_dense_paired)
-        # covers the stored 128-key, non-joint C128 and window-only G2 plans.
+        # The grouped plans (query_group 2 and 4, launch_sharedkv_c8_dense_paired
+        # / _packed) cover the stored 128-key, non-joint G2 and G4 plans.
         joint_here = splits == 1 and c8_attention.joint_plan(ratio, z["q"].shape[1], "ori_indices" in z.files)
         stored_joint = bool(jd) if ratio == 128 else bool(js) if ratio == 4 else False
-        paired = group == 2 and ratio in (1, 128) and not jd and z["q"].shape[1] <= 8
-        if tile != 128 or dense or not (group == 1 and stored_joint == joint_here or paired):
+        grouped = group in (2, 4) and not jd and z["q"].shape[1] <= 8 and "ori_indices" not in z.files
+        if tile != 128 or dense or not (group == 1 and stored_joint == joint_here or grouped):
             continue
         say(f"[reference vectors] {name} plan {i}: splits={splits}, query group {group}")
-        got, got_lse = launch(splits, query_group=2 if paired else None)
+        got, got_lse = launch(splits, query_group=group if grouped else None)
         assert (got == want).mean() >= 0.999, (name, i)
         np.testing.assert_allclose(got_lse, z[f"lse_{i}"][:live], rtol=0, atol=1e-5)
 
@@ -1157,16 +1161,17 @@ def test_empty_launch_is_a_no_op():
 
 def test_planner_knobs_report_the_plan_that_ran():
     """The Ascend planner's knobs (attention.py:27-30 of the reference) are
-    validated; query_group and the planner switches are not applied, and the
-    operator reports the plan that ran (tile_size, query_group, splits), the
-    fields the reference's tests rebuild their oracle plan from."""
+    validated; the planner switches are not applied (query_group is, in
+    test_gpu_paired.py), and the operator reports the plan that ran
+    (tile_size, query_group, splits), the fields the reference's tests
+    rebuild their oracle plan from."""
     import torch
     from npu_sparse_attn_sharedkv_int8 import PreparedAttention
     case = workloads.make_case(27, 4, [2, 2], [700, 3000], index_mode="uniform")
     dev, oscale, cscale, keep = to_device(case)
     plain = PreparedAttention(dev, oscale, cscale, return_lse=True)
     plain.run()
-    for kw in ({"query_group": 2}, {"query_group": 4, "max_seq_len": 1024}, {"adaptive_splits": True},
+    for kw in ({"query_group": 1}, {"tile_size": 128, "max_seq_len": 1024}, {"adaptive_splits": True},
                {"trim_cube_tails": True, "dynamic_c4": True}):
         op = PreparedAttention(dev, oscale, cscale, return_lse=True, **kw)
         assert (op.tile_size, op.query_group, op.splits) == (128, 1, plain.splits), kw

@@ -3,10 +3,9 @@ explicit original slots, C4 index modes, short contexts (joint rows),
 prefill-like chunks of 260-400 tokens (c8_rows: work-groups taking rows in
 turn), graph-capacity padding rows (a few, or enough that the device
 re-plans the live rows, c8_rows capacities included), compressed block
-tables as wide as a serving table, the paired plan (query_group 2 on C128
-and window-only launches), KV partitions (1-8) and both merge placements,
-all bit-exact (BF16 outputs) with the checker on the launch's own plan and
-LSE within 2e-6."""
+tables as wide as a serving table, the grouped plans (query_group 2 and
+4), KV partitions (1-8) and both merge placements, all bit-exact (BF16
+outputs) with the checker on the launch's own plan and LSE within 2e-6."""
 import os
 import sys
 
@@ -67,8 +66,9 @@ def random_case(seed):
         if extra > 0:
             case["cmp"].table = np.ascontiguousarray(
                 np.concatenate([narrow, np.tile(narrow[:, :1], (1, extra))], axis=1))
-    # One C128 / window-only launch in four asks for the paired plan.
-    group = 2 if ratio in (1, 128) and heads <= 8 and not slot_mode and rng.random() < 0.25 else None
+    # One launch in four asks for a grouped plan (groups of two or four query
+    # tokens).
+    group = int(rng.choice([2, 4])) if heads <= 8 and not slot_mode and rng.random() < 0.25 else None
     if pad:
         # Graph capacity: a synthetic request of `pad` NaN query rows with
         # seq_len 0 after the live ones (zero-filled by the kernel).

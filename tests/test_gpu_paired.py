@@ -1,14 +1,18 @@
-"""The paired plan (query_group 2) on the GPU against the CPU checker.
+"""The query-grouped plans (query_group 2 and 4) on the GPU against the CPU
+checker.
 
-reference.py:224-323 with query_group 2: consecutive tokens 2j, 2j + 1 of a
-request share one window list (positions max(0, p0 + 1 - 128) .. p1) and one
-C128 compressed list (rows below (p1 + 1) / 128), each masking what it may
-not see.  PreparedAttention(query_group=2) runs it through
-launch_sharedkv_c8_dense_paired (c8_pairs: one work-group per group and
-partition, the group's tiles fetched once).  Every launch is checked bit for
-bit against oracle.tiled_attention(query_group=2) at the launch's
-partitions, and shown to differ from the ungrouped plan where the window of
-the second token makes the tiling differ.
+reference.py:224-323 with query_group G: consecutive tokens G j .. G j + G - 1
+of a request share one window list (positions max(0, p_first + 1 - 128) ..
+p_last) and one compressed list (C128: rows below (p_last + 1) / 128; C4:
+rows below (p_last + 1) / 4, each token weighing a row by its multiplicity
+among its own valid top-k entries), each masking what it may not see.  PreparedAttention(query_group=2) runs it
+through launch_sharedkv_c8_dense_paired, query_group=4 through
+launch_sharedkv_c8_dense_packed (c8_pairs: one work-group per pair of tokens
+within a group and partition, the group's tiles fetched once per pair).
+Every launch is checked bit for bit against
+oracle.tiled_attention(query_group=G) at the launch's partitions, and shown
+to differ from the ungrouped plan (and G = 4 from G = 2) where the group's
+window makes the tiling differ.
 """
 import sys
 
@@ -25,10 +29,10 @@ def say(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def check(case, splits, tag, merge_mode=0):
-    out, lse, op = run_hip(case, splits=splits, query_group=2)
-    assert op.query_group == 2 and op.device_splits() == op.splits
-    ref, ref_lse, _ = run_oracle(case, op.splits, query_group=2)
+def check(case, splits, tag, group=2):
+    out, lse, op = run_hip(case, splits=splits, query_group=group)
+    assert op.query_group == group and op.device_splits() == op.splits
+    ref, ref_lse, _ = run_oracle(case, op.splits, query_group=group)
     live = int(case["cu_q"][-1])
     diff = out[:live] != ref[:live]
     assert not diff.any(), f"{tag}: {int(diff.sum())} BF16 mismatches of {diff[:live].size}"
@@ -43,40 +47,65 @@ CASES = [
     ("odd_groups", 103, 128, [3, 1, 5, 2], [3000, 700, 9000, 128]),
     ("prefill_chunk", 104, 128, [24], [6000]),
     ("window_only", 105, 1, [2, 3, 1, 4], [90, 700, 5, 300]),
+    ("ragged_fours", 110, 128, [4, 7, 1, 6, 4], [131, 4000, 900, 20000, 256]),
+    ("window_fours", 111, 1, [4, 5, 8, 3], [4, 133, 700, 2000]),
+    # C4 groups: the dense list of the group's compressed rows, each token
+    # weighing a row by its multiplicity among its own valid top-k entries.
+    ("c4_short", 114, 4, [2, 3, 4], [300, 1000, 700]),
+    ("c4_dups", 115, 4, [4, 2], [5000, 3000], "dups"),
+    ("c4_holes", 116, 4, [3, 4, 1], [4200, 9000, 40], "holes"),
+    ("c4_long_mixed", 117, 4, [4], [20000], "mixed"),
+    ("c4_one_key", 118, 4, [2, 4, 2], [600, 2500, 9], "one_key_duplicates"),
 ]
 
 
-@pytest.mark.parametrize("name,seed,ratio,queries,lengths", CASES, ids=[c[0] for c in CASES])
+@pytest.mark.parametrize("name,seed,ratio,queries,lengths,mode", [c + ("uniform",) * (6 - len(c)) for c in CASES],
+                         ids=[c[0] for c in CASES])
 @pytest.mark.parametrize("splits", [1, 2, 3, 5])
-def test_paired_plan_matches_checker(name, seed, ratio, queries, lengths, splits):
-    case = workloads.make_case(seed, ratio, queries, lengths)
-    say(f"[paired] {name} splits {splits}")
-    out, op = check(case, splits, f"{name} splits {splits}")
-    if name == "mtp_pairs":
-        # The second token's window starts one row later: the tiling, and so
-        # the numerics, differ from the ungrouped plan.
+@pytest.mark.parametrize("group", [2, 4])
+def test_grouped_plan_matches_checker(name, seed, ratio, queries, lengths, mode, splits, group):
+    case = workloads.make_case(seed, ratio, queries, lengths, index_mode=mode)
+    say(f"[grouped G{group}] {name} splits {splits}")
+    out, op = check(case, splits, f"G{group} {name} splits {splits}", group)
+    if name in ("mtp_pairs", "ragged_fours"):
+        # A later token's window starts later than the group's: the tiling,
+        # and so the numerics, differ from the ungrouped plan, and between
+        # groups of two and of four unless every request has two tokens.
         ungrouped, _, _ = run_oracle(case, splits)
         assert (out != ungrouped).any()
+        other, _, _ = run_oracle(case, splits, query_group=6 - group)
+        assert np.array_equal(out, other) == (name == "mtp_pairs")
 
 
-def test_paired_plan_heads_and_default_partitions():
+@pytest.mark.parametrize("group", [2, 4])
+def test_grouped_plan_heads_and_default_partitions(group):
     """Fewer than eight heads (the padding heads of the work-group are never
     written) and the library's own partition plan (choose_paired_splits)."""
     from npu_sparse_attn_sharedkv_int8 import c8_attention
     for heads in (4, 8):
-        case = workloads.make_case(106, 128, [2] * 8, [2000 + 997 * i for i in range(8)], heads=heads)
-        out, op = check(case, None, f"{heads} heads")
-        assert op.splits == c8_attention.choose_paired_splits(16, 128)
+        case = workloads.make_case(106, 128, [4] * 8, [2000 + 997 * i for i in range(8)], heads=heads)
+        out, op = check(case, None, f"G{group} {heads} heads", group)
+        assert op.splits == c8_attention.choose_paired_splits(32, 128)
 
 
+def test_packed_prefill_chunk():
+    """A C128 prefill chunk (B = 1 x T = 256 at 9000 context) in groups of
+    four, at one partition (the reference device's packed plan) and at two."""
+    case = workloads.make_case(112, 128, [256], [9000])
+    for splits in (1, 2):
+        say(f"[grouped G4] prefill chunk splits {splits}")
+        check(case, splits, f"G4 prefill splits {splits}", 4)
+
+
+@pytest.mark.parametrize("group", [2, 4])
 @pytest.mark.parametrize("mode", [0, 1])
-def test_paired_plan_padding_and_merge_modes(mode):
+def test_grouped_plan_padding_and_merge_modes(mode, group):
     """Graph-padding rows past the live tokens come back zero (NaN-poisoned
     Q), in both merge placements (fused, or the separate merge launch)."""
     import torch
     from npu_sparse_attn_sharedkv_int8 import PreparedAttention
     from npu_sparse_attn_sharedkv_int8.runtime import library
-    case = workloads.make_case(107, 128, [2, 2, 3], [5000, 2600, 9000])
+    case = workloads.make_case(107, 128, [2, 5, 3], [5000, 2600, 9000])
     live = int(case["cu_q"][-1])
     pad = 5
     padded = dict(case, q=np.concatenate([case["q"], np.full((pad, 8, 512), 0x7FC0, np.uint16)]))
@@ -87,30 +116,33 @@ def test_paired_plan_padding_and_merge_modes(mode):
     assert library().sharedkv_c8_set_merge_mode(mode) == 0
     try:
         dev, oscale, cscale, keep = to_device(padded)
-        op = PreparedAttention(dev, oscale, cscale, splits=3, return_lse=True, query_group=2)
+        op = PreparedAttention(dev, oscale, cscale, splits=3, return_lse=True, query_group=group)
         op.out.fill_(float("nan"))
         op.lse.fill_(float("nan"))
-        say(f"[paired padding] merge mode {mode}")
+        say(f"[grouped G{group} padding] merge mode {mode}")
         op.run()
         torch.cuda.synchronize()
     finally:
         library().sharedkv_c8_set_merge_mode(0)
     out, lse = bits_of(op.out), op.lse.cpu().numpy()
     assert not out[live:].any() and not lse[live:].any(), "padding rows are not zero"
-    ref, ref_lse, _ = run_oracle(case, 3, query_group=2)
+    ref, ref_lse, _ = run_oracle(case, 3, query_group=group)
     assert np.array_equal(out[:live], ref)
     np.testing.assert_allclose(lse[:live], ref_lse, rtol=0, atol=2e-6)
 
 
-def test_other_groupings_run_the_ungrouped_plan():
-    """query_group 2 on C4 launches, query_group 4, or explicit original
-    slots run (and report) the ungrouped plan."""
+@pytest.mark.parametrize("group", [2, 4])
+def test_other_groupings_run_the_ungrouped_plan(group):
+    """query_group 2 or 4 above eight heads or with explicit original slots
+    runs (and reports) the ungrouped plan."""
     from npu_sparse_attn_sharedkv_int8 import c8_attention
-    case = workloads.make_case(108, 4, [2, 2], [3000, 5000], index_mode="uniform")
-    out, lse, op = run_hip(case, splits=3, query_group=2)
-    assert op.query_group == 1 and op.variant != c8_attention.VARIANT_DENSE_PAIRED
-    ref, _, _ = run_oracle(case, op.device_splits())
-    assert np.array_equal(out, ref)
-    case = workloads.make_case(109, 128, [2, 2], [3000, 5000])
-    out, lse, op = run_hip(case, splits=3, query_group=4)
-    assert op.query_group == 1
+    grouped = (c8_attention.VARIANT_DENSE_PAIRED, c8_attention.VARIANT_DENSE_PACKED)
+    for tag, case in (
+            ("C4, 12 heads", workloads.make_case(108, 4, [2, 2], [3000, 5000], heads=12)),
+            ("12 heads", workloads.make_case(109, 128, [4, 4], [3000, 5000], heads=12)),
+            ("original slots", workloads.make_case(113, 128, [4, 2], [3000, 5000], ori_slots="draft"))):
+        say(f"[grouped G{group}] {tag}: ungrouped")
+        out, lse, op = run_hip(case, splits=3, query_group=group)
+        assert op.query_group == 1 and op.variant not in grouped, tag
+        ref, _, _ = run_oracle(case, op.device_splits())
+        assert np.array_equal(out, ref), tag
