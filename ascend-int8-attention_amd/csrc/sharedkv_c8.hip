@@ -293,6 +293,15 @@ struct Row {
 // through to, and read from, the point of coherence of all XCDs) instead of
 // flushing and invalidating the whole L2 around a device-scope fence.
 constexpr int SC1 = 16;                    // cache-policy operand: sc1
+constexpr int SC0 = 1;                     // cache-policy operand: sc0 (miss the CU's L1, read the XCD's L2)
+// Bits of the attention kernels' `fused` argument.  FUSED_MERGE: the last
+// partition of a row folds it in the launch.  FUSED_XCD_LOCAL: work-groups
+// whose blockIdx agree modulo 8 run on one XCD (checked once per device by
+// the library's dispatch probe), so a row whose partitions all sit on one
+// XCD exchanges its states through that XCD's L2 (sc0 stores and loads)
+// instead of the device's point of coherence; its ticket stays
+// device-coherent.
+constexpr uint32_t FUSED_MERGE = 1, FUSED_XCD_LOCAL = 2;
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t row_states(float *base)
 {
     return __builtin_amdgcn_make_buffer_rsrc(base, 0, 0x7fffffff, 0x00020000);
@@ -442,7 +451,8 @@ c8_attention(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, n = lane & 15;
 
     // XCD-aware order: consecutive work items (the partitions of one row,
-    // then the next row) stay on one XCD and share its L2.
+    // then the next row) stay on one XCD and share its L2: XCD x takes the
+    // items [x G / 8, (x + 1) G / 8).
     const uint32_t G = grid;
     const uint32_t item = (blockIdx.x & 7u) * (G >> 3) + (blockIdx.x >> 3);
     const uint32_t items = rows_arg * splits;
@@ -459,6 +469,13 @@ c8_attention(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base
     int32_t hbase = ANYH ? HEADS * (qrow % HG) : 0;
     int hlive = ANYH ? (H - hbase < HEADS ? H - hbase : HEADS) : HEADS;
     int32_t part = (int32_t)(item % splits);
+    // Whether every partition of this work item's row runs on this
+    // work-group's XCD: items [x G / 8, (x + 1) G / 8) are on XCD x.
+    const uint32_t per_xcd_items = G >> 3;
+    auto same_xcd = [&](uint32_t row, uint32_t parts) {
+        return (row * parts) / per_xcd_items == (row * parts + parts - 1) / per_xcd_items;
+    };
+    bool together = same_xcd((uint32_t)qrow, splits);
 
     // ---- prologue: the loads the selection needs, issued together ----
     // cu_q, seq_lens, q_base, cmp_indices, batch_arg, topk_arg, heads_arg,
@@ -595,6 +612,8 @@ c8_attention(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base
         // every XCD has the work-groups for its share (the fullest XCD holds
         // ceil(R / 8) rows; XCD 7 loses the grid's rounding work-groups);
         // otherwise item i takes row i / plan on the launch's own order.
+        // (XCD x holds min(G / 8, items - x G / 8) work-groups; usable is
+        // the fewest, that of XCD 7, or negative when XCD 7 holds none.)
         int32_t row;
         const int32_t per_xcd = (int32_t)(G >> 3), usable = per_xcd - (int32_t)(G - items);
         if ((live_rows + 7) / 8 * plan <= usable) {
@@ -602,10 +621,12 @@ c8_attention(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base
             row = x * live_rows / 8 + j / plan;
             if (row >= (x + 1) * live_rows / 8) return;
             part = j % plan;
+            together = true;
         } else {
             if (item >= (uint32_t)(live_rows * plan)) return;
             row = (int32_t)(item / (uint32_t)plan);
             part = (int32_t)(item % (uint32_t)plan);
+            together = same_xcd((uint32_t)row, (uint32_t)plan);
         }
         S = plan;
         if (row != qrow) {
@@ -1373,18 +1394,32 @@ c8_attention(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base
         }
 
         // ---- publish this partition: [num 512, max, den] per head ----
+        // A fused row whose partitions share this XCD exchanges its states
+        // through the XCD's L2 (uniform over the row: a function of the row,
+        // the plan and the grid).
+        const bool local = (fused & FUSED_XCD_LOCAL) && together;
         float *row_partial = reinterpret_cast<float *>(p.partial) + (int64_t)qrow * S * HEADS * PART_FLOATS;
         const __amdgpu_buffer_rsrc_t states = row_states(row_partial);
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
             const int h = 2 * g + hh;
             const int base = ((part * HEADS + h) * PART_FLOATS) * 4;   // byte offset in the row's states
+            if (local) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j)
-                state_store<SC1>(num[hh][j], states, base + (c0 + 16 * j + n) * 4);
-            if (wave == 0 && n == 0) {
-                state_store<SC1>(mx[hh], states, base + 512 * 4);
-                state_store<SC1>(den[hh], states, base + 513 * 4);
+                for (int j = 0; j < 4; ++j)
+                    state_store<SC0>(num[hh][j], states, base + (c0 + 16 * j + n) * 4);
+                if (wave == 0 && n == 0) {
+                    state_store<SC0>(mx[hh], states, base + 512 * 4);
+                    state_store<SC0>(den[hh], states, base + 513 * 4);
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    state_store<SC1>(num[hh][j], states, base + (c0 + 16 * j + n) * 4);
+                if (wave == 0 && n == 0) {
+                    state_store<SC1>(mx[hh], states, base + 512 * 4);
+                    state_store<SC1>(den[hh], states, base + 513 * 4);
+                }
             }
         }
         if (!fused) {
@@ -1393,9 +1428,10 @@ c8_attention(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base
         }
 
         // ---- the last partition of the row to finish folds all of them ----
-        // Every state store above has completed (vmcnt 0) before the ticket is
-        // taken; the partition that takes the last ticket reads the states back
-        // with device-coherent (sc1) loads.
+        // Every state store above has completed (vmcnt 0: acknowledged by
+        // the XCD's L2, or by the point of coherence) before the ticket is
+        // taken; the partition that takes the last ticket reads the states
+        // back with loads of the same scope (sc0 from the shared L2, or sc1).
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
@@ -1405,7 +1441,8 @@ c8_attention(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base
         if (s.misc[5] != folded - 1) return;
         if (tid == 0) __hip_atomic_store(&tickets[qrow], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-        fold_row<SC1>(states, folded, tid, out_row, lse_row, ANYH ? hlive : HEADS);
+        if (local) fold_row<SC0>(states, folded, tid, out_row, lse_row, ANYH ? hlive : HEADS);
+        else fold_row<SC1>(states, folded, tid, out_row, lse_row, ANYH ? hlive : HEADS);
     };
     if constexpr (RATIO == 4 && JOINT) {
         if (joint_launch) run_row(std::integral_constant<bool, true>{});
@@ -2595,6 +2632,60 @@ int check_attention(const SharedKVArgs *a)
 // setting (tests and bench.py use it); read once per launch.
 std::atomic<int> g_merge_mode{0};
 
+// ---- dispatch probe: which XCD runs which work-group ----
+// The XCD-local state exchange (FUSED_XCD_LOCAL) needs work-groups whose
+// blockIdx agree modulo 8 to run on one XCD (the hardware hands work-groups
+// to the XCDs in turn).  Once per device the library launches a probe grid
+// whose work-groups record their XCC_ID and enables the exchange only if
+// the XCC_ID depends on blockIdx modulo 8 alone.  The probe writes a
+// file-scope array (no allocation) and synchronizes the stream once; it is
+// skipped while the stream is being captured (those launches use the
+// device-coherent exchange until a later eager launch has probed).
+constexpr int PROBE_GROUPS = 1024;
+static __device__ uint32_t probe_xcc[PROBE_GROUPS];
+
+__global__ void __launch_bounds__(64) xcd_probe(uint32_t *out)
+{
+    // Hardware register 20 (XCC_ID), bits 3:0: the XCD running this work-group.
+    if (threadIdx.x == 0) out[blockIdx.x] = __builtin_amdgcn_s_getreg(20 | (3 << 11)) & 15u;
+}
+
+std::atomic<int> g_xcd_allowed{1};          // sharedkv_c8_set_xcd_local
+std::atomic<int> g_xcd_state[64];           // per device: 0 not probed, 1 off, 2 on
+std::mutex g_probe_mutex;
+
+bool xcd_local_dispatch(hipStream_t stream, bool may_probe)
+{
+    if (!g_xcd_allowed.load(std::memory_order_relaxed)) return false;
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64) return false;
+    int known = g_xcd_state[device].load(std::memory_order_acquire);
+    if (known) return known == 2;
+    if (!may_probe) return false;
+    hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &status) != hipSuccess || status != hipStreamCaptureStatusNone) return false;
+    std::lock_guard<std::mutex> lock(g_probe_mutex);
+    known = g_xcd_state[device].load(std::memory_order_acquire);
+    if (known) return known == 2;
+    // Relaxed capture mode for this thread: another thread's global-mode
+    // capture does not forbid this thread's synchronization.
+    hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+    const bool exchanged = hipThreadExchangeStreamCaptureMode(&mode) == hipSuccess;
+    uint32_t *ptr = nullptr;
+    uint32_t host[PROBE_GROUPS];
+    bool ok = hipGetSymbolAddress(reinterpret_cast<void **>(&ptr), HIP_SYMBOL(probe_xcc)) == hipSuccess;
+    if (ok) {
+        hipLaunchKernelGGL(xcd_probe, dim3(PROBE_GROUPS), dim3(64), 0, stream, ptr);
+        ok = hipGetLastError() == hipSuccess &&
+             hipMemcpyAsync(host, ptr, sizeof(host), hipMemcpyDeviceToHost, stream) == hipSuccess &&
+             hipStreamSynchronize(stream) == hipSuccess;
+    }
+    for (int b = 0; ok && b < PROBE_GROUPS; ++b) ok = host[b] == host[b & 7];
+    if (exchanged) (void)hipThreadExchangeStreamCaptureMode(&mode);
+    g_xcd_state[device].store(ok ? 2 : 1, std::memory_order_release);
+    return ok;
+}
+
 template <bool DEBUG, bool ANYH>
 void launch_variant(hipStream_t stream, const SharedKVArgs *a, const SharedKVDebug &dbg, bool slots, uint32_t grid,
                     uint32_t splits, uint32_t rows, uint32_t fused, bool small_entry)
@@ -2629,7 +2720,7 @@ void launch_variant(hipStream_t stream, const SharedKVArgs *a, const SharedKVDeb
                                  : streamed    ? &c8_rows<4, true, ANYH>
                                                : &c8_rows<4, false, ANYH>;
         hipLaunchKernelGGL(rows_kernel, dim3(g2), dim3(ROWS_THREADS), 0, stream, a->cuQ, a->seqLens, a->q, a->indices,
-                           a->batch, a->topk, rows, g2, a->heads, *a, fused);
+                           a->batch, a->topk, rows, g2, a->heads, *a, fused & FUSED_MERGE);
         return;
     }
     decltype(&c8_attention<1, false, false, ANYH, false, false>) kernel =
@@ -2656,7 +2747,8 @@ void launch_variant(hipStream_t stream, const SharedKVArgs *a, const SharedKVDeb
 }
 
 template <bool DEBUG>
-int launch_attention(hipStream_t stream, const SharedKVArgs *a, const SharedKVDebug *debug, bool small_entry = false)
+int launch_attention(hipStream_t stream, const SharedKVArgs *a, const SharedKVDebug *debug, bool small_entry = false,
+                     bool may_probe = true)
 {
     if (check_attention(a)) return (int)hipErrorInvalidValue;
     if (a->tokens == 0) return (int)hipSuccess;
@@ -2664,12 +2756,21 @@ int launch_attention(hipStream_t stream, const SharedKVArgs *a, const SharedKVDe
     const uint32_t splits = a->splits;
     const uint32_t rows = a->tokens * head_groups(a->heads);
     const uint32_t items = rows * splits;
-    const uint32_t grid = (items + 7u) & ~7u;
     // Partition states may be merged inside the launch (merge mode 0) when
     // the launch has several partitions, or has one and supplies partition
     // states and tickets for the device re-plan of a padded launch.
-    const uint32_t fused = g_merge_mode.load(std::memory_order_relaxed) == 0 &&
-                           (splits > 1 || (a->partial && a->workspace && !DEBUG));
+    const bool merge = g_merge_mode.load(std::memory_order_relaxed) == 0 &&
+                       (splits > 1 || (a->partial && a->workspace && !DEBUG));
+    uint32_t fused = merge ? FUSED_MERGE | (xcd_local_dispatch(stream, may_probe) ? FUSED_XCD_LOCAL : 0u) : 0u;
+    // With the XCD-local exchange, a launch of several partitions whose
+    // items per XCD (grid / 8) are not a multiple of splits, so that some
+    // row's partitions would fall on two XCDs, takes a grid of
+    // 8 x splits x ceil(rows / 8): XCD x then holds whole rows
+    // [x ceil(rows / 8), (x + 1) ceil(rows / 8)).
+    uint32_t grid = (items + 7u) & ~7u;
+    if ((fused & FUSED_XCD_LOCAL) && splits > 1 && !DEBUG && (grid / 8u) % splits != 0 &&
+        8ull * splits * ((rows + 7u) / 8u) <= 0x7ffffff8ull)
+        grid = 8u * splits * ((rows + 7u) / 8u);
     // Debug dumps hold eight heads and one original tile (list places 0..127) per row.
     if (DEBUG && (a->heads != HEADS || (a->oriIndices && a->oriTopk > N))) return (int)hipErrorInvalidValue;
     const bool slots = a->oriIndices != 0;
@@ -2869,8 +2970,10 @@ int launch_sharedkv_c8_noalloc(uint32_t blocks, void *stream, const SharedKVArgs
     a.partial = (uint64_t)(uintptr_t)base + states;
     // The entry the package routes the launch to: C4 launches of fewer than
     // SMALL_TOKENS tokens as launch_sharedkv_c8_sparse_small.
+    // No dispatch probe from here (it copies to the host): the XCD-local
+    // exchange applies once another entry has probed this device.
     return launch_attention<false>(static_cast<hipStream_t>(stream), &a, nullptr,
-                                   a.ratio == 4 && a.tokens < SMALL_TOKENS);
+                                   a.ratio == 4 && a.tokens < SMALL_TOKENS, false);
 }
 
 uint64_t sharedkv_c8_noalloc_scratch_bytes(void) { return NOALLOC_SCRATCH_BYTES; }
@@ -2886,6 +2989,21 @@ int sharedkv_c8_set_merge_mode(int mode)
     if (mode != 0 && mode != 1) return (int)hipErrorInvalidValue;
     g_merge_mode.store(mode, std::memory_order_relaxed);
     return (int)hipSuccess;
+}
+
+int sharedkv_c8_set_xcd_local(int enable)
+{
+    if (enable != 0 && enable != 1) return (int)hipErrorInvalidValue;
+    g_xcd_allowed.store(enable, std::memory_order_relaxed);
+    return (int)hipSuccess;
+}
+
+int sharedkv_c8_xcd_local(void)
+{
+    int device = 0;
+    if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64) return -1;
+    const int known = g_xcd_state[device].load(std::memory_order_acquire);
+    return known == 0 ? -1 : known == 2 ? 1 : 0;
 }
 
 uint32_t sharedkv_attention_args_size(void) { return (uint32_t)sizeof(SharedKVArgs); }

@@ -53,7 +53,8 @@ EXPORTS = ("launch_sharedkv_c8_sparse", "launch_sharedkv_c8_dense", "launch_shar
            "launch_sharedkv_c8_dense_paired", "launch_sharedkv_c8_dense_packed",
            "launch_sharedkv_c8_noalloc", "sharedkv_c8_attention_debug", "launch_cache_write",
            "sharedkv_c8_workspace_bytes", "sharedkv_c8_partial_bytes", "sharedkv_c8_noalloc_scratch_bytes",
-           "sharedkv_c8_noalloc_layout", "sharedkv_c8_set_merge_mode", "sharedkv_attention_args_size", "sharedkv_cache_args_size",
+           "sharedkv_c8_noalloc_layout", "sharedkv_c8_set_merge_mode", "sharedkv_c8_set_xcd_local",
+           "sharedkv_c8_xcd_local", "sharedkv_attention_args_size", "sharedkv_cache_args_size",
            "sharedkv_abi_version")
 
 
@@ -88,6 +89,10 @@ def library():
     lib.sharedkv_c8_noalloc_layout.restype = ctypes.c_int
     lib.sharedkv_c8_set_merge_mode.argtypes = [ctypes.c_int]
     lib.sharedkv_c8_set_merge_mode.restype = ctypes.c_int
+    lib.sharedkv_c8_set_xcd_local.argtypes = [ctypes.c_int]
+    lib.sharedkv_c8_set_xcd_local.restype = ctypes.c_int
+    lib.sharedkv_c8_xcd_local.argtypes = []
+    lib.sharedkv_c8_xcd_local.restype = ctypes.c_int
     for name in ("sharedkv_attention_args_size", "sharedkv_cache_args_size", "sharedkv_abi_version"):
         getattr(lib, name).argtypes = []
         getattr(lib, name).restype = ctypes.c_uint32

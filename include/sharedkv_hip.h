@@ -184,6 +184,23 @@ int sharedkv_c8_noalloc_layout(uint32_t rows, uint32_t splits, uint64_t *tickets
  * identical results.  Returns 0, or hipErrorInvalidValue for other modes. */
 int sharedkv_c8_set_merge_mode(int mode);
 
+/* XCD-local partition-state exchange of the fused merge (process-wide; no
+ * counterpart in the reference, whose merge runs on one core's memory).
+ * Enabled (1, default): on a device where a one-time dispatch probe shows
+ * that work-groups whose blockIdx agree modulo 8 run on one XCD, rows whose
+ * partitions all run on one XCD pass their states through that XCD's L2;
+ * other rows, and every row on other devices, use device-coherent stores
+ * and loads.  The probe (first eager launch per device through the launch
+ * entries above, never during stream capture or from the allocation-free
+ * entry) launches one small kernel and synchronizes the stream once.
+ * Disabled (0): device-coherent exchange everywhere.  Results are identical
+ * either way.  Returns 0, or hipErrorInvalidValue for other values. */
+int sharedkv_c8_set_xcd_local(int enable);
+
+/* The current device's probe result: 1 XCD-local exchange in use, 0 not
+ * (probe failed), -1 not probed yet. */
+int sharedkv_c8_xcd_local(void);
+
 /* sizeof(SharedKVArgs), sizeof(CacheWriteArgs), library ABI version. */
 uint32_t sharedkv_attention_args_size(void);
 uint32_t sharedkv_cache_args_size(void);

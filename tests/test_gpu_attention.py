@@ -1210,6 +1210,43 @@ def test_merge_modes_match_checker(mode):
         lib.sharedkv_c8_set_merge_mode(0)
 
 
+def test_xcd_local_state_exchange():
+    """The fused merge passes a row's partition states through one XCD's L2
+    when the dispatch probe shows that work-groups agreeing in blockIdx
+    modulo 8 share an XCD; launches of several partitions then place every
+    row with all its partitions on one XCD (the headline shape: 8 rows x 3
+    partitions per XCD; one row x 5 partitions: all on XCD 0; 5 rows x 5:
+    one row on each of five XCDs).  With the exchange disabled every row
+    uses device-coherent stores and loads.  Every launch is bit-exact with
+    the checker either way, and the probe reports the exchange in use on
+    MI355X."""
+    from npu_sparse_attn_sharedkv_int8.runtime import library
+    lib = library()
+    cases = [
+        ("headline-like", workloads.make_case(29, 4, [2] * 32, [2048 + 1999 * i for i in range(32)],
+                                              index_mode="uniform"), None),
+        ("one row", workloads.make_case(32, 4, [1], [16384], index_mode="uniform"), 5),
+        ("five rows", workloads.make_case(30, 4, [1, 2, 2], [16384, 9000, 40000], index_mode="mixed"), 5),
+        ("C128 rows", workloads.make_case(31, 128, [2] * 16, [2048 + 3999 * i for i in range(16)]), None),
+    ]
+    try:
+        results = {}
+        for enable in (1, 0):
+            assert lib.sharedkv_c8_set_xcd_local(enable) == 0
+            for tag, case, splits in cases:
+                say(f"[xcd local {enable}] {tag}")
+                out, lse, op = run_hip(case, splits=splits)
+                compare(case, out, lse, op.splits, tag=f"xcd local {enable} {tag}")
+                results[(enable, tag)] = (out, lse)
+        assert lib.sharedkv_c8_xcd_local() == 1, "dispatch probe did not enable the XCD-local exchange"
+        for tag, _, _ in cases:
+            assert np.array_equal(results[(1, tag)][0], results[(0, tag)][0]), tag
+            assert np.array_equal(results[(1, tag)][1], results[(0, tag)][1]), tag
+    finally:
+        lib.sharedkv_c8_set_xcd_local(1)
+    assert lib.sharedkv_c8_set_xcd_local(2) != 0
+
+
 @pytest.mark.parametrize("mode", [0, 1])
 @pytest.mark.parametrize("ratio", [4, 128, 1])
 def test_rows_with_negative_position_are_zero(mode, ratio):
