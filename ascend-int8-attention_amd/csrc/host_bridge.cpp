@@ -15,8 +15,10 @@
 namespace {
 
 constexpr long VARIANT_SPARSE = 20, VARIANT_DENSE = 21, VARIANT_SPARSE_SMALL = 22;   // c8_launch.cpp:14-17
-constexpr long VARIANT_DENSE_PAIRED = 23;   // the query-grouped plan (launch_sharedkv_c8_dense_paired)
+constexpr long VARIANT_DENSE_PAIRED = 23;   // grouped plans, 256-key tiles: groups of two (launch_sharedkv_c8_dense_paired)
 constexpr long VARIANT_DENSE_PACKED = 24;   // groups of four (launch_sharedkv_c8_dense_packed)
+constexpr long VARIANT_PAIRED_NARROW = 25;  // grouped plans, 128-key tiles (launch_sharedkv_c8_dense_paired_narrow)
+constexpr long VARIANT_PACKED_NARROW = 26;  // (launch_sharedkv_c8_dense_packed_narrow)
 
 bool read_u64(PyObject *o, uint64_t *out)
 {
@@ -48,7 +50,9 @@ PyObject *attention(PyObject *, PyObject *const *args, Py_ssize_t nargs)
         : variant == VARIANT_DENSE ? launch_sharedkv_c8_dense
         : variant == VARIANT_SPARSE_SMALL ? launch_sharedkv_c8_sparse_small
         : variant == VARIANT_DENSE_PAIRED ? launch_sharedkv_c8_dense_paired
-        : variant == VARIANT_DENSE_PACKED ? launch_sharedkv_c8_dense_packed : nullptr;
+        : variant == VARIANT_DENSE_PACKED ? launch_sharedkv_c8_dense_packed
+        : variant == VARIANT_PAIRED_NARROW ? launch_sharedkv_c8_dense_paired_narrow
+        : variant == VARIANT_PACKED_NARROW ? launch_sharedkv_c8_dense_packed_narrow : nullptr;
     if (!launch) {
         PyErr_SetString(PyExc_ValueError, "Invalid C8 variant");   // c8_launch.cpp:17
         return nullptr;

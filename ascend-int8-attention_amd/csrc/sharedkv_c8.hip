@@ -2032,15 +2032,24 @@ c8_rows(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, con
 // logit, rows with m_r = 0 masked).  The multiplicities of the resident
 // tiles are counted in LDS per code chunk (both tokens' counts packed in one
 // word), and only rows that one of the two tokens lists are fetched.
-template <int RATIO>
+// KT = 256: the reference device's grouped plans (c128.cpp:17-27 compile
+// them with 256-key tiles; its operator accepts no other tile for grouped
+// queries, attention.py:104-106).  A 256-key tile is two 128-row halves, one
+// in each buffer of the ring: waves (tok, 0-1) take their QK keys from the
+// first half, (tok, 2-3) from the second (64 keys a wave), every wave's PV
+// runs over both halves, and the FP32 epilogue runs once per 256 keys.
+// With one tile filling the ring, the next tile's copies are issued after
+// the current tile's PV.
+template <int RATIO, int KT>
 struct alignas(16) PairShared {
-    static constexpr int CT = RATIO == 4 ? 8 : CODE_TILES;   // tiles whose row codes are resident at once
+    // Code slots resident at once (CT 128-row halves' worth).
+    static constexpr int CT = RATIO == 4 ? (KT == 256 ? 4 : 8) : CODE_TILES;
     int32_t redmax[2][HEADS][4];   // per token: per-wave tile maxima (fkey)
-    float redsum[2][HEADS][4];     // per token: per-wave weight sums of its two 16-key blocks
+    float redsum[2][HEADS][4];     // per token: per-wave weight sums of its 16-key blocks
     float asc[2][2][HEADS];        // [token][kind][head]: alpha * softmax_scale
     int32_t misc[8];
     float scale[2][D];             // channel scales of the window / compressed cache
-    int8_t p[2][16 * PROW];        // P codes per token [MFMA row][key]
+    int8_t p[2][16 * (KT + 16)];   // P codes per token [MFMA row][key]
     int32_t code[CT * N];          // row codes of the resident tiles: page * 32 + row, -1 masked
     uint64_t addr[CT * N];         // HBM address of each resident row (masked rows: the Q base)
     uint32_t mult[RATIO == 4 ? CT * N : 1];   // C4: multiplicity of each resident row, token 0 | token 1 << 16
@@ -2048,21 +2057,33 @@ struct alignas(16) PairShared {
     alignas(16) int8_t tile[2][N * D];   // the DMA ring; Q code staging before tile 1
 };
 static_assert(2 * 2 * 16 * QSTAGE <= N * D, "both tokens' Q codes fit one tile buffer");
-static_assert(sizeof(PairShared<128>) <= 160 * 1024 && sizeof(PairShared<4>) <= 160 * 1024, "one work-group per CU");
+static_assert(sizeof(PairShared<128, 128>) <= 160 * 1024 && sizeof(PairShared<4, 128>) <= 160 * 1024 &&
+                  sizeof(PairShared<128, 256>) <= 160 * 1024 && sizeof(PairShared<4, 256>) <= 160 * 1024,
+              "one work-group per CU");
 static_assert(2 * MAX_LIST == 4 * THREADS, "four index entries per thread: two tokens' top-k lists");
-static_assert(PairShared<4>::CT * N % THREADS == 0 && PairShared<128>::CT * N % THREADS == 0, "whole code rounds");
-static_assert(offsetof(PairShared<4>, tile) % 16 == 0 && offsetof(PairShared<128>, tile) % 16 == 0,
+static_assert(PairShared<4, 256>::CT * N % THREADS == 0 && PairShared<4, 128>::CT * N % THREADS == 0 &&
+                  PairShared<128, 128>::CT * N % THREADS == 0 && PairShared<4, 256>::CT * N % 256 == 0,
+              "whole code rounds, whole 256-key tiles");
+using PairsC4 = PairShared<4, 128>;
+using PairsC128 = PairShared<128, 128>;
+using PairsC4Wide = PairShared<4, 256>;
+using PairsC128Wide = PairShared<128, 256>;
+static_assert(offsetof(PairsC4, tile) % 16 == 0 && offsetof(PairsC128, tile) % 16 == 0 &&
+                  offsetof(PairsC4Wide, tile) % 16 == 0 && offsetof(PairsC128Wide, tile) % 16 == 0,
               "16-byte LDS DMA rows and tile reads");
 
-template <int RATIO, bool STREAM>
+template <int RATIO, bool STREAM, int KT>
 __global__ void __launch_bounds__(THREADS, 1)
 c8_pairs(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, const uint32_t batch_arg,
          const uint32_t heads_arg, const uint32_t splits, const uint32_t rows_arg, const uint32_t grid,
          const SharedKVArgs p, const uint32_t fused, const uint32_t group)
 {
     static_assert(RATIO == 1 || RATIO == 4 || RATIO == 128, "grouped plans: window-only, C4 and C128 launches");
-    __shared__ PairShared<RATIO> s;
-    constexpr int CT = PairShared<RATIO>::CT;
+    static_assert(KT == N || KT == 2 * N, "128- or 256-key tiles");
+    __shared__ PairShared<RATIO, KT> s;
+    constexpr int CT = PairShared<RATIO, KT>::CT;
+    constexpr int TPC = CT * N / KT;             // tiles per code chunk
+    constexpr int PR = KT + 16;                  // LDS row stride of the P codes
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, n = lane & 15;
     const int tok = wave >> 2, tw = wave & 3;   // token of the group, wave within the token
     const uint32_t G = grid;
@@ -2154,9 +2175,9 @@ c8_pairs(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, co
     // ---- the group's lists (reference.py:229-253) ----
     const int lo0 = pfirst + 1 - WINDOW > 0 ? pfirst + 1 - WINDOW : 0;
     const int ori_count = plast + 1 - lo0;            // window rows max(0, pfirst + 1 - 128) .. plast
-    const int t0w = (ori_count + N - 1) / N;
+    const int t0w = (ori_count + KT - 1) / KT;
     const int list_len = RATIO == 1 ? 0 : (plast + 1) / RATIO;   // C4: the group's dense list
-    const int total = t0w + (list_len + N - 1) / N;
+    const int total = t0w + (list_len + KT - 1) / KT;
     const int folded = S < total ? S : total;
     if (part >= folded) return;
     const int my_tiles = (total - part + S - 1) / S;
@@ -2212,10 +2233,10 @@ c8_pairs(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, co
     constexpr int DMA_STEP = DMA_PER_TILE / 4;
 
     v4i qa0[8], qa1[8];
-    for (int first = 0; first < my_tiles; first += CT) {
-        const int ntiles = my_tiles - first < CT ? my_tiles - first : CT;
+    for (int first = 0; first < my_tiles; first += TPC) {
+        const int ntiles = my_tiles - first < TPC ? my_tiles - first : TPC;
         // ---- row codes of partition tiles [first, first + ntiles) ----
-        for (int i = tid; i < ntiles * N; i += THREADS) {
+        for (int i = tid; i < ntiles * KT; i += THREADS) {
             s.code[i] = -1;
             s.addr[i] = p.q;
             if (RATIO == 4) s.mult[i] = 0;
@@ -2225,7 +2246,7 @@ c8_pairs(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, co
             // entries of both tokens (threads 0-255 the first token's, 256-511
             // the second's, four entries each) that are valid for their token
             // (reference.py:243-245: 0 <= index < count).  List place idx is
-            // tile t0w + idx / N, on this partition when that tile is
+            // tile t0w + idx / KT, on this partition when that tile is
             // part + S * l, resident when first <= l < first + ntiles.
             const int u = tid >> 8;
             const int ucount = (p0 + u + 1) / 4;
@@ -2241,10 +2262,10 @@ c8_pairs(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, co
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 if (cix[e] < 0 || cix[e] >= ucount) continue;
-                const int k = t0w + cix[e] / N;
+                const int k = t0w + cix[e] / KT;
                 if (k % S != part) continue;
                 const int l = k / S - first;
-                if (l >= 0 && l < ntiles) atomicAdd(&s.mult[l * N + cix[e] % N], u ? 65536u : 1u);
+                if (l >= 0 && l < ntiles) atomicAdd(&s.mult[l * KT + cix[e] % KT], u ? 65536u : 1u);
             }
             lds_barrier();
         }
@@ -2255,17 +2276,17 @@ c8_pairs(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, co
             const int i = tid + e * THREADS;
             tidx[e] = -1;
             tpage[e] = -1;
-            if (i >= ntiles * N) continue;
-            const int k = part + S * (first + i / N), r = i % N;
+            if (i >= ntiles * KT) continue;
+            const int k = part + S * (first + i / KT), r = i % KT;
             if (k < t0w) {
-                const int j = k * N + r;      // place in the group's window list
+                const int j = k * KT + r;     // place in the group's window list
                 const int idx = lo0 + j;
                 if (j < ori_count && idx / BLOCK_ROWS < (int)p.oriTableWidth) {
                     tidx[e] = idx;
                     tpage[e] = otab[idx / BLOCK_ROWS];
                 }
             } else if (RATIO != 1) {
-                const int idx = (k - t0w) * N + r;
+                const int idx = (k - t0w) * KT + r;
                 // C4: rows that neither token lists are not fetched.
                 if (idx < list_len && idx / BLOCK_ROWS < (int)p.cmpTableWidth && (RATIO != 4 || s.mult[i])) {
                     tidx[e] = idx;
@@ -2279,7 +2300,7 @@ c8_pairs(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, co
         for (int e = 0; e < PER; ++e) {
             if (tidx[e] < 0) continue;
             const int i = tid + e * THREADS;
-            const bool window = part + S * (first + i / N) < t0w;
+            const bool window = part + S * (first + i / KT) < t0w;
             const bool ok = tpage[e] >= 0 && (!window || (uint32_t)tpage[e] < p.oriPages);
             if (ok) {
                 s.code[i] = tpage[e] * BLOCK_ROWS + tidx[e] % BLOCK_ROWS;
@@ -2294,7 +2315,7 @@ c8_pairs(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, co
             // ---- Q folding and residual split per token and kind (reference.py:274-279),
             // staged in tile buffer 1, then picked up in the MFMA A layout ----
             // Window tiles are tiles 0 .. t0w - 1 (t0w <= 2, the window list
-            // holding at most 131 rows): this partition
+            // holding at most 131 rows; t0w = 1 with 256-key tiles): this partition
             // holds one when its first tile is one; a compressed one when its
             // last tile is one.
             const bool want[2] = {part < t0w, part + S * (my_tiles - 1) >= t0w};
@@ -2344,6 +2365,156 @@ c8_pairs(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, co
             }
             lds_barrier();                    // every wave holds its Q codes: buffer 1 is free
         }
+        if constexpr (KT == 2 * N) {
+            issue_rows(1, 1, 0, DMA_PER_TILE);           // the second half of tile 0
+            for (int i = 0; i < ntiles; ++i) {
+                const int k = part + S * (first + i);
+                const int kind = k >= t0w ? 1 : 0;
+                vm_wait<0>();
+                lds_barrier();   // both halves of tile i have landed for every wave
+                // ---- QK: S[16 rows][64 keys of this wave] (reference.py:286-289),
+                // keys 64 tw .. 64 tw + 63 of the tile, in half tw / 2 ----
+                const int8_t *tb = s.tile[tw >> 1];
+                float lg[4][2];
+                int qx = lane;                   // read addresses from a fresh lane copy (not hoisted)
+                asm volatile("" : "+v"(qx));
+#pragma unroll
+                for (int kb = 0; kb < 4; ++kb) {
+                    const int key = 64 * tw + 16 * kb + n;    // key of the tile
+                    const int sl = slot_of(64 * (tw & 1) + 16 * kb + (qx & 15));   // its slot in its half
+                    v4i acc = {0, 0, 0, 0};
+#pragma unroll
+                    for (int jq = 0; jq < 2; ++jq) {
+                        v4i b[4];
+#pragma unroll
+                        for (int j = 0; j < 4; ++j)
+                            b[j] = *reinterpret_cast<const v4i *>(tb + tile_offset(sl, 4 * (4 * jq + j) + (qx >> 4)));
+                        if (kind) {
+#pragma unroll
+                            for (int j = 0; j < 4; ++j)
+                                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(qa1[4 * jq + j], b[j], acc, 0, 0, 0);
+                        } else {
+#pragma unroll
+                            for (int j = 0; j < 4; ++j)
+                                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(qa0[4 * jq + j], b[j], acc, 0, 0, 0);
+                        }
+                    }
+                    // ---- logits with this token's masks (reference.py:288-303) ----
+                    const int idx = kind ? (k - t0w) * KT + key : lo0 + k * KT + key;
+                    const int times = RATIO == 4 && kind ? (int)((s.mult[i * KT + key] >> (16 * tok)) & 0xffffu) : 0;
+                    const bool mine = RATIO == 4 && kind ? times > 0
+                                      : kind ? idx < own_count : (idx >= own_lo && idx <= ptok);
+                    const bool valid = tok_live && mine && s.code[i * KT + key] >= 0;
+                    const float bias = RATIO == 4 && kind ? s.logt[times] : 0.0f;
+#pragma unroll
+                    for (int hh = 0; hh < 2; ++hh) {
+                        float dots = (float)acc[2 * hh];
+                        dots = dots + (float)acc[2 * hh + 1] * (float)(1.0 / 127.0);
+                        float l = dots * s.asc[tok][kind][2 * g + hh];
+                        if (RATIO == 4 && kind) l = l + bias;
+                        lg[kb][hh] = valid ? l : -1e30f;
+                    }
+                    // One block's tile reads in flight at a time: hoisting all
+                    // four blocks' reads would need 128 more registers.
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    const int kmax = row16_max_key(max(max(fkey(lg[0][hh]), fkey(lg[1][hh])),
+                                                       max(fkey(lg[2][hh]), fkey(lg[3][hh]))));
+                    if (n == 0) s.redmax[tok][2 * g + hh][tw] = kmax;
+                }
+                lds_barrier();
+                float mnew[2], factor[2];
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    const v4i a = *reinterpret_cast<const v4i *>(&s.redmax[tok][2 * g + hh][0]);
+                    mnew[hh] = fkey_value(max(max(fkey(mx[hh]), a.x), max(max(a.y, a.z), a.w)));
+                }
+                {
+                    const bool odd = n & 1;   // exp(max_old - max_new), one exponential per lane pair
+                    const float mine = sk_expf_nonpos(odd ? mx[1] - mnew[1] : mx[0] - mnew[0]);
+                    const float other = dpp<DPP_XOR1>(mine);
+                    factor[0] = odd ? other : mine;
+                    factor[1] = odd ? mine : other;
+                }
+                // ---- weights, pairwise tile sum, P codes (reference.py:304-312):
+                // 16-key blocks 4 tw .. 4 tw + 3, pairwise in key order ----
+                int8_t *pt = s.p[tok];
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    float blk[4];
+#pragma unroll
+                    for (int kb = 0; kb < 4; ++kb) {
+                        const int key = 64 * tw + 16 * kb + n;
+                        const float w = sk_expf_nonpos(lg[kb][hh] - mnew[hh]);
+                        const float x = w * 127.0f;
+                        const float ph = __builtin_rintf(x);
+                        const float pl = __builtin_rintf((x - ph) * 127.0f);
+                        pt[row_of(2 * g + hh, 0) * PR + key] = (int8_t)(int32_t)ph;
+                        pt[row_of(2 * g + hh, 1) * PR + key] = (int8_t)(int32_t)pl;
+                        blk[kb] = row16_tree_sum(w);
+                    }
+                    if (n == 0) s.redsum[tok][2 * g + hh][tw] = (blk[0] + blk[1]) + (blk[2] + blk[3]);
+                }
+                lds_barrier();
+#pragma unroll
+                for (int hh = 0; hh < 2; ++hh) {
+                    const f32x4 a = *reinterpret_cast<const f32x4 *>(&s.redsum[tok][2 * g + hh][0]);
+                    const float tile_sum = (a.x + a.y) + (a.z + a.w);   // pairwise over the sixteen blocks
+                    den[hh] = den[hh] * factor[hh] + tile_sum;
+                }
+                // ---- PV: [16 rows][this wave's 128 columns] over the 256 keys,
+                // in two halves of 64 columns, each with its FP32 epilogue.  The
+                // read addresses come from a fresh lane copy: hoisted out of
+                // the tile loop, the 64 of them would not fit beside the Q codes ----
+                int lx = lane;
+                asm volatile("" : "+v"(lx));
+                const int ng = lx >> 4, nn = lx & 15;
+#pragma unroll
+                for (int jh = 0; jh < 2; ++jh) {
+                    v4i vacc[4];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) vacc[j] = v4i{0, 0, 0, 0};
+#pragma unroll
+                    for (int kc = 0; kc < 4; ++kc) {   // keys 64 kc .. 64 kc + 63, in half kc / 2
+                        const lds_i8 *vbase = (const lds_i8 *)(s.tile[kc >> 1]);
+                        const v4i pa = *reinterpret_cast<const v4i *>(pt + nn * PR + 64 * kc + 16 * ng);
+                        const int sl_lo = slot_of(64 * (kc & 1) + 16 * ng + (nn >> 1));
+                        const int sl_hi = slot_of(64 * (kc & 1) + 16 * ng + 8 + (nn >> 1));
+                        v2i b0[4], b1[4];
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            const int chunk = 8 * tw + 4 * jh + j;
+                            b0[j] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i *)(vbase + tile_offset(sl_lo, chunk) + 8 * (nn & 1)));
+                            b1[j] = __builtin_amdgcn_ds_read_tr8_b64_v2i32((lds_v2i *)(vbase + tile_offset(sl_hi, chunk) + 8 * (nn & 1)));
+                        }
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            const v4i vb = {b0[j].x, b0[j].y, b1[j].x, b1[j].y};
+                            vacc[j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(pa, vb, vacc[j], 0, 0, 0);
+                        }
+                        __builtin_amdgcn_sched_barrier(0);   // one 64-key chunk's reads in flight at a time
+                    }
+#pragma unroll
+                    for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                        for (int j = 0; j < 4; ++j) {
+                            float dots = (float)vacc[j][2 * hh];
+                            dots = dots + (float)vacc[j][2 * hh + 1] * (float)(1.0 / 127.0);
+                            const float pv = dots * s.scale[kind][c0 + 16 * (4 * jh + j) + n] * (float)(1.0 / 127.0);
+                            num[hh][4 * jh + j] = num[hh][4 * jh + j] * factor[hh] + pv;
+                        }
+                }
+                mx[0] = mnew[0];
+                mx[1] = mnew[1];
+                if (i + 1 < ntiles) {
+                    lds_barrier();   // every wave is done with both halves and the P codes
+                    issue_rows(2 * (i + 1), 0, 0, DMA_PER_TILE);
+                    issue_rows(2 * (i + 1) + 1, 1, 0, DMA_PER_TILE);
+                }
+            }
+        } else {
         if (ntiles > 1) issue_rows(1, 1, 0, DMA_PER_TILE);
 
         for (int i = 0; i < ntiles; ++i) {
@@ -2433,8 +2604,8 @@ c8_pairs(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, co
                     const float x = w * 127.0f;
                     const float ph = __builtin_rintf(x);
                     const float pl = __builtin_rintf((x - ph) * 127.0f);
-                    pt[row_of(2 * g + hh, 0) * PROW + key] = (int8_t)(int32_t)ph;
-                    pt[row_of(2 * g + hh, 1) * PROW + key] = (int8_t)(int32_t)pl;
+                    pt[row_of(2 * g + hh, 0) * PR + key] = (int8_t)(int32_t)ph;
+                    pt[row_of(2 * g + hh, 1) * PR + key] = (int8_t)(int32_t)pl;
                     blk[kb] = row16_tree_sum(w);   // one 16-key block
                 }
                 if (n == 0) s.redsum[tok][2 * g + hh][tw] = blk[0] + blk[1];   // blocks 2 tw and 2 tw + 1
@@ -2459,7 +2630,7 @@ c8_pairs(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, co
                 for (int j = 0; j < 4; ++j) vacc[j] = v4i{0, 0, 0, 0};
 #pragma unroll
                 for (int kb = 0; kb < 2; ++kb) {
-                    const v4i pa = *reinterpret_cast<const v4i *>(pt + n * PROW + 64 * kb + 16 * g);
+                    const v4i pa = *reinterpret_cast<const v4i *>(pt + n * PR + 64 * kb + 16 * g);
                     const int sl_lo = slot_of(64 * kb + 16 * g + (n >> 1));
                     const int sl_hi = slot_of(64 * kb + 16 * g + 8 + (n >> 1));
                     v2i b0[4], b1[4];
@@ -2488,7 +2659,8 @@ c8_pairs(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, co
             mx[0] = mnew[0];
             mx[1] = mnew[1];
         }
-        if (first + CT < my_tiles) __syncthreads();   // s.code and the tile buffers are rebuilt next
+        }
+        if (first + TPC < my_tiles) __syncthreads();   // s.code and the tile buffers are rebuilt next
     }
     const int tt = t + tok;   // this wave's token
     uint16_t *out_row = out_base + (int64_t)tt * H * D;
@@ -2783,24 +2955,28 @@ int launch_attention(hipStream_t stream, const SharedKVArgs *a, const SharedKVDe
     return (int)hipGetLastError();
 }
 
-// Query-grouped launch (groups of `group` = 2 or 4 tokens, c8_pairs): any
-// ratio, at most eight heads, no explicit original slots.  The partition
-// plan is the launch's (`splits`); graph padding is zero-filled but not
-// re-planned.
-int launch_paired(hipStream_t stream, const SharedKVArgs *a, uint32_t group)
+// Query-grouped launch (groups of `group` = 2 or 4 tokens, c8_pairs, tiles
+// of `keys` = 128 or 256 keys): any ratio, at most eight heads, no explicit
+// original slots.  The partition plan is the launch's (`splits`); graph
+// padding is zero-filled but not re-planned.
+int launch_paired(hipStream_t stream, const SharedKVArgs *a, uint32_t group, uint32_t keys)
 {
     if (check_attention(a)) return (int)hipErrorInvalidValue;
     if (a->heads > HEADS || a->oriIndices) return (int)hipErrorInvalidValue;
-    if (group != 2 && group != 4) return (int)hipErrorInvalidValue;
+    if ((group != 2 && group != 4) || (keys != N && keys != 2 * N)) return (int)hipErrorInvalidValue;
     if (a->tokens == 0) return (int)hipSuccess;
     const uint32_t splits = a->splits, rows = a->tokens;
     const uint32_t grid = (rows * splits + 7u) & ~7u;
     const uint32_t fused = splits > 1 && g_merge_mode.load(std::memory_order_relaxed) == 0;
     const bool streamed = a->ratio == 128 && a->tokens <= STREAM_TOKENS_C128 * a->batch;
-    const auto kernel = a->ratio == 1 ? &c8_pairs<1, false>
-                        : a->ratio == 4 ? &c8_pairs<4, false>
-                        : streamed    ? &c8_pairs<128, true>
-                                      : &c8_pairs<128, false>;
+    const auto kernel = keys == N ? (a->ratio == 1 ? &c8_pairs<1, false, N>
+                                     : a->ratio == 4 ? &c8_pairs<4, false, N>
+                                     : streamed    ? &c8_pairs<128, true, N>
+                                                   : &c8_pairs<128, false, N>)
+                                  : (a->ratio == 1 ? &c8_pairs<1, false, 2 * N>
+                                     : a->ratio == 4 ? &c8_pairs<4, false, 2 * N>
+                                     : streamed    ? &c8_pairs<128, true, 2 * N>
+                                                   : &c8_pairs<128, false, 2 * N>);
     hipLaunchKernelGGL(kernel, dim3(grid), dim3(THREADS), 0, stream, a->cuQ, a->seqLens, a->q, a->batch, a->heads,
                        splits, rows, grid, *a, fused, group);
     if (splits > 1 && !fused)
@@ -2910,14 +3086,28 @@ int launch_sharedkv_c8_dense_paired(uint32_t blocks, void *stream, const SharedK
 {
     if (!blocks) return (int)hipSuccess;
     if (!args) return (int)hipErrorInvalidValue;
-    return launch_paired(static_cast<hipStream_t>(stream), args, 2);
+    return launch_paired(static_cast<hipStream_t>(stream), args, 2, 2 * N);
 }
 
 int launch_sharedkv_c8_dense_packed(uint32_t blocks, void *stream, const SharedKVArgs *args)
 {
     if (!blocks) return (int)hipSuccess;
     if (!args) return (int)hipErrorInvalidValue;
-    return launch_paired(static_cast<hipStream_t>(stream), args, 4);
+    return launch_paired(static_cast<hipStream_t>(stream), args, 4, 2 * N);
+}
+
+int launch_sharedkv_c8_dense_paired_narrow(uint32_t blocks, void *stream, const SharedKVArgs *args)
+{
+    if (!blocks) return (int)hipSuccess;
+    if (!args) return (int)hipErrorInvalidValue;
+    return launch_paired(static_cast<hipStream_t>(stream), args, 2, N);
+}
+
+int launch_sharedkv_c8_dense_packed_narrow(uint32_t blocks, void *stream, const SharedKVArgs *args)
+{
+    if (!blocks) return (int)hipSuccess;
+    if (!args) return (int)hipErrorInvalidValue;
+    return launch_paired(static_cast<hipStream_t>(stream), args, 4, N);
 }
 
 int sharedkv_c8_attention_debug(void *stream, const SharedKVArgs *args, const SharedKVDebug *debug)

@@ -110,23 +110,29 @@ class PreparedAttention:
         # to the live rows of a padded launch (c8_attention.device_splits).
         # query_group 2 or 4 on a launch of at most eight heads without
         # explicit slots runs the grouped plan (reference.py:224-323 with
-        # that query_group; launch_sharedkv_c8_dense_paired / _packed).  C4
-        # groups take the dense multiplicity list of reference.py:246-249 at
-        # any sequence length (the reference's operator accepts grouped C4
-        # only under max_seq_len <= 1024, attention.py:88-98 there).  Any
-        # other request runs the ungrouped plan, and self.query_group tells
+        # that query_group).  As in the reference's operator
+        # (attention.py:104-112 there) its tiles are 256 keys and it runs one
+        # KV partition unless told otherwise (launch_sharedkv_c8_dense_paired
+        # / _packed); tile_size=128 runs it on 128-key tiles at the library's
+        # partition plan (..._paired_narrow / _packed_narrow), and explicit
+        # splits apply to either.  C4 groups take the dense multiplicity list
+        # of reference.py:246-249 at any sequence length (the reference's
+        # operator accepts grouped C4 only under max_seq_len <= 1024,
+        # attention.py:88-98 there).  Any other request runs the ungrouped
+        # plan on 128-key tiles, and self.query_group / self.tile_size tell
         # callers which plan ran (the reference's C8 path likewise runs its
         # kernel's own plan, c8_attention.py:74-113; its tests rebuild the
         # oracle plan from the device's choice, attention_cases.py:56-111).
-        if tile_size is not None and tile_size != c8_attention.TILE:
-            raise ValueError(f"This build tiles keys in groups of {c8_attention.TILE}; tile_size must be None or "
-                             f"{c8_attention.TILE}")
         if query_group not in (None, 1, 2, 4):
             raise ValueError("query_group must be 1, 2 or 4")
         if splits is not None and (not isinstance(splits, int) or not 1 <= splits <= c8_attention.MAX_SPLITS):
             raise ValueError(f"Expected 1..{c8_attention.MAX_SPLITS} KV partitions")
-        self.tile_size = c8_attention.TILE
         paired = query_group in (2, 4) and heads <= c8_attention.HEADS and case.ori_indices is None
+        allowed = (c8_attention.TILE, c8_attention.GROUPED_TILE) if paired else (c8_attention.TILE,)
+        if tile_size is not None and tile_size not in allowed:
+            raise ValueError(f"tile_size must be None or one of {allowed} for this plan (grouped plans: 128 or 256 "
+                             f"keys, others: 128)")
+        self.tile_size = (tile_size or c8_attention.GROUPED_TILE) if paired else c8_attention.TILE
         self.query_group = query_group if paired else 1
         self.adaptive_splits = bool(adaptive_splits)
         self.trim_cube_tails = bool(trim_cube_tails)
@@ -144,7 +150,8 @@ class PreparedAttention:
         if splits is not None:
             self.splits = splits
         elif paired:
-            self.splits = c8_attention.choose_paired_splits(tokens, case.ratio, max_seq_len)
+            self.splits = (1 if self.tile_size == c8_attention.GROUPED_TILE
+                           else c8_attention.choose_paired_splits(tokens, case.ratio, max_seq_len))
         else:
             self.splits = c8_attention.choose_splits(
                 tokens * c8_attention.head_groups(heads), case.ratio,
@@ -177,8 +184,10 @@ class PreparedAttention:
         prepared = c8_attention.prepare(self, scratch_allocator=scratch_allocator)
         self.__dict__.update(prepared.__dict__)
         if paired:
-            self.variant = (c8_attention.VARIANT_DENSE_PAIRED if query_group == 2
-                            else c8_attention.VARIANT_DENSE_PACKED)
+            wide = self.tile_size == c8_attention.GROUPED_TILE
+            self.variant = ((c8_attention.VARIANT_DENSE_PAIRED if wide else c8_attention.VARIANT_PAIRED_NARROW)
+                            if query_group == 2 else
+                            (c8_attention.VARIANT_DENSE_PACKED if wide else c8_attention.VARIANT_PACKED_NARROW))
 
     def _rebind_same_geometry(self, case, *, output=None, lse_output=None):
         """Serving fast path: same geometry, new tensors (attention.py:233-247)."""

@@ -48,8 +48,11 @@ SPLITS_MANY_ROWS = 3
 PARTIAL_FLOATS = 520       # per (token, partition, head): 512 numerator, max, denominator, pad
 
 VARIANT_SPARSE, VARIANT_DENSE, VARIANT_SPARSE_SMALL = 20, 21, 22
-VARIANT_DENSE_PAIRED = 23      # the query-grouped (two tokens per group) plan
-VARIANT_DENSE_PACKED = 24      # the same in groups of four tokens
+VARIANT_DENSE_PAIRED = 23      # the query-grouped plans on 256-key tiles: two tokens per group
+VARIANT_DENSE_PACKED = 24      # four tokens per group
+VARIANT_PAIRED_NARROW = 25     # the same on 128-key tiles
+VARIANT_PACKED_NARROW = 26
+GROUPED_TILE = 256             # the reference's grouped plans' tile (attention.py:104-106 there)
 
 # A workspace of this size serves any launch of up to WORKSPACE_ROWS rows (one
 # uint32 merge ticket per row), for callers that size one shared workspace up

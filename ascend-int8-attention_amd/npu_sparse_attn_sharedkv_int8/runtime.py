@@ -20,9 +20,11 @@ from types import SimpleNamespace
 from ._paths import native_path
 
 VARIANT_SPARSE, VARIANT_DENSE, VARIANT_SPARSE_SMALL = 20, 21, 22
-VARIANT_DENSE_PAIRED = 23          # the query-grouped plan (launch_sharedkv_c8_dense_paired)
+VARIANT_DENSE_PAIRED = 23          # grouped plans, 256-key tiles: groups of two (launch_sharedkv_c8_dense_paired)
 VARIANT_DENSE_PACKED = 24          # groups of four (launch_sharedkv_c8_dense_packed)
-ATTENTION_VARIANT_COUNT = 25
+VARIANT_PAIRED_NARROW = 25         # grouped plans, 128-key tiles (launch_sharedkv_c8_dense_paired_narrow)
+VARIANT_PACKED_NARROW = 26         # (launch_sharedkv_c8_dense_packed_narrow)
+ATTENTION_VARIANT_COUNT = 27
 
 
 class SharedKVArgs(ctypes.Structure):
@@ -51,6 +53,7 @@ class SharedKVDebug(ctypes.Structure):
 
 EXPORTS = ("launch_sharedkv_c8_sparse", "launch_sharedkv_c8_dense", "launch_sharedkv_c8_sparse_small",
            "launch_sharedkv_c8_dense_paired", "launch_sharedkv_c8_dense_packed",
+           "launch_sharedkv_c8_dense_paired_narrow", "launch_sharedkv_c8_dense_packed_narrow",
            "launch_sharedkv_c8_noalloc", "sharedkv_c8_attention_debug", "launch_cache_write",
            "sharedkv_c8_workspace_bytes", "sharedkv_c8_partial_bytes", "sharedkv_c8_noalloc_scratch_bytes",
            "sharedkv_c8_noalloc_layout", "sharedkv_c8_set_merge_mode", "sharedkv_c8_set_xcd_local",
@@ -71,7 +74,9 @@ def library():
     import torch  # noqa: F401  (binds the library to torch's HIP runtime)
     lib = ctypes.CDLL(str(native_path()))
     for name in ("launch_sharedkv_c8_sparse", "launch_sharedkv_c8_dense", "launch_sharedkv_c8_sparse_small",
-                 "launch_sharedkv_c8_dense_paired", "launch_sharedkv_c8_dense_packed", "launch_sharedkv_c8_noalloc"):
+                 "launch_sharedkv_c8_dense_paired", "launch_sharedkv_c8_dense_packed",
+                 "launch_sharedkv_c8_dense_paired_narrow", "launch_sharedkv_c8_dense_packed_narrow",
+                 "launch_sharedkv_c8_noalloc"):
         fn = getattr(lib, name)
         fn.argtypes = [ctypes.c_uint32, ctypes.c_void_p, ctypes.c_void_p]
         fn.restype = ctypes.c_int
@@ -145,7 +150,9 @@ class _Host:
                            VARIANT_DENSE: lib.launch_sharedkv_c8_dense,
                            VARIANT_SPARSE_SMALL: lib.launch_sharedkv_c8_sparse_small,
                            VARIANT_DENSE_PAIRED: lib.launch_sharedkv_c8_dense_paired,
-                           VARIANT_DENSE_PACKED: lib.launch_sharedkv_c8_dense_packed}
+                           VARIANT_DENSE_PACKED: lib.launch_sharedkv_c8_dense_packed,
+                           VARIANT_PAIRED_NARROW: lib.launch_sharedkv_c8_dense_paired_narrow,
+                           VARIANT_PACKED_NARROW: lib.launch_sharedkv_c8_dense_packed_narrow}
 
     def attention(self, address, blocks, variant, device):
         """Launch on the current stream of `device` (c8_launch.cpp:20-25)."""

@@ -323,7 +323,7 @@ def host_cores():
     return max(1, min(share, affinity))
 
 
-def cpu_baseline(dc, layers, splits, seconds, cmp_rows, query_group=1):
+def cpu_baseline(dc, layers, splits, seconds, cmp_rows, query_group=1, tile=128):
     """Time the C restatement on whole launches of the same workload until
     about `seconds` of wall time have passed (bounded sample), on every host
     core of the job's share and then on one thread (half the time)."""
@@ -333,14 +333,14 @@ def cpu_baseline(dc, layers, splits, seconds, cmp_rows, query_group=1):
     hosts = [workloads.oracle_case(dc.host(layer)) for layer in range(min(layers, 2))]
     m = dc.meta
     joint_dense = c8_attention.joint_plan(m["ratio"], dc.heads, False) and m["ratio"] == 128 and query_group == 1
-    joint_sparse = m["ratio"] == 4 and splits == 1 and c8_attention.joint_launch(
+    joint_sparse = m["ratio"] == 4 and splits == 1 and query_group == 1 and c8_attention.joint_launch(
         splits, int(m["cu_q"][-1]), dc.heads, 4, m["cu_q"], m["seq_lens"], cmp_rows=cmp_rows)
 
     def timed(threads, budget):
         queries = launches = 0
         start = time.perf_counter()
         while time.perf_counter() - start < budget:
-            ora.tiled_attention(hosts[launches % len(hosts)], tile=128, splits=splits, return_lse=False,
+            ora.tiled_attention(hosts[launches % len(hosts)], tile=tile, splits=splits, return_lse=False,
                                 joint_dense=joint_dense, joint_sparse=joint_sparse, threads=threads,
                                 query_group=query_group)
             queries += int(dc.meta["cu_q"][-1])
@@ -442,7 +442,9 @@ def main():
     ap.add_argument("--heads", type=int, default=8, help="query heads per token (the metric is quoted at 8)")
     ap.add_argument("--query-group", type=int, default=None, choices=[1, 2, 4],
                     help="2 or 4: the query-grouped plan (groups of 2 or 4 query tokens share one window and one "
-                         "compressed list) for C128 / window-only launches")
+                         "compressed list)")
+    ap.add_argument("--tile-size", type=int, default=None, choices=[128, 256],
+                    help="keys per tile of a grouped plan (default 256, the reference operator's; 128 also)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-floor", action="store_true", help="skip the gather-floor and streaming-read legs")
@@ -488,7 +490,7 @@ def main():
     log(f"[bench] generated in {time.perf_counter() - t0:.1f} s: ori pages {dc.ori.pages}, "
         f"cmp pages {dc.cmp.pages if dc.cmp else 0}")
     ops = [PreparedAttention(dc.cases[l], dc.ori_scales[l], dc.cmp_scales[l], splits=args.splits,
-                             query_group=args.query_group)
+                             query_group=args.query_group, tile_size=args.tile_size)
            for l in range(layers)]
     splits = ops[0].splits
     group = ops[0].query_group
@@ -614,7 +616,7 @@ def main():
         "scaling": "weak", "vs_baseline": None, "dtype": "i8", "data": "synthetic (GPU-generated, seeded)",
         "config": {"workload": description, "batch": len(queries), "query_tokens": live_queries, "heads": args.heads,
                    "dim": 512, "ratio": ratio, "topk": 1024 if ratio == 4 else 0, "window": 128,
-                   "page_stride": stride, "layers_rotated": layers, "tile": 128, "splits": splits,
+                   "page_stride": stride, "layers_rotated": layers, "tile": ops[0].tile_size, "splits": splits,
                    "device_splits": device_plan,
                    "joint_rows": bool(joint), "query_group": group,
                    "lse": False, "merge": "fused" if args.merge == 0 else "separate launch",
@@ -636,7 +638,8 @@ def main():
     copy_calibration(args.copy_calibration, torch)
     if not args.no_cpu:
         log(f"[bench] CPU baseline ({args.cpu_seconds:.0f} s sample)")
-        record["cpu_baseline"] = cpu_baseline(dc, layers, device_plan, args.cpu_seconds, cmp_rows, group)
+        record["cpu_baseline"] = cpu_baseline(dc, layers, device_plan, args.cpu_seconds, cmp_rows, group,
+                                              ops[0].tile_size)
     print(json.dumps(record), flush=True)
 
 

@@ -102,29 +102,38 @@ int launch_sharedkv_c8_sparse_small(uint32_t blocks, void *stream, const SharedK
 int launch_sharedkv_c8_dense(uint32_t blocks, void *stream, const SharedKVArgs *args);
 
 /* Query-grouped attention: the reference device's paired plan (c128.cpp:17-23,
- * numerics reference.py:224-323 with query_group 2), here chosen by the
- * caller (PreparedAttention(query_group=2)); the reference's launcher picks
- * it inside launch_sharedkv_c8_dense (C128), its operator through
- * launch_sharedkv_paired[_sparse] (attention.py:189-190).  Tokens 2j and
- * 2j + 1 of each request form a group sharing one window list (up to 129
- * rows) and one compressed list (C128: rows below (p_last + 1) / 128; C4:
- * every row below (p_last + 1) / 4, each token weighing a row by its
+ * numerics reference.py:224-323 with query_group 2, tile_size 256), here
+ * chosen by the caller (PreparedAttention(query_group=2)); the reference's
+ * launcher picks it inside launch_sharedkv_c8_dense (C128), its operator
+ * through launch_sharedkv_paired[_sparse] (attention.py:189-190).  Tokens
+ * 2j and 2j + 1 of each request form a group sharing one window list (up to
+ * 129 rows) and one compressed list (C128: rows below (p_last + 1) / 128;
+ * C4: every row below (p_last + 1) / 4, each token weighing a row by its
  * multiplicity among its own valid top-k entries), each masking what it may
- * not see; 128-key tiles, tile k on partition k % splits, no joint rows.
- * Any ratio, heads <= 8, no explicit original slots (else
- * hipErrorInvalidValue).  Scratch as for the other launches at rows =
- * tokens; graph padding rows are zero-filled and the launch keeps its
- * partition plan. */
+ * not see; 256-key tiles, tile k on partition k % splits (the reference's
+ * operator runs one partition), no joint rows.  Any ratio, heads <= 8, no
+ * explicit original slots (else hipErrorInvalidValue).  Scratch as for the
+ * other launches at rows = tokens; graph padding rows are zero-filled and
+ * the launch keeps its partition plan. */
 int launch_sharedkv_c8_dense_paired(uint32_t blocks, void *stream, const SharedKVArgs *args);
 
 /* Query-grouped attention in groups of four: the reference device's packed
- * plan (c128.cpp:24-27, numerics reference.py:224-323 with query_group 4;
- * the operator's launch_sharedkv_packed[_sparse], attention.py:186), chosen
- * by the caller (PreparedAttention(query_group=4)).  Tokens 4j .. 4j + 3 of
- * each request form a group sharing one window list (up to 131 rows) and
- * one compressed list; otherwise as launch_sharedkv_c8_dense_paired (same
- * limits, scratch and padding behaviour). */
+ * plan (c128.cpp:24-27, numerics reference.py:224-323 with query_group 4,
+ * tile_size 256; the operator's launch_sharedkv_packed[_sparse],
+ * attention.py:186), chosen by the caller (PreparedAttention(query_group=4)).
+ * Tokens 4j .. 4j + 3 of each request form a group sharing one window list
+ * (up to 131 rows) and one compressed list; otherwise as
+ * launch_sharedkv_c8_dense_paired (same limits, scratch and padding
+ * behaviour). */
 int launch_sharedkv_c8_dense_packed(uint32_t blocks, void *stream, const SharedKVArgs *args);
+
+/* The same two grouped plans on 128-key tiles (reference.py:224-323 with
+ * tile_size 128 and that query_group; no counterpart among the reference's
+ * device entries, whose grouped plans are 256-key only), chosen by
+ * PreparedAttention(query_group=2 or 4, tile_size=128).  Same limits,
+ * scratch and padding behaviour. */
+int launch_sharedkv_c8_dense_paired_narrow(uint32_t blocks, void *stream, const SharedKVArgs *args);
+int launch_sharedkv_c8_dense_packed_narrow(uint32_t blocks, void *stream, const SharedKVArgs *args);
 
 /* Same launch as launch_sharedkv_c8_sparse / _dense (ratio taken from
  * args->ratio; ungrouped plan), with the integer dumps written to `debug`.

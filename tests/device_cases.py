@@ -61,12 +61,13 @@ def bits_of(tensor):
     return tensor.detach().cpu().view(torch.int16).numpy().view(np.uint16)
 
 
-def run_hip(case, splits=None, return_lse=True, device="cuda", query_group=None):
+def run_hip(case, splits=None, return_lse=True, device="cuda", query_group=None, tile_size=None):
     """One PreparedAttention launch; returns (out bits, lse, prepared)."""
     import torch
     from npu_sparse_attn_sharedkv_int8 import PreparedAttention
     dev, ori_scale, cmp_scale, keep = to_device(case, device)
-    op = PreparedAttention(dev, ori_scale, cmp_scale, splits=splits, return_lse=return_lse, query_group=query_group)
+    op = PreparedAttention(dev, ori_scale, cmp_scale, splits=splits, return_lse=return_lse, query_group=query_group,
+                           tile_size=tile_size)
     op._keep = keep
     op.run()
     torch.cuda.synchronize()
@@ -148,12 +149,12 @@ def joint_flags(case, splits, merge_mode=0):
 
 
 def run_oracle(case, splits, debug=False, cmp_capacity=None, tile_capacity=None, threads=None, joint=None,
-               query_group=1):
-    """The CPU checker with this build's plan: 128-key tiles, `splits`
-    partitions (the ones the kernel runs), and joint rows where the kernel
-    takes them: `joint` = joint_flags of the launch (default: those of
-    `case` as its own launch at `splits`); the debug entry runs the tiled
-    plan."""
+               query_group=1, tile=128):
+    """The CPU checker with this build's plan: `tile`-key tiles (128; the
+    grouped plans also 256), `splits` partitions (the ones the kernel runs),
+    and joint rows where the kernel takes them: `joint` = joint_flags of the
+    launch (default: those of `case` as its own launch at `splits`); the
+    debug entry runs the tiled plan."""
     import oracle.oracle as ora
     if joint is None:   # a joint-plan launch runs one partition
         dense, sparse = joint_flags(case, splits)
@@ -162,7 +163,7 @@ def run_oracle(case, splits, debug=False, cmp_capacity=None, tile_capacity=None,
         dense, sparse = joint
     if query_group != 1:   # the paired plan has no joint rows
         dense = sparse = False
-    return ora.tiled_attention(workloads.oracle_case(case), tile=128, splits=splits, return_lse=True,
+    return ora.tiled_attention(workloads.oracle_case(case), tile=tile, splits=splits, return_lse=True,
                                joint_dense=dense and not debug, joint_sparse=sparse and not debug, debug=debug,
                                cmp_capacity=cmp_capacity, tile_capacity=tile_capacity, threads=threads,
                                query_group=query_group)

@@ -450,10 +450,11 @@ def test_against_reference_vectors(name):
     (128-key tiles, one partition); every stored output is within the
     BASELINE tolerance of it (BF16 mean-abs 2e-3, max-abs 2e-2 or one BF16
     ulp of the reference value, whichever is larger; LSE within 2e-3).
-    Where a stored plan is a 128-key plan the HIP launch can run (ungrouped
-    with the same joint rows, or query groups of 2 or 4 through the grouped
-    entries: c4_prefill G2 and G4, c4_pairs, c4_raw_holes, c128_mixed and
-    c1_group G2) the HIP launch also runs that plan's partitions and equals
+    Where a stored plan is one the HIP launch can run (128-key ungrouped
+    with the same joint rows, or query groups of 2 or 4 on 128- or 256-key
+    tiles through the grouped entries: c4_prefill G2 and G4, c4_pairs G2 at
+    128 and 256 keys, c4_raw_holes, c128_mixed and c1_group G2, c128_pairs
+    G2 at 256 keys) the HIP launch also runs that plan's partitions and equals
     reference.py bit for bit except rare one-ulp exp flips (at most 0.1 %),
     LSE within 1e-5.
     Above eight heads (no residual codes) only the same-plan check applies."""
@@ -476,11 +477,11 @@ def test_against_reference_vectors(name):
         ori_indices=torch.from_numpy(z["ori_indices"]).to(dev) if "ori_indices" in z.files else None)
     live = int(z["cu_q"][-1])
 
-    def launch(splits, query_group=None):
+    def launch(splits, query_group=None, tile_size=None):
         op = PreparedAttention(case, torch.from_numpy(z["ori_scale"]).to(dev),
                                torch.from_numpy(z["cmp_scale"]).to(dev) if ratio != 1 else None, splits=splits,
-                               return_lse=True, query_group=query_group)
-        assert op.query_group == (query_group or 1)
+                               return_lse=True, query_group=query_group, tile_size=tile_size)
+        assert op.query_group == (query_group or 1) and op.tile_size == (tile_size or 128)
         op.run()
         torch.cuda.synchronize()
         return bits_of(op.out)[:live], op.lse.cpu().numpy()[:live]
@@ -516,10 +517,10 @@ def test_against_reference_vectors(name):
         joint_here = splits == 1 and c8_attention.joint_plan(ratio, z["q"].shape[1], "ori_indices" in z.files)
         stored_joint = bool(jd) if ratio == 128 else bool(js) if ratio == 4 else False
         grouped = group in (2, 4) and not jd and z["q"].shape[1] <= 8 and "ori_indices" not in z.files
-        if tile != 128 or dense or not (group == 1 and stored_joint == joint_here or grouped):
+        if dense or not (tile == 128 and group == 1 and stored_joint == joint_here or grouped and tile in (128, 256)):
             continue
-        say(f"[reference vectors] {name} plan {i}: splits={splits}, query group {group}")
-        got, got_lse = launch(splits, query_group=group if grouped else None)
+        say(f"[reference vectors] {name} plan {i}: tile={tile}, splits={splits}, query group {group}")
+        got, got_lse = launch(splits, query_group=group if grouped else None, tile_size=tile if grouped else None)
         assert (got == want).mean() >= 0.999, (name, i)
         np.testing.assert_allclose(got_lse, z[f"lse_{i}"][:live], rtol=0, atol=1e-5)
 

@@ -4,8 +4,9 @@ prefill-like chunks of 260-400 tokens (c8_rows: work-groups taking rows in
 turn), graph-capacity padding rows (a few, or enough that the device
 re-plans the live rows, c8_rows capacities included), compressed block
 tables as wide as a serving table, the grouped plans (query_group 2 and
-4), KV partitions (1-8) and both merge placements, all bit-exact (BF16
-outputs) with the checker on the launch's own plan and LSE within 2e-6."""
+4, 128- and 256-key tiles), KV partitions (1-8) and both merge placements,
+all bit-exact (BF16 outputs) with the checker on the launch's own plan and
+LSE within 2e-6."""
 import os
 import sys
 
@@ -69,6 +70,7 @@ def random_case(seed):
     # One launch in four asks for a grouped plan (groups of two or four query
     # tokens).
     group = int(rng.choice([2, 4])) if heads <= 8 and not slot_mode and rng.random() < 0.25 else None
+    tile = int(rng.choice([128, 256])) if group else None
     if pad:
         # Graph capacity: a synthetic request of `pad` NaN query rows with
         # seq_len 0 after the live ones (zero-filled by the kernel).
@@ -85,7 +87,7 @@ def random_case(seed):
                 case[key] = np.concatenate([case[key], filler])
     return case, (None if splits is None else int(splits)), merge, dict(
         ratio=ratio, queries=queries, lengths=lengths, heads=heads, mode=mode, slots=slot_mode, topk=topk,
-        pad=pad, wide=case["cmp"].table.shape[1] if wide else 0, group=group,
+        pad=pad, wide=case["cmp"].table.shape[1] if wide else 0, group=group, tile=tile,
         joint=bool(ratio != 1 and max(lengths) // ratio <= 128 and heads <= 8 and not slot_mode))
 
 
@@ -97,7 +99,7 @@ def test_random_launch_matches_checker(seed):
     lib = library()
     try:
         assert lib.sharedkv_c8_set_merge_mode(merge) == 0
-        out, lse, op = run_hip(case, splits=splits, query_group=desc["group"])
+        out, lse, op = run_hip(case, splits=splits, query_group=desc["group"], tile_size=desc["tile"])
     finally:
         lib.sharedkv_c8_set_merge_mode(0)
     assert op.query_group == (desc["group"] or 1)
@@ -107,7 +109,7 @@ def test_random_launch_matches_checker(seed):
     if desc["pad"]:
         assert not out[live:].any() and not lse[live:].any(), "padding rows are not zero"
         case = dict(case, q=case["q"][:live], cu_q=case["cu_q"][:-1], seq_lens=case["seq_lens"][:-1])
-    ref, ref_lse, _ = run_oracle(case, plan, joint=joint, query_group=op.query_group)
+    ref, ref_lse, _ = run_oracle(case, plan, joint=joint, query_group=op.query_group, tile=op.tile_size)
     diff = out[:live] != ref[:live]
     assert not diff.any(), f"seed {seed}: {int(diff.sum())} BF16 mismatches of {diff.size}"
     np.testing.assert_allclose(lse[:live], ref_lse[:live], rtol=0, atol=2e-6)

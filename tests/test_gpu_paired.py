@@ -5,14 +5,16 @@ reference.py:224-323 with query_group G: consecutive tokens G j .. G j + G - 1
 of a request share one window list (positions max(0, p_first + 1 - 128) ..
 p_last) and one compressed list (C128: rows below (p_last + 1) / 128; C4:
 rows below (p_last + 1) / 4, each token weighing a row by its multiplicity
-among its own valid top-k entries), each masking what it may not see.  PreparedAttention(query_group=2) runs it
-through launch_sharedkv_c8_dense_paired, query_group=4 through
-launch_sharedkv_c8_dense_packed (c8_pairs: one work-group per pair of tokens
-within a group and partition, the group's tiles fetched once per pair).
-Every launch is checked bit for bit against
-oracle.tiled_attention(query_group=G) at the launch's partitions, and shown
-to differ from the ungrouped plan (and G = 4 from G = 2) where the group's
-window makes the tiling differ.
+among its own valid top-k entries), each masking what it may not see.
+PreparedAttention(query_group=G) runs it on 256-key tiles at one partition
+(the reference operator's grouped plan: launch_sharedkv_c8_dense_paired /
+_packed), or with tile_size=128 on 128-key tiles
+(launch_sharedkv_c8_dense_paired_narrow / _packed_narrow); c8_pairs: one
+work-group per pair of tokens within a group and partition, the group's
+tiles fetched once per pair.  Every launch is checked bit for bit against
+oracle.tiled_attention(tile, query_group=G) at the launch's partitions, and
+shown to differ from the ungrouped plan (and G = 4 from G = 2, 256-key tiles
+from 128-key ones) where the group's window makes the tiling differ.
 """
 import sys
 
@@ -29,10 +31,10 @@ def say(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def check(case, splits, tag, group=2):
-    out, lse, op = run_hip(case, splits=splits, query_group=group)
-    assert op.query_group == group and op.device_splits() == op.splits
-    ref, ref_lse, _ = run_oracle(case, op.splits, query_group=group)
+def check(case, splits, tag, group=2, tile=None):
+    out, lse, op = run_hip(case, splits=splits, query_group=group, tile_size=tile)
+    assert op.query_group == group and op.device_splits() == op.splits and op.tile_size == (tile or 256)
+    ref, ref_lse, _ = run_oracle(case, op.splits, query_group=group, tile=op.tile_size)
     live = int(case["cu_q"][-1])
     diff = out[:live] != ref[:live]
     assert not diff.any(), f"{tag}: {int(diff.sum())} BF16 mismatches of {diff[:live].size}"
@@ -63,43 +65,54 @@ CASES = [
                          ids=[c[0] for c in CASES])
 @pytest.mark.parametrize("splits", [1, 2, 3, 5])
 @pytest.mark.parametrize("group", [2, 4])
-def test_grouped_plan_matches_checker(name, seed, ratio, queries, lengths, mode, splits, group):
+@pytest.mark.parametrize("tile", [256, 128])
+def test_grouped_plan_matches_checker(name, seed, ratio, queries, lengths, mode, splits, group, tile):
     case = workloads.make_case(seed, ratio, queries, lengths, index_mode=mode)
-    say(f"[grouped G{group}] {name} splits {splits}")
-    out, op = check(case, splits, f"G{group} {name} splits {splits}", group)
+    say(f"[grouped G{group} tile {tile}] {name} splits {splits}")
+    out, op = check(case, splits, f"G{group} tile {tile} {name} splits {splits}", group, tile)
     if name in ("mtp_pairs", "ragged_fours"):
-        # A later token's window starts later than the group's: the tiling,
-        # and so the numerics, differ from the ungrouped plan, and between
-        # groups of two and of four unless every request has two tokens.
+        # A later token's window starts later than the group's: on 128-key
+        # tiles the tiling, and so the numerics, differ from the ungrouped
+        # plan and between groups of two and of four (unless every request
+        # has two tokens); a group's window list takes two 128-key tiles but
+        # one 256-key tile (whose masked rows change nothing), so the tile
+        # sizes differ too.
         ungrouped, _, _ = run_oracle(case, splits)
         assert (out != ungrouped).any()
-        other, _, _ = run_oracle(case, splits, query_group=6 - group)
-        assert np.array_equal(out, other) == (name == "mtp_pairs")
+        if tile == 128:
+            other, _, _ = run_oracle(case, splits, query_group=6 - group, tile=tile)
+            assert np.array_equal(out, other) == (name == "mtp_pairs")
+        other_tile, _, _ = run_oracle(case, splits, query_group=group, tile=384 - tile)
+        assert (out != other_tile).any()
 
 
 @pytest.mark.parametrize("group", [2, 4])
-def test_grouped_plan_heads_and_default_partitions(group):
+@pytest.mark.parametrize("tile", [256, 128])
+def test_grouped_plan_heads_and_default_partitions(group, tile):
     """Fewer than eight heads (the padding heads of the work-group are never
-    written) and the library's own partition plan (choose_paired_splits)."""
+    written) and the default partition plan: one partition on 256-key tiles
+    (the reference operator's), choose_paired_splits on 128-key tiles."""
     from npu_sparse_attn_sharedkv_int8 import c8_attention
     for heads in (4, 8):
         case = workloads.make_case(106, 128, [4] * 8, [2000 + 997 * i for i in range(8)], heads=heads)
-        out, op = check(case, None, f"G{group} {heads} heads", group)
-        assert op.splits == c8_attention.choose_paired_splits(32, 128)
+        out, op = check(case, None, f"G{group} tile {tile} {heads} heads", group, tile)
+        assert op.splits == (1 if tile == 256 else c8_attention.choose_paired_splits(32, 128))
 
 
 def test_packed_prefill_chunk():
     """A C128 prefill chunk (B = 1 x T = 256 at 9000 context) in groups of
-    four, at one partition (the reference device's packed plan) and at two."""
+    four, at one partition on 256-key tiles (the reference device's packed
+    plan), and on 128-key tiles at one and two."""
     case = workloads.make_case(112, 128, [256], [9000])
-    for splits in (1, 2):
-        say(f"[grouped G4] prefill chunk splits {splits}")
-        check(case, splits, f"G4 prefill splits {splits}", 4)
+    for tile, splits in ((256, 1), (128, 1), (128, 2)):
+        say(f"[grouped G4] prefill chunk tile {tile} splits {splits}")
+        check(case, splits, f"G4 prefill tile {tile} splits {splits}", 4, tile)
 
 
+@pytest.mark.parametrize("tile", [256, 128])
 @pytest.mark.parametrize("group", [2, 4])
 @pytest.mark.parametrize("mode", [0, 1])
-def test_grouped_plan_padding_and_merge_modes(mode, group):
+def test_grouped_plan_padding_and_merge_modes(mode, group, tile):
     """Graph-padding rows past the live tokens come back zero (NaN-poisoned
     Q), in both merge placements (fused, or the separate merge launch)."""
     import torch
@@ -116,17 +129,17 @@ def test_grouped_plan_padding_and_merge_modes(mode, group):
     assert library().sharedkv_c8_set_merge_mode(mode) == 0
     try:
         dev, oscale, cscale, keep = to_device(padded)
-        op = PreparedAttention(dev, oscale, cscale, splits=3, return_lse=True, query_group=group)
+        op = PreparedAttention(dev, oscale, cscale, splits=3, return_lse=True, query_group=group, tile_size=tile)
         op.out.fill_(float("nan"))
         op.lse.fill_(float("nan"))
-        say(f"[grouped G{group} padding] merge mode {mode}")
+        say(f"[grouped G{group} tile {tile} padding] merge mode {mode}")
         op.run()
         torch.cuda.synchronize()
     finally:
         library().sharedkv_c8_set_merge_mode(0)
     out, lse = bits_of(op.out), op.lse.cpu().numpy()
     assert not out[live:].any() and not lse[live:].any(), "padding rows are not zero"
-    ref, ref_lse, _ = run_oracle(case, 3, query_group=group)
+    ref, ref_lse, _ = run_oracle(case, 3, query_group=group, tile=tile)
     assert np.array_equal(out[:live], ref)
     np.testing.assert_allclose(lse[:live], ref_lse, rtol=0, atol=2e-6)
 
@@ -136,13 +149,17 @@ def test_other_groupings_run_the_ungrouped_plan(group):
     """query_group 2 or 4 above eight heads or with explicit original slots
     runs (and reports) the ungrouped plan."""
     from npu_sparse_attn_sharedkv_int8 import c8_attention
-    grouped = (c8_attention.VARIANT_DENSE_PAIRED, c8_attention.VARIANT_DENSE_PACKED)
+    grouped = (c8_attention.VARIANT_DENSE_PAIRED, c8_attention.VARIANT_DENSE_PACKED,
+               c8_attention.VARIANT_PAIRED_NARROW, c8_attention.VARIANT_PACKED_NARROW)
     for tag, case in (
             ("C4, 12 heads", workloads.make_case(108, 4, [2, 2], [3000, 5000], heads=12)),
             ("12 heads", workloads.make_case(109, 128, [4, 4], [3000, 5000], heads=12)),
             ("original slots", workloads.make_case(113, 128, [4, 2], [3000, 5000], ori_slots="draft"))):
         say(f"[grouped G{group}] {tag}: ungrouped")
         out, lse, op = run_hip(case, splits=3, query_group=group)
-        assert op.query_group == 1 and op.variant not in grouped, tag
+        assert op.query_group == 1 and op.tile_size == 128 and op.variant not in grouped, tag
         ref, _, _ = run_oracle(case, op.device_splits())
         assert np.array_equal(out, ref), tag
+    # 256-key tiles exist only for the grouped plans.
+    with pytest.raises(ValueError):
+        run_hip(workloads.make_case(109, 128, [4, 4], [3000, 5000], heads=12), query_group=group, tile_size=256)
