@@ -105,6 +105,13 @@ def library():
         raise RuntimeError("Native SharedKVArgs ABI changed; rebuild the library")
     if lib.sharedkv_cache_args_size() != ctypes.sizeof(CacheWriteArgs):
         raise RuntimeError("Native CacheWriteArgs ABI changed; rebuild the library")
+    # SHAREDKV_XCD_LOCAL=0 turns the fused merge's XCD-local state exchange
+    # off for the process (device-coherent exchange everywhere; same results).
+    xcd = os.environ.get("SHAREDKV_XCD_LOCAL", "1")
+    if xcd not in ("0", "1"):
+        raise ValueError("SHAREDKV_XCD_LOCAL must be 0 or 1")
+    if lib.sharedkv_c8_set_xcd_local(int(xcd)) != 0:
+        raise RuntimeError("sharedkv_c8_set_xcd_local failed")
     return lib
 
 

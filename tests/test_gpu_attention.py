@@ -6,6 +6,7 @@ Bar: INT8 Q codes, int32 QK partials, P codes and int32 PV partials bit-exact
 mean-abs 2e-3 of the reference's own reference.py vectors; LSE within 2e-6
 absolute of the checker (log is the device's own).
 """
+import os
 import sys
 from pathlib import Path
 
@@ -1244,7 +1245,7 @@ def test_xcd_local_state_exchange():
             assert np.array_equal(results[(1, tag)][0], results[(0, tag)][0]), tag
             assert np.array_equal(results[(1, tag)][1], results[(0, tag)][1]), tag
     finally:
-        lib.sharedkv_c8_set_xcd_local(1)
+        lib.sharedkv_c8_set_xcd_local(int(os.environ.get("SHAREDKV_XCD_LOCAL", "1")))
     assert lib.sharedkv_c8_set_xcd_local(2) != 0
 
 
