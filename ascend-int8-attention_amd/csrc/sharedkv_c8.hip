@@ -2016,16 +2016,17 @@ c8_rows(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, con
 // (positions max(0, p_first + 1 - 128) .. p_last, up to 127 + G rows) and,
 // for C128, one compressed list (rows below (p_last + 1) / 128); each token
 // masks what it may not see (its own window, its own compressed count) and
-// keeps its own online softmax.  128-key tiles numbered across both kinds,
-// tile k on partition k % S, no joint rows.  One work-group of 8 waves per
-// (sub-pair, partition), a sub-pair being tokens 2 i and 2 i + 1 of the
-// request within one group (a group of four has two): the group's tiles are
-// fetched into a two-tile LDS ring, waves 0-3 compute the sub-pair's first
-// token and waves 4-7 its second, each wave taking 32 keys in QK and 128
-// output columns in PV (the per-row layout of c8_rows).  Work items are
-// (token, partition); items of the second token of a sub-pair exit (the
-// sub-pair's first token takes both), items of padding or keyless tokens
-// zero-fill them.  At most eight heads (residual codes on).
+// keeps its own online softmax.  KT-key tiles (KT = 128 or 256, below)
+// numbered across both kinds, tile k on partition k % S, no joint rows.  One
+// work-group of 8 waves per (sub-pair, partition), a sub-pair being tokens
+// 2 i and 2 i + 1 of the request within one group (a group of four has
+// two): the group's tiles are fetched into a two-buffer LDS ring (two
+// 128-key tiles, or one 256-key tile), waves 0-3 compute the sub-pair's first
+// token and waves 4-7 its second, each wave taking 32 keys (64 with 256-key
+// tiles) in QK and 128 output columns in PV (the per-row layout of c8_rows).
+// Work items are (token, partition); items of the second token of a
+// sub-pair exit (the sub-pair's first token takes both), items of padding or
+// keyless tokens zero-fill them.  At most eight heads (residual codes on).
 // C4 groups (reference.py:242-253 with query_group > 1) list every
 // compressed row below (p_last + 1) / 4 once; each token weighs row r by its
 // multiplicity m_r among its own valid top-k entries (log(m_r) added to the
