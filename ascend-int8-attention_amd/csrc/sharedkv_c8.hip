@@ -1970,17 +1970,29 @@ c8_rows(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, con
             return;
         }
         // ---- publish this partition, the last one to finish folds the row
-        // (the protocol of c8_attention's fused merge) ----
+        // (the protocol of c8_attention's fused merge; a re-planned row's
+        // partitions all run on one XCD, so with the XCD-local exchange its
+        // states pass through that XCD's L2) ----
+        const bool local = (fused & FUSED_XCD_LOCAL) != 0;
         const __amdgpu_buffer_rsrc_t states =
             row_states(reinterpret_cast<float *>(p.partial) + (int64_t)qrow * S * HEADS * PART_FLOATS);
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
             const int base = ((part * HEADS + 2 * g + hh) * PART_FLOATS) * 4;
+            if (local) {
 #pragma unroll
-            for (int j = 0; j < 8; ++j) state_store<SC1>(num[hh][j], states, base + (c0 + 16 * j + n) * 4);
-            if (wave == 0 && n == 0) {
-                state_store<SC1>(mx[hh], states, base + 512 * 4);
-                state_store<SC1>(den[hh], states, base + 513 * 4);
+                for (int j = 0; j < 8; ++j) state_store<SC0>(num[hh][j], states, base + (c0 + 16 * j + n) * 4);
+                if (wave == 0 && n == 0) {
+                    state_store<SC0>(mx[hh], states, base + 512 * 4);
+                    state_store<SC0>(den[hh], states, base + 513 * 4);
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) state_store<SC1>(num[hh][j], states, base + (c0 + 16 * j + n) * 4);
+                if (wave == 0 && n == 0) {
+                    state_store<SC1>(mx[hh], states, base + 512 * 4);
+                    state_store<SC1>(den[hh], states, base + 513 * 4);
+                }
             }
         }
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
@@ -1995,8 +2007,10 @@ c8_rows(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base, con
         // fold_row covers eight heads with 512 threads: heads 0-3, then 4-7
         // (one copy of its code: the loop is kept).
 #pragma nounroll
-        for (int half = 0; half < 2; ++half)
-            fold_row<SC1>(states, folded, tid + ROWS_THREADS * half, out_row, lse_row, ANYH ? hlive : HEADS);
+        for (int half = 0; half < 2; ++half) {
+            if (local) fold_row<SC0>(states, folded, tid + ROWS_THREADS * half, out_row, lse_row, ANYH ? hlive : HEADS);
+            else fold_row<SC1>(states, folded, tid + ROWS_THREADS * half, out_row, lse_row, ANYH ? hlive : HEADS);
+        }
     };
 
     // Capacity plan: rows first_row, first_row + G, ...  Re-planned: the live
@@ -2893,7 +2907,7 @@ void launch_variant(hipStream_t stream, const SharedKVArgs *a, const SharedKVDeb
                                  : streamed    ? &c8_rows<4, true, ANYH>
                                                : &c8_rows<4, false, ANYH>;
         hipLaunchKernelGGL(rows_kernel, dim3(g2), dim3(ROWS_THREADS), 0, stream, a->cuQ, a->seqLens, a->q, a->indices,
-                           a->batch, a->topk, rows, g2, a->heads, *a, fused & FUSED_MERGE);
+                           a->batch, a->topk, rows, g2, a->heads, *a, fused);
         return;
     }
     decltype(&c8_attention<1, false, false, ANYH, false, false>) kernel =
