@@ -121,6 +121,19 @@ def test_launchers_reject_bad_blocks_without_a_device():
     assert lib.sharedkv_c8_set_merge_mode(2) == 1
     assert lib.sharedkv_c8_set_merge_mode(1) == 0
     assert lib.sharedkv_c8_set_merge_mode(0) == 0
+    # The grouped entries (both tile sizes) check the block the same way.
+    for name in ("launch_sharedkv_c8_dense_paired", "launch_sharedkv_c8_dense_packed",
+                 "launch_sharedkv_c8_dense_paired_narrow", "launch_sharedkv_c8_dense_packed_narrow"):
+        fn = getattr(lib, name)
+        assert fn(0, None, ctypes.byref(args)) == 0, name
+        assert fn(1, None, None) == 1, name
+        assert fn(1, None, ctypes.byref(args)) == 1, name   # null pointers rejected
+    # The XCD-local exchange switch takes 0 or 1; no probe runs without a launch.
+    assert lib.sharedkv_c8_set_xcd_local(2) == 1
+    assert lib.sharedkv_c8_set_xcd_local(0) == 0
+    assert lib.sharedkv_c8_set_xcd_local(1) == 0
+    if not torch.cuda.is_available():
+        assert lib.sharedkv_c8_xcd_local() == -1
 
 
 @pytest.mark.skipif(torch.cuda.is_available(), reason="placeholder addresses: host-side check only")
