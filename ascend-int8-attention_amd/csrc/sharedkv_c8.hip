@@ -379,34 +379,56 @@ __device__ __forceinline__ void fold_states(const __amdgpu_buffer_rsrc_t states,
     if (lse_row && (tid & 63) == 0) lse_row[h] = top + logf(dsum);
 }
 
-// The same fold for more than eight partitions, in the same order, with the
-// loads of each partition issued inside the loop: holding sixteen
-// partitions' values at once would spill registers in the attention kernel.
+// The same fold for more than eight partitions, in the same order: every
+// partition maximum is loaded at once (MAX_SPLITS of them, clamped as
+// above), then the partitions' sums and accumulators eight at a time, each
+// group's loads issued before any is used.  Holding sixteen partitions'
+// accumulators at once would spill registers in the attention kernel; a
+// loop over the partitions one by one would wait on every load.
 template <int POLICY>
 __device__ __forceinline__ void fold_states_wide(const __amdgpu_buffer_rsrc_t states, int S, int tid,
                                                  uint16_t *out_row, float *lse_row, int heads)
 {
+    constexpr int CHUNK = 8;
+    static_assert(MAX_SPLITS % CHUNK == 0, "whole groups of partitions");
     const int h = tid >> 6, col = (tid & 63) * 8;
     const int head_base = h * PART_FLOATS * 4;
     const int part_step = HEADS * PART_FLOATS * 4;
-    float top = state_load<POLICY>(states, head_base + 512 * 4);
-    for (int sp = 1; sp < S; ++sp) top = fmaxf(top, state_load<POLICY>(states, head_base + sp * part_step + 512 * 4));
+    float ms[MAX_SPLITS];
+#pragma unroll
+    for (int sp = 0; sp < (int)MAX_SPLITS; ++sp)
+        ms[sp] = state_load<POLICY>(states, head_base + (sp < S ? sp : 0) * part_step + 512 * 4);
+    float top = ms[0];
+#pragma unroll
+    for (int sp = 1; sp < (int)MAX_SPLITS; ++sp) top = sp < S ? fmaxf(top, ms[sp]) : top;
     float dsum = 0.0f;
     float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-    for (int sp = 0; sp < S; ++sp) {
-        const int at = head_base + sp * part_step;
-        const float f = sk_expf_nonpos(state_load<POLICY>(states, at + 512 * 4) - top);
-        dsum = dsum + state_load<POLICY>(states, at + 513 * 4) * f;
-        const f32x4 v0 = state_load4<POLICY>(states, at + col * 4);
-        const f32x4 v1 = state_load4<POLICY>(states, at + (col + 4) * 4);
-        acc[0] = acc[0] + v0.x * f;
-        acc[1] = acc[1] + v0.y * f;
-        acc[2] = acc[2] + v0.z * f;
-        acc[3] = acc[3] + v0.w * f;
-        acc[4] = acc[4] + v1.x * f;
-        acc[5] = acc[5] + v1.y * f;
-        acc[6] = acc[6] + v1.z * f;
-        acc[7] = acc[7] + v1.w * f;
+#pragma unroll
+    for (int c = 0; c < (int)MAX_SPLITS; c += CHUNK) {
+        if (c >= S) break;
+        float ds[CHUNK];
+        f32x4 v0[CHUNK], v1[CHUNK];
+#pragma unroll
+        for (int k = 0; k < CHUNK; ++k) {
+            const int at = head_base + (c + k < S ? c + k : 0) * part_step;
+            ds[k] = state_load<POLICY>(states, at + 513 * 4);
+            v0[k] = state_load4<POLICY>(states, at + col * 4);
+            v1[k] = state_load4<POLICY>(states, at + (col + 4) * 4);
+        }
+#pragma unroll
+        for (int k = 0; k < CHUNK; ++k)
+            if (c + k < S) {
+                const float f = sk_expf_nonpos(ms[c + k] - top);
+                dsum = dsum + ds[k] * f;
+                acc[0] = acc[0] + v0[k].x * f;
+                acc[1] = acc[1] + v0[k].y * f;
+                acc[2] = acc[2] + v0[k].z * f;
+                acc[3] = acc[3] + v0[k].w * f;
+                acc[4] = acc[4] + v1[k].x * f;
+                acc[5] = acc[5] + v1[k].y * f;
+                acc[6] = acc[6] + v1[k].z * f;
+                acc[7] = acc[7] + v1[k].w * f;
+            }
     }
     uint32_t w[4];
 #pragma unroll
