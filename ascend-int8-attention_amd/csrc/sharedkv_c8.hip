@@ -59,9 +59,11 @@ constexpr int HEADS = 8;               // heads per work-group (one MFMA row blo
 constexpr int MAX_HEADS = 128;
 constexpr int N = SHAREDKV_C8_TILE;    // keys per tile
 // Partition plan of a launch's live rows (the host's choose_splits rule):
-// PLAN_FEW partitions while rows x PLAN_FEW work-groups fit the PLAN_CUS
-// compute units, else PLAN_MANY.
-constexpr int32_t PLAN_CUS = 256, PLAN_FEW = 5, PLAN_MANY = 3;
+// one partition per tile of the longest row while rows x tiles stay within
+// PLAN_ONE_TILE work items and the launch's work items allow it (a row then
+// waits for one tile and the merge); else PLAN_FEW partitions while rows x PLAN_FEW work-groups fit the
+// PLAN_CUS compute units, else PLAN_MANY.
+constexpr int32_t PLAN_CUS = 256, PLAN_FEW = 5, PLAN_MANY = 3, PLAN_ONE_TILE = 112;
 constexpr int THREADS = 512;           // 8 waves: two per SIMD
 constexpr int WAVES = THREADS / 64;
 constexpr int PROW = N + 16;           // LDS row stride of the P codes
@@ -623,6 +625,7 @@ c8_attention(const uint64_t cu_q, const uint64_t seq_lens, const uint64_t q_base
         int32_t plan = live_rows * PLAN_FEW <= PLAN_CUS ? PLAN_FEW : PLAN_MANY;
         const int32_t fit = PLAN_CUS / live_rows > 1 ? PLAN_CUS / live_rows : 1;
         const int32_t room = (int32_t)(items / (uint32_t)live_rows);
+        if (live_rows * tiles <= PLAN_ONE_TILE && tiles <= (int32_t)MAX_SPLITS && tiles <= room) plan = tiles;
         plan = plan < fit ? plan : fit;
         plan = plan < tiles ? plan : tiles;
         plan = plan < room ? plan : room;
@@ -1501,10 +1504,12 @@ c8_merge(const SharedKVArgs p, uint32_t splits)
 // r, r + grid, ... in turn.
 // When graph padding leaves fewer live rows than the launch's capacity and
 // the launch may merge (`fused`: partition states and tickets supplied), the
-// live rows are re-planned as c8_attention re-plans them (the same rule, so
-// the same partitions and numerics): each work item is a (row, partition)
-// pair, every XCD takes a contiguous eighth of the live rows, and the last
-// partition of a row folds the states.  A row's tiles are a chain (QK -> tile
+// live rows are re-planned with c8_attention's PLAN_FEW / PLAN_MANY rule
+// (not its one-tile plan for few rows: each partition here repeats the
+// row's set-up on four waves, and one-tile partitions measured slower):
+// each work item is a (row, partition) pair, every XCD takes a contiguous
+// eighth of the live rows, and the last partition of a row folds the
+// states.  A row's tiles are a chain (QK -> tile
 // maximum -> exponentials and P codes -> PV) through work-group barriers;
 // with one row per CU nothing fills those waits, with two rows per CU the
 // other work-group computes while this one waits for its barrier or its next

@@ -45,6 +45,7 @@ MAX_TOPK = 1024
 SMALL_TOKENS = 24          # C4 launches of fewer tokens go through the small-launch entry
 SPLITS_FEW_ROWS = 5        # when rows x 5 work-groups fit one wave on the CUs
 SPLITS_MANY_ROWS = 3
+ONE_TILE_ITEMS = 112       # one partition per tile while rows x tiles stay within this
 PARTIAL_FLOATS = 520       # per (token, partition, head): 512 numerator, max, denominator, pad
 
 VARIANT_SPARSE, VARIANT_DENSE, VARIANT_SPARSE_SMALL = 20, 21, 22
@@ -84,13 +85,21 @@ def max_tiles(ratio, topk, max_seq_len=None, ori_topk=0):
     return window_tiles
 
 
-def plan_splits(rows, tiles):
+def plan_splits(rows, tiles, one_tile=True, room=None):
     """Partitions for `rows` query rows of at most `tiles` tiles each.
 
-    Five partitions while rows x 5 work-groups fit one wave on the CUs (a
-    row's nine tiles then take at most two per partition), else three; on
-    MI355X this is the fastest of 2..6 at 1, 32 and 64 rows.  The kernel
-    applies the same rule to the live rows of a padded launch."""
+    One partition per tile while rows x tiles <= ONE_TILE_ITEMS, tiles <=
+    MAX_SPLITS and tiles <= `room` (the work items a padded launch has per
+    live row), if `one_tile`: every partition then waits for one tile before
+    the merge (on MI355X 1-12 C4 rows of nine tiles take 0.1-0.8 us less
+    than at five partitions, 14 and 16 rows more; eight partitions, where
+    one holds two tiles, were slower than five).  Else five partitions while rows x 5
+    work-groups fit one wave on the CUs (a row's nine tiles then take at
+    most two per partition), else three; the fastest of 2..8 at 32 and 64
+    rows.  The kernel applies the same rule to the live rows of a padded
+    launch (c8_rows without the one-tile plan)."""
+    if one_tile and rows * tiles <= ONE_TILE_ITEMS and tiles <= MAX_SPLITS and (room is None or tiles <= room):
+        return max(1, tiles)
     wanted = SPLITS_FEW_ROWS if rows * SPLITS_FEW_ROWS <= CORES else SPLITS_MANY_ROWS
     wanted = min(wanted, max(1, CORES // rows))
     return max(1, min(wanted, tiles, MAX_SPLITS))
@@ -115,7 +124,7 @@ def choose_paired_splits(tokens, ratio, max_seq_len=None):
         tiles = MAX_SPLITS if max_seq_len is None else 2 + (max(0, int(max_seq_len)) // 4 + TILE - 1) // TILE
     else:
         tiles = max_tiles(ratio, 0, max_seq_len) + 1
-    return plan_splits((tokens + 1) // 2, tiles)
+    return plan_splits((tokens + 1) // 2, tiles, one_tile=False)
 
 
 def live_shape(cu_q, seq_lens, tokens):
@@ -163,10 +172,11 @@ def device_splits(splits, tokens, heads, ratio, topk, cu_q, seq_lens, ori_topk=0
     `splits`.  Only launches that merge in themselves re-plan (`fused`: the
     library's merge mode 0, with several partitions or with one partition
     and the re-plan's partition states supplied, which prepare() always
-    does); one-partition C4 launches of more rows than CUs (c8_rows) apply
-    the same rule with their rows as the work-groups.  The kernel's numerics
-    follow this count (tile k folds into partition k % count), so checkers
-    use it in place of `splits`.
+    does); one-partition C4 and window-only launches of more rows than CUs
+    (rows_launch: c8_rows) apply the same rule with their rows as the
+    work-groups, without the one-tile plan.  The kernel's numerics follow
+    this count (tile k folds into partition k % count), so checkers use it
+    in place of `splits`.
 
     Joint-plan launches (joint_launch; `cmp_rows` = the compressed block
     table's rows per sequence, width x 32) run as one partition per row
@@ -184,7 +194,23 @@ def device_splits(splits, tokens, heads, ratio, topk, cu_q, seq_lens, ori_topk=0
         tiles += (min(longest // 4, topk) + TILE - 1) // TILE
     elif ratio == 128:
         tiles += (longest // 128 + TILE - 1) // TILE
-    return max(splits, min(plan_splits(live_rows, tiles), rows * splits // live_rows))
+    one_tile = not rows_launch(splits, tokens, heads, ratio, ori_topk, cmp_rows, small)
+    room = rows * splits // live_rows
+    return max(splits, min(plan_splits(live_rows, tiles, one_tile, room), room))
+
+
+def rows_launch(splits, tokens, heads, ratio, ori_topk=0, cmp_rows=None, small=None):
+    """Whether the kernel runs a launch on c8_rows (two four-wave work-groups
+    per CU taking rows in turn): one partition, more rows than CUs, no
+    explicit original slots, and window-only or C4 without joint rows
+    compiled in (C4 kernels carry them for launches through the small-launch
+    entry and for compressed block tables of at most one tile of rows per
+    sequence)."""
+    if small is None:
+        small = tokens < SMALL_TOKENS
+    joint4 = heads <= HEADS and (small or (cmp_rows is not None and cmp_rows <= TILE))
+    return (splits == 1 and not ori_topk and tokens * head_groups(heads) > CORES
+            and (ratio == 1 or (ratio == 4 and not joint4)))
 
 
 def joint_launch(splits, tokens, heads, ratio, cu_q, seq_lens, ori_topk=0, fused=True, cmp_rows=None, small=None):

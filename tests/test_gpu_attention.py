@@ -650,9 +650,9 @@ def _padded_rows_case(heads=8, mode=0):
     assert (op.out[live:].float().cpu() == 0).all() and (op.lse[live:].cpu() == 0).all()
     # Fused launches hand the padding rows' work-groups to the live rows.
     splits = op.device_splits(merge_mode=mode)
-    # 3 (or 6) live rows of at most 1 + ceil(750 / 128) = 7 tiles: 5
-    # partitions, as an eager launch of those rows would choose.
-    assert splits == (4 if mode else 5), splits
+    # 3 (or 6) live rows of at most 1 + ceil(750 / 128) = 7 tiles: one
+    # partition per tile, as an eager launch of those rows would choose.
+    assert splits == (4 if mode else 7), splits
     compare(case, bits_of(op.out)[:live], op.lse.cpu().numpy()[:live], splits, tag="padding")
 
 
@@ -774,7 +774,7 @@ def test_graph_at_capacity_replayed_at_fewer_live_sequences(cap):
         cu = np.array(list(range(live + 1)) + [live] * (cap - live), np.int32)
         lens = np.array(lengths[:live] + [0] * (cap - live), np.int32)
         plan = c8_attention.device_splits(op.splits, cap, 8, 4, 1024, cu, lens)
-        assert plan == {64: {64: 3, 8: 5, 16: 5, 32: 5}, 160: {64: 2, 8: 5, 16: 5, 32: 5}}[cap][live], plan
+        assert plan == {64: {64: 3, 8: 7, 16: 7, 32: 5}, 160: {64: 2, 8: 7, 16: 7, 32: 5}}[cap][live], plan
         dev.cu_q.copy_(torch.from_numpy(cu))
         dev.seq_lens.copy_(torch.from_numpy(lens))
         op.out.fill_(float("nan"))

@@ -179,11 +179,16 @@ def test_host_plan():
     assert c8_attention.choose_splits(64, 4, 1024) == 3
     assert c8_attention.choose_splits(32, 4, 1024) == 5       # 160 work-groups: one wave
     assert c8_attention.choose_splits(51, 4, 1024) == 5 and c8_attention.choose_splits(52, 4, 1024) == 3
-    assert c8_attention.choose_splits(1, 4, 1024) == 5
+    # Up to 112 work items: one partition per tile (12 C4 rows of 9 tiles).
+    assert c8_attention.choose_splits(1, 4, 1024) == 9
+    assert c8_attention.choose_splits(12, 4, 1024) == 9 and c8_attention.choose_splits(13, 4, 1024) == 5
+    assert c8_attention.choose_splits(16, 128, 0, 20000) == 3       # 1 + 2 tiles
+    assert c8_attention.plan_splits(2, 9, one_tile=False) == 5
+    assert c8_attention.plan_splits(8, 9, room=8) == 5                # no room for 9
     assert c8_attention.choose_splits(100, 4, 1024) == 2       # one wave of work-groups
     assert c8_attention.choose_splits(4096, 4, 1024) == 1
     assert c8_attention.choose_splits(1, 128, 0, 4096) == 2
-    assert c8_attention.choose_splits(2, 128, 0) == 5
+    assert c8_attention.choose_splits(2, 128, 0) == 16       # tile count unknown: its bound
     assert c8_attention.choose_splits(1, 1, 0) == 1
 
 
@@ -196,7 +201,7 @@ def test_device_plan_of_padded_launches():
     plan = c8_attention.device_splits
     cap = 64
     assert c8_attention.choose_splits(cap, 4, 1024) == 3
-    for live, want, one in ((8, 5, 5), (16, 5, 4), (32, 5, 2), (51, 3, 1), (64, 3, 1)):
+    for live, want, one in ((8, 9, 5), (16, 5, 4), (32, 5, 2), (51, 3, 1), (64, 3, 1)):
         cu = list(range(live + 1)) + [cap] * (cap - live)
         lens = [20000] * live + [0] * (cap - live)
         assert plan(3, cap, 8, 4, 1024, cu, lens) == want, live
@@ -221,8 +226,10 @@ def test_device_plan_of_padded_launches():
     assert plan(2, 64, 8, 128, 0, [0, 1, 64], [20000, 0]) == 3      # 1 + ceil(156 / 128) tiles
     assert plan(2, 64, 8, 1, 0, [0, 1, 64], [4096, 0]) == 2
     assert plan(2, 64, 8, 1, 0, [0, 1, 64], [4096, 0], ori_topk=384) == 3
-    # Head groups count as rows: 16 heads, 4 live tokens of 32 -> 8 rows.
-    assert plan(3, 32, 16, 4, 1024, [0, 4, 32], [30000, 0]) == 5
+    # Head groups count as rows: 16 heads, 4 live tokens of 32 -> 8 rows of
+    # 9 tiles, one partition per tile; 8 live tokens -> 16 rows, 5.
+    assert plan(3, 32, 16, 4, 1024, [0, 4, 32], [30000, 0]) == 9
+    assert plan(3, 32, 16, 4, 1024, [0, 8, 32], [30000, 0]) == 5
     # The live shape: a cu_q sentinel (-1) or seq_len 0 ends the live batch.
     assert c8_attention.live_shape([0, 2, 4, -1], [5000, 2600, 9000], 6) == (4, 5000)
     assert c8_attention.live_shape([0, 2, 4, 6], [5000, 0, 0], 6) == (2, 5000)
@@ -274,10 +281,11 @@ def test_device_plan_constants_match_the_host_rule():
     """The kernel's re-plan uses the host's partition rule: its constants
     (csrc/sharedkv_c8.hip) equal c8_attention's."""
     src = (ROOT / "ascend-int8-attention_amd" / "csrc" / "sharedkv_c8.hip").read_text()
-    found = re.search(r"constexpr int32_t PLAN_CUS = (\d+), PLAN_FEW = (\d+), PLAN_MANY = (\d+);", src)
+    found = re.search(r"constexpr int32_t PLAN_CUS = (\d+), PLAN_FEW = (\d+), PLAN_MANY = (\d+), "
+                      r"PLAN_ONE_TILE = (\d+);", src)
     assert found, "plan constants not found in the kernel source"
     assert tuple(int(x) for x in found.groups()) == (c8_attention.CORES, c8_attention.SPLITS_FEW_ROWS,
-                                                      c8_attention.SPLITS_MANY_ROWS)
+                                                      c8_attention.SPLITS_MANY_ROWS, c8_attention.ONE_TILE_ITEMS)
     assert re.search(r"constexpr uint32_t MAX_SPLITS = (\d+);", src).group(1) == str(c8_attention.MAX_SPLITS)
 
 
