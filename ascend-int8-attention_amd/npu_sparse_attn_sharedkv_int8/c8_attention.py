@@ -117,14 +117,16 @@ def choose_paired_splits(tokens, ratio, max_seq_len=None):
     of its work-groups (one per pair of tokens, at most ceil(tokens / 2) of
     them), whose window list can take a second tile (up to 129 or 131
     rows).  A C4 group lists every compressed row below its last position
-    / 4 (max_seq_len // 4 rows at most)."""
+    / 4 (max_seq_len // 4 rows at most).  Few work-groups with a known tile
+    count take one partition per tile, as ungrouped launches do (config 2's
+    C128 launch at G2: 17.4 us at 5 partitions, 14.7 at one per tile)."""
     if tokens <= 0:
         return 1
     if ratio == 4:
-        tiles = MAX_SPLITS if max_seq_len is None else 2 + (max(0, int(max_seq_len)) // 4 + TILE - 1) // TILE
+        tiles = MAX_SPLITS + 1 if max_seq_len is None else 2 + (max(0, int(max_seq_len)) // 4 + TILE - 1) // TILE
     else:
         tiles = max_tiles(ratio, 0, max_seq_len) + 1
-    return plan_splits((tokens + 1) // 2, tiles, one_tile=False)
+    return plan_splits((tokens + 1) // 2, tiles)
 
 
 def live_shape(cu_q, seq_lens, tokens):

@@ -61,13 +61,13 @@ def bits_of(tensor):
     return tensor.detach().cpu().view(torch.int16).numpy().view(np.uint16)
 
 
-def run_hip(case, splits=None, return_lse=True, device="cuda", query_group=None, tile_size=None):
+def run_hip(case, splits=None, return_lse=True, device="cuda", query_group=None, tile_size=None, max_seq_len=None):
     """One PreparedAttention launch; returns (out bits, lse, prepared)."""
     import torch
     from npu_sparse_attn_sharedkv_int8 import PreparedAttention
     dev, ori_scale, cmp_scale, keep = to_device(case, device)
     op = PreparedAttention(dev, ori_scale, cmp_scale, splits=splits, return_lse=return_lse, query_group=query_group,
-                           tile_size=tile_size)
+                           tile_size=tile_size, max_seq_len=max_seq_len)
     op._keep = keep
     op.run()
     torch.cuda.synchronize()

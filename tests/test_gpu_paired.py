@@ -31,8 +31,8 @@ def say(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def check(case, splits, tag, group=2, tile=None):
-    out, lse, op = run_hip(case, splits=splits, query_group=group, tile_size=tile)
+def check(case, splits, tag, group=2, tile=None, max_seq_len=None):
+    out, lse, op = run_hip(case, splits=splits, query_group=group, tile_size=tile, max_seq_len=max_seq_len)
     assert op.query_group == group and op.device_splits() == op.splits and op.tile_size == (tile or 256)
     ref, ref_lse, _ = run_oracle(case, op.splits, query_group=group, tile=op.tile_size)
     live = int(case["cu_q"][-1])
@@ -97,6 +97,22 @@ def test_grouped_plan_heads_and_default_partitions(group, tile):
         case = workloads.make_case(106, 128, [4] * 8, [2000 + 997 * i for i in range(8)], heads=heads)
         out, op = check(case, None, f"G{group} tile {tile} {heads} heads", group, tile)
         assert op.splits == (1 if tile == 256 else c8_attention.choose_paired_splits(32, 128))
+
+
+@pytest.mark.parametrize("group", [2, 4])
+def test_grouped_plan_one_partition_per_tile(group):
+    """128-key grouped plans at one partition per tile: the library's choice
+    for few work-groups with a known tile count (max_seq_len 66000: a
+    window list of up to two tiles and five compressed tiles, 7 partitions
+    for 6 work-groups of pairs), and 9 and 12 partitions (the fold above
+    eight partitions, in groups of eight)."""
+    from npu_sparse_attn_sharedkv_int8 import c8_attention
+    case = workloads.make_case(119, 128, [2, 4, 2, 3], [66000, 41000, 20000, 9000])
+    _, op = check(case, None, f"G{group} one tile per partition", group, 128, max_seq_len=66000)
+    assert op.splits == c8_attention.choose_paired_splits(11, 128, 66000) == 7
+    for splits in (9, 12):
+        say(f"[grouped G{group}] tile 128 splits {splits}")
+        check(case, splits, f"G{group} tile 128 splits {splits}", group, 128)
 
 
 def test_packed_prefill_chunk():

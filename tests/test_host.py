@@ -189,6 +189,11 @@ def test_host_plan():
     assert c8_attention.choose_splits(4096, 4, 1024) == 1
     assert c8_attention.choose_splits(1, 128, 0, 4096) == 2
     assert c8_attention.choose_splits(2, 128, 0) == 16       # tile count unknown: its bound
+    # Grouped 128-key plans: one partition per tile for few work-groups of a
+    # known tile count (16 pairs x 6 tiles at 64 K), else five.
+    assert c8_attention.choose_paired_splits(32, 128, 65536) == 6
+    assert c8_attention.choose_paired_splits(32, 128) == 5 and c8_attention.choose_paired_splits(64, 128, 65536) == 5
+    assert c8_attention.choose_paired_splits(32, 4) == 5 and c8_attention.choose_paired_splits(32, 4, 1024) == 4
     assert c8_attention.choose_splits(1, 1, 0) == 1
 
 
