@@ -4,8 +4,8 @@ prefill-like chunks of 260-400 tokens (c8_rows: work-groups taking rows in
 turn), graph-capacity padding rows (a few, or enough that the device
 re-plans the live rows, c8_rows capacities included), compressed block
 tables as wide as a serving table, the grouped plans (query_group 2 and
-4, 128- and 256-key tiles), KV partitions (1-8) and both merge placements,
-all bit-exact (BF16 outputs) with the checker on the launch's own plan and
+4, 128- and 256-key tiles), KV partitions (1-16, the host plan included)
+and both merge placements, all bit-exact (BF16 outputs) with the checker on the launch's own plan and
 LSE within 2e-6."""
 import os
 import sys
@@ -45,7 +45,7 @@ def random_case(seed):
     mode = str(rng.choice(["uniform", "holes", "dups", "mixed"] + list(workloads.EDGE_MODES)))
     slots = rng.random() < 0.25 and not prefill      # a draft's slots cover at most 384 rows
     slot_mode = str(rng.choice(["draft", "shuffled", "pool"])) if slots else None
-    splits = rng.choice([None, 1, 2, 3, 4, 5, 6, 8])
+    splits = rng.choice([None, 1, 2, 3, 4, 5, 6, 8, 9, 12, 16])
     if prefill and rng.random() < 0.6:
         splits = None                                 # the host plan: one partition
     merge = int(rng.integers(0, 2))
