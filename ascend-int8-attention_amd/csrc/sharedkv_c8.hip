@@ -332,8 +332,9 @@ __device__ __forceinline__ f32x4 state_load4(__amdgpu_buffer_rsrc_t r, int offse
 // group.  Partitions are folded in order.  MAXS bounds S at compile time so
 // every load is issued before any is used (offsets of partitions past S are
 // clamped to partition 0 and their values ignored); fold_row instantiates it
-// exactly for the partition counts the host plan picks (up to 6), since every
-// clamped partition still costs its loads and its exponential.
+// exactly for 2-6 partitions (the five-or-three plan and short rows), since
+// every clamped partition still costs its loads and its exponential, for 7-8
+// at once, and above eight in groups (fold_states_wide).
 template <int MAXS, int POLICY>
 __device__ __forceinline__ void fold_states(const __amdgpu_buffer_rsrc_t states, int S, int tid,
                                             uint16_t *out_row, float *lse_row, int heads)
