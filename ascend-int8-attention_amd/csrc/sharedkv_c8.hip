@@ -61,8 +61,8 @@ constexpr int N = SHAREDKV_C8_TILE;    // keys per tile
 // Partition plan of a launch's live rows (the host's choose_splits rule):
 // one partition per tile of the longest row while rows x tiles stay within
 // PLAN_ONE_TILE work items and the launch's work items allow it (a row then
-// waits for one tile and the merge); else PLAN_FEW partitions while rows x PLAN_FEW work-groups fit the
-// PLAN_CUS compute units, else PLAN_MANY.
+// waits for one tile and the merge); else PLAN_FEW partitions while rows x
+// PLAN_FEW work-groups fit the PLAN_CUS compute units, else PLAN_MANY.
 constexpr int32_t PLAN_CUS = 256, PLAN_FEW = 5, PLAN_MANY = 3, PLAN_ONE_TILE = 112;
 constexpr int THREADS = 512;           // 8 waves: two per SIMD
 constexpr int WAVES = THREADS / 64;
@@ -1510,11 +1510,10 @@ c8_merge(const SharedKVArgs p, uint32_t splits)
 // row's set-up on four waves, and one-tile partitions measured slower):
 // each work item is a (row, partition) pair, every XCD takes a contiguous
 // eighth of the live rows, and the last partition of a row folds the
-// states.  A row's tiles are a chain (QK -> tile
-// maximum -> exponentials and P codes -> PV) through work-group barriers;
-// with one row per CU nothing fills those waits, with two rows per CU the
-// other work-group computes while this one waits for its barrier or its next
-// tile.  Each wave takes 32 keys in QK (two 16-key blocks) and 128 output
+// states.  A row's tiles are a chain (QK -> tile maximum -> exponentials and
+// P codes -> PV) through work-group barriers; with one row per CU nothing
+// fills those waits, with two rows per CU the other work-group computes
+// while this one waits for its barrier or its next tile.  Each wave takes 32 keys in QK (two 16-key blocks) and 128 output
 // columns in PV.
 // RATIO 4: the window tile and up to eight compressed tiles, every row's HBM
 // address resident in LDS.  RATIO 1: the window tile alone.  (C128 launches
