@@ -285,6 +285,30 @@ def test_integer_oracle_close_to_fp64_attention(ratio):
     np.testing.assert_allclose(lse, ref_lse, rtol=2e-4, atol=2e-4)
 
 
+@pytest.mark.parametrize("ratio", [4, 128])
+def test_many_partition_folds_close_to_fp64_attention(ratio):
+    """The fold over 5-16 KV partitions (the one-partition-per-tile plans and
+    the fold above eight partitions): rel-L2 < 0.01 and LSE within 2e-4 of
+    FP64 attention at every partition count, as at one; and partitions that
+    own no tile change nothing (rows of at most nine tiles give the same
+    bits at 9, 12 and 16 partitions)."""
+    lengths = [129, 9000, 70000] if ratio == 4 else [20000, 70000, 131072]
+    case = workloads.make_case(41, ratio, [1, 2, 1], lengths)
+    c = workloads.oracle_case(case)
+    ref, ref_lse = ora.fp64_attention(c)
+    outs = {}
+    for splits in (5, 8, 9, 12, 16):
+        out, lse, _ = ora.tiled_attention(c, splits=splits)
+        got = ora.bf16_to_f32(out).astype(np.float64)
+        assert np.linalg.norm(got - ref) / np.linalg.norm(ref) < 0.01, splits
+        np.testing.assert_allclose(lse, ref_lse, rtol=2e-4, atol=2e-4, err_msg=f"S={splits}")
+        outs[splits] = (out, lse)
+    for splits in (12, 16):
+        np.testing.assert_array_equal(outs[splits][0], outs[9][0])
+        np.testing.assert_array_equal(outs[splits][1], outs[9][1])
+    assert not np.array_equal(outs[5][0], outs[9][0])     # the partition count is part of the numerics
+
+
 @pytest.mark.parametrize("mode", workloads.EDGE_MODES)
 def test_edge_selections_close_to_fp64_attention(mode):
     """The reference's sparse-edge selections (tests/npu/test_sparse_edges.py
