@@ -1113,6 +1113,29 @@ def test_splits_variants_match_checker():
         compare(case, out, lse, splits, tag=f"splits {splits}")
 
 
+@pytest.mark.parametrize("name,ratio,queries,lengths,heads,want", [
+    ("c4_one_row", 4, [1], [16384], 8, 9),                     # config 1's shape
+    ("c4_seven_tiles", 4, [2, 2], [3000, 2900], 8, 9),          # two partitions own no tile
+    ("c4_twelve_heads", 4, [2, 1], [30000, 9000], 12, 9),       # 3 tokens x 2 head groups
+    ("c128_unknown_length", 128, [2], [131072], 8, 16),          # nine tiles; the bound is 16
+    ("c4_twelve_rows", 4, [2] * 6, [4000 + 5000 * i for i in range(6)], 8, 9),
+    ("c4_thirteen_rows", 4, [1] * 13, [4000 + 3000 * i for i in range(13)], 8, 5),
+])
+def test_one_partition_per_tile_plans(name, ratio, queries, lengths, heads, want):
+    """The library's plan for launches of at most 112 row tiles: one KV
+    partition per tile (nine for C4 top-k rows; sixteen, the bound, for C128
+    rows whose length the launch was not told), the fold above eight
+    partitions; thirteen rows of nine tiles take five.
+    Bit-exact with the checker on that plan."""
+    from npu_sparse_attn_sharedkv_int8 import c8_attention
+    case = workloads.make_case(77, ratio, queries, lengths, heads=heads)
+    say(f"[one tile] {name}")
+    out, lse, op = run_hip(case)
+    assert op.splits == want, (name, op.splits)
+    assert effective_splits(case, op.splits) == want
+    compare(case, out, lse, op.splits, tag=name)
+
+
 def test_long_c128_rows_span_two_code_chunks():
     """C128 rows longer than twelve tiles per partition (ctx 300000: 2343
     compressed rows, 20 tiles) rebuild their row codes in a second chunk."""
